@@ -1,0 +1,306 @@
+"""Benchmark of the xtile_amd HIP path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c5]
+
+One step = one launch of the tile program over one batch of synthetic input
+(numpy PCG64, seed = config index, shapes of BASELINE.json's configs).  The
+headline line is C2 (row softmax fp32 8192x4096);
+all five configurations are measured and reported under "per_config".
+
+Timing: W untimed warm-up launches, then K launches captured in a HIP graph and
+replayed once between two HIP events on the replay stream, with device
+synchronisation on both sides; per-step time = elapsed / K.  Every step reads
+a different input set (buffer rotation over >= 1 GiB) so inputs are not left
+resident in the 256 MB Infinity Cache between steps.  Inputs are in HBM before
+the timed region starts; no host transfer is timed.
+
+roofline.achieved = algorithmic bytes (or FLOPs) of one launch / per-step
+time; roofline.traffic = measured HBM bytes per launch from the rocprofv3
+FETCH_SIZE / WRITE_SIZE summaries under profiles/ (null when absent).
+
+cpu_baseline = the oracle (oracle/xt_oracle.c, the loop-lowered C executor of
+the same xt program) timed on this host's cores over whole repetitions of the
+same workload for about --cpu-seconds.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "GB/s (add, softmax) & TFLOP/s (matmul, conv2d) on 1 MI355X, % of roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0}
+ROTATE_BYTES = 1 << 30
+
+
+def _f32(a):
+    return np.asarray(a, dtype=np.float32)
+
+
+def make_config(name: str):
+    """(module, host inputs, dtypes, out index, meta) for one configuration."""
+    from oracle import f32_to_bf16_bits
+    from xtile_amd import kernels as K
+
+    if name == "c1":
+        rng = np.random.default_rng(1)
+        a = _f32(rng.uniform(-1, 1, (1024, 1024)))
+        b = _f32(rng.uniform(-1, 1, (1024, 1024)))
+        return K.CONFIGS["c1_add"](), [a, b, np.zeros_like(a)], ["f32"] * 3, {
+            "workload": "c1_add: C = A + B fp32 1024x1024, 32x64 tiles, grid (32,16,1)",
+            "unit": "GB/s",
+            "bound": "hbm",
+            "dtype": "f32",
+            "data": "synthetic: numpy PCG64 seed=1, uniform[-1,1]",
+        }
+    if name == "c2":
+        rng = np.random.default_rng(2)
+        x = _f32(rng.normal(0.0, 2.0, (8192, 4096)))
+        return K.CONFIGS["c2_softmax"](), [x, np.zeros_like(x)], ["f32"] * 2, {
+            "workload": "c2_softmax: row softmax fp32 8192x4096, one 1x4096 row per Block, grid (8192,1,1)",
+            "unit": "GB/s",
+            "bound": "hbm",
+            "dtype": "f32",
+            "data": "synthetic: numpy PCG64 seed=2, normal(0,2)",
+        }
+    if name == "c3":
+        rng = np.random.default_rng(3)
+        a = rng.uniform(-1, 1, (4096, 4096)).astype(np.float16)
+        b = rng.uniform(-1, 1, (4096, 4096)).astype(np.float16)
+        return K.CONFIGS["c3_matmul_f16"](), [a, b, np.zeros((4096, 4096), np.float32)], [
+            "f16",
+            "f16",
+            "f32",
+        ], {
+            "workload": "c3_matmul_f16: C = A @ B, M=N=K=4096, f16 in, f32 acc/out, 128x128 Block tiles, B shared=1, grid (32,32,1)",
+            "unit": "TFLOP/s",
+            "bound": "mfma",
+            "dtype": "f16",
+            "data": "synthetic: numpy PCG64 seed=3, uniform[-1,1] -> f16",
+        }
+    if name == "c4":
+        rng = np.random.default_rng(4)
+        x = rng.normal(0, 0.1, (32, 56, 56, 64)).astype(np.float16)
+        f = rng.normal(0, 0.1, (3, 3, 64, 64)).astype(np.float16)
+        return K.CONFIGS["c4_conv2d_f16"](), [x, f, np.zeros((32, 56, 56, 64), np.float32)], [
+            "f16",
+            "f16",
+            "f32",
+        ], {
+            "workload": "c4_conv2d_f16: NHWC 32x56x56x64 * 3x3x64x64, stride 1, pad 1, f16 in, f32 out, 1x4x56x64 Block tiles, filter shared=2, grid (32,14,1)",
+            "unit": "TFLOP/s",
+            "bound": "hbm",
+            "dtype": "f16",
+            "data": "synthetic: numpy PCG64 seed=4, normal(0,0.1) -> f16",
+        }
+    if name == "c5":
+        rng = np.random.default_rng(5)
+        a = f32_to_bf16_bits(_f32(rng.normal(0, 0.02, (4096, 4096))))
+        b = f32_to_bf16_bits(_f32(rng.normal(0, 0.02, (4096, 11008))))
+        return K.CONFIGS["c5_matmul_bf16"](), [a, b, np.zeros((4096, 11008), np.float32)], [
+            "bf16",
+            "bf16",
+            "f32",
+        ], {
+            "workload": "c5_matmul_bf16: C = A @ B, M=4096 N=11008 K=4096, bf16 in (RNE), f32 out, 256x128 Block tiles, A shared=1, grid (86,16,1)",
+            "unit": "TFLOP/s",
+            "bound": "mfma",
+            "dtype": "bf16",
+            "data": "synthetic: numpy PCG64 seed=5, normal(0,0.02) -> bf16 (RNE)",
+        }
+    raise ValueError(f"unknown config {name}")
+
+
+def _traffic(name: str):
+    """HBM bytes per launch from profiles/traffic_<config>.txt (fetch + write)."""
+    path = ROOT / "profiles" / f"traffic_{name}.txt"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        m = re.match(r"\s*(fetch_bytes|write_bytes)\s*[:=]\s*([0-9.eE+]+)", line)
+        if m:
+            vals[m.group(1)] = float(m.group(2))
+    if "fetch_bytes" in vals and "write_bytes" in vals:
+        return vals["fetch_bytes"] + vals["write_bytes"]
+    return None
+
+
+def gpu_time(module, host, dtypes, steps: int, warmup: int, use_graph: bool):
+    """Average ms per launch over `steps` launches, rotating input sets."""
+    import torch
+
+    import xtile_amd as xt
+    from tests.gpu_util import to_device
+
+    dev = torch.device("cuda:0")
+    set_bytes = sum(h.nbytes for h in host)
+    nsets = max(1, min(16, math.ceil(ROTATE_BYTES / set_bytes)))
+    first = [to_device(h, d, dev) for h, d in zip(host, dtypes)]
+    sets = [first] + [[t.clone() for t in first] for _ in range(nsets - 1)]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            xt.launch(module, *sets[i % nsets])
+    torch.cuda.synchronize()
+    mode = "eager"
+    graph = None
+    if use_graph:
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(steps):
+                    xt.launch(module, *sets[i % nsets])
+            graph.replay()
+            torch.cuda.synchronize()
+            mode = "hip_graph"
+        except Exception as exc:  # capture unsupported: fall back to eager launches
+            print(f"[bench] graph capture failed ({exc}); timing eager launches", file=sys.stderr)
+            graph = None
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(steps):
+                xt.launch(module, *sets[i % nsets])
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    out = sets[0]
+    return ms, mode, nsets, out
+
+
+def cpu_time(module, host, seconds: float):
+    """Rate of the oracle over whole repetitions of the workload."""
+    import oracle
+
+    threads = int(os.environ.get("XT_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    text = str(module)
+    bufs = [np.array(h, copy=True) for h in host]
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.run(text, bufs, threads)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    return elapsed / reps, reps, threads
+
+
+def measure(name: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool) -> dict:
+    import xtile_amd as xt
+
+    module, host, dtypes, meta = make_config(name)
+    plan = xt.plan(module)
+    print(f"[bench] {name}: {plan['kernel']}", file=sys.stderr, flush=True)
+    ms, mode, nsets, _ = gpu_time(module, host, dtypes, steps, warmup, use_graph)
+    sec = ms * 1e-3
+    if meta["unit"] == "GB/s":
+        value = plan["bytes"] / sec / 1e9
+    else:
+        value = plan["flops"] / sec / 1e12
+    if meta["bound"] == "hbm":
+        achieved = plan["bytes"] / sec / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic(name)}
+    else:
+        achieved = plan["flops"] / sec / 1e12
+        peak = MFMA_PEAK_TFLOPS[meta["dtype"]]
+        roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": _traffic(name)}
+    if name == "c4":  # report against the MFMA peak as well
+        tf = plan["flops"] / sec / 1e12
+        roof["mfma_tflops"] = tf
+        roof["mfma_frac"] = tf / MFMA_PEAK_TFLOPS["f16"]
+    result = {
+        "config": name,
+        "workload": meta["workload"],
+        "kernel": plan["kernel"],
+        "value": value,
+        "unit": meta["unit"],
+        "ms_per_step": ms,
+        "dtype": meta["dtype"],
+        "data": meta["data"],
+        "timing": f"{mode}, {steps} launches, {nsets} rotating input sets",
+        "roofline": roof,
+        "algo_bytes": plan["bytes"],
+        "algo_flops": plan["flops"],
+    }
+    if cpu_seconds > 0:
+        cpu_s, reps, threads = cpu_time(module, host, cpu_seconds)
+        cpu_value = (plan["bytes"] / cpu_s / 1e9) if meta["unit"] == "GB/s" else (
+            plan["flops"] / cpu_s / 1e12)
+        result["cpu_baseline"] = {
+            "value": cpu_value,
+            "unit": meta["unit"],
+            "cores": threads,
+            "kind": "port",
+            "sample": f"oracle/xt_oracle.c over the full workload, {reps} repetition(s), "
+                      f"{cpu_s * 1e3:.1f} ms each, {threads} OpenMP threads (nproc={os.cpu_count()})",
+        }
+    return result
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="all", help="all, or one of c1..c5")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            "bench.py measures one MI355X: the xtile tile programs run on a single GPU "
+            "(multi-GPU sharding is a design note, not built); use --gpus 1",
+            file=sys.stderr,
+        )
+        return 2
+    names = ["c1", "c2", "c3", "c4", "c5"] if args.config == "all" else [args.config]
+    headline = "c2" if "c2" in names else names[0]
+    results = {n: measure(n, args.steps, args.warmup, args.cpu_seconds, not args.no_graph) for n in names}
+    h = results[headline]
+    line = {
+        "metric": METRIC,
+        "value": h["value"],
+        "unit": h["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": h["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": h["dtype"],
+        "data": h["data"],
+        "config": {"workload": h["workload"], "kernel": h["kernel"], "timing": h["timing"]},
+        "roofline": h["roofline"],
+        "cpu_baseline": h.get("cpu_baseline"),
+        "per_config": [results[n] for n in names],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,142 @@
+"""GPU parity: every HIP kernel against the oracle on the same seeded inputs.
+
+Bars: bit-exact for f32 add; max relative error <= 1e-5
+for f32 softmax; Frobenius relative error <= 1e-3 for f16/bf16 matmul and conv.
+Inputs follow the benchmark recipe: numpy PCG64, seed = config index.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import xtile_amd as xt
+from oracle import bf16_bits_to_f32, closed_form as cf, f32_to_bf16_bits
+from tests.conftest import oracle_threads
+from tests.gpu_util import frob_rel, run_gpu, run_oracle
+from xtile_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+SOFTMAX_RTOL = 1e-5
+MM_FROB = 1e-3
+
+
+# -- add (C1) ------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "rows,cols,th,tw",
+    [(1024, 1024, 32, 64), (64, 128, 32, 64), (96, 40, 32, 8), (33, 7, 11, 7), (1, 4, 1, 4)],
+)
+def test_add_bit_exact(cuda, rows, cols, th, tw):
+    rng = np.random.default_rng(1)
+    m = K.add(rows, cols, th, tw)
+    a = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    b = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    c = np.zeros_like(a)
+    got = run_gpu(m, [a, b, c], ["f32"] * 3, cuda, case=f"add {rows}x{cols} tile {th}x{tw}")[2]
+    want = run_oracle(m, [a, b, c], oracle_threads())[2]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(want, a + b)
+
+
+def test_add_rows_reference_program(cuda):
+    """kernels/add.py form: 64-row full-width tiles, grid (rows/64, 1, 1)."""
+    rng = np.random.default_rng(1)
+    m = K.add_rows(256, 384, 64)
+    a = rng.uniform(-1, 1, (256, 384)).astype(np.float32)
+    b = rng.uniform(-1, 1, (256, 384)).astype(np.float32)
+    got = run_gpu(m, [a, b, np.zeros_like(a)], ["f32"] * 3, cuda, case="add_rows")[2]
+    assert np.array_equal(got, a + b)
+
+
+@pytest.mark.parametrize("op", ["sub", "mul"])
+def test_sub_mul_bit_exact(cuda, op):
+    text = f"""
+func.func @k(%a: memref<64x96xf32>, %b: memref<64x96xf32>, %c: memref<64x96xf32>) attributes {{xt.grid = array<i32: 2, 3, 1>}} {{
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %0 = xt.load(%a, %bid#0, %bid#1) : (memref<64x96xf32>, i32, i32) -> tensor<32x32xf32>
+  %1 = xt.load(%b, %bid#0, %bid#1) : (memref<64x96xf32>, i32, i32) -> tensor<32x32xf32>
+  %2 = xt.{op}(%0, %1) : tensor<32x32xf32>, tensor<32x32xf32> -> tensor<32x32xf32>
+  xt.store(%2, %c, %bid#0, %bid#1) : (tensor<32x32xf32>, memref<64x96xf32>, i32, i32) -> ()
+  func.return
+}}"""
+    m = xt.parse(text)
+    rng = np.random.default_rng(7)
+    a = rng.normal(size=(64, 96)).astype(np.float32)
+    b = rng.normal(size=(64, 96)).astype(np.float32)
+    got = run_gpu(m, [a, b, np.zeros_like(a)], ["f32"] * 3, cuda, case=op)[2]
+    want = run_oracle(m, [a, b, np.zeros_like(a)], 2)[2]
+    assert np.array_equal(got, want)
+
+
+# -- softmax (C2) ----------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "rows,cols,trow",
+    [(8192, 4096, 1), (128, 64, 64), (64, 4096, 2), (16, 1000, 4), (24, 8192, 1), (5, 3, 5)],
+)
+def test_softmax(cuda, rows, cols, trow):
+    rng = np.random.default_rng(2)
+    m = K.softmax(rows, cols, trow)
+    x = rng.normal(0.0, 2.0, (rows, cols)).astype(np.float32)
+    got = run_gpu(m, [x, np.zeros_like(x)], ["f32"] * 2, cuda, case=f"softmax {rows}x{cols}/{trow}")[1]
+    want = run_oracle(m, [x, np.zeros_like(x)], oracle_threads())[1]
+    rel = np.max(np.abs(got - want) / np.abs(want))
+    assert rel <= SOFTMAX_RTOL
+    np.testing.assert_allclose(got.sum(axis=1), 1.0, rtol=0, atol=1e-5)
+
+
+# -- matmul (C3, C5) --------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "m_,n_,k_,tm,tn",
+    [(4096, 4096, 4096, 128, 128), (256, 384, 192, 128, 128), (128, 192, 64, 64, 64), (512, 256, 512, 256, 128)],
+)
+def test_matmul_f16(cuda, m_, n_, k_, tm, tn):
+    rng = np.random.default_rng(3)
+    mod = K.matmul_f16(m_, n_, k_, tm, tn)
+    a = rng.uniform(-1, 1, (m_, k_)).astype(np.float16)
+    b = rng.uniform(-1, 1, (k_, n_)).astype(np.float16)
+    c = np.zeros((m_, n_), np.float32)
+    got = run_gpu(mod, [a, b, c], ["f16", "f16", "f32"], cuda, case=f"mm f16 {m_}x{n_}x{k_}")[2]
+    want = run_oracle(mod, [a, b, c], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+    assert frob_rel(want, cf.matmul(a, b)) <= 1e-6
+
+
+@pytest.mark.parametrize(
+    "m_,n_,k_,tm,tn", [(4096, 11008, 4096, 256, 128), (512, 640, 256, 256, 128), (256, 128, 128, 128, 64)]
+)
+def test_matmul_bf16(cuda, m_, n_, k_, tm, tn):
+    rng = np.random.default_rng(5)
+    mod = K.matmul_bf16(m_, n_, k_, tm, tn)
+    a = f32_to_bf16_bits(rng.normal(0, 0.02, (m_, k_)).astype(np.float32))
+    b = f32_to_bf16_bits(rng.normal(0, 0.02, (k_, n_)).astype(np.float32))
+    c = np.zeros((m_, n_), np.float32)
+    got = run_gpu(mod, [a, b, c], ["bf16", "bf16", "f32"], cuda, case=f"mm bf16 {m_}x{n_}x{k_}")[2]
+    ref = cf.matmul(bf16_bits_to_f32(a), bf16_bits_to_f32(b)) if m_ * n_ * k_ > 2**33 else None
+    if ref is None:
+        ref = run_oracle(mod, [a, b, c], oracle_threads())[2]
+    assert frob_rel(got, ref) <= MM_FROB
+
+
+# -- conv2d (C4) -------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,th,tw",
+    [(32, 56, 56, 64, 64, 4, 56), (2, 8, 16, 32, 16, 4, 8), (1, 7, 7, 64, 32, 7, 7), (3, 12, 20, 32, 128, 2, 10), (2, 6, 10, 96, 16, 3, 5)],
+)
+def test_conv2d_f16(cuda, n, h, w, cin, cout, th, tw):
+    rng = np.random.default_rng(4)
+    mod = K.conv2d(n, h, w, cin, cout, 3, 3, th, tw)
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float16)
+    f = rng.normal(0, 0.1, (3, 3, cin, cout)).astype(np.float16)
+    o = np.zeros((n, h, w, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], ["f16", "f16", "f32"], cuda, case=f"conv {n}x{h}x{w}x{cin}->{cout}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB

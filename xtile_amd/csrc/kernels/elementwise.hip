@@ -1,0 +1,260 @@
+// Bandwidth-bound tile programs: elementwise binary ops and row softmax.
+//
+// One xt Block is one workgroup of 256 threads (4 wave64s).  Tiles are read
+// and written with 128-bit global accesses whenever every row start is
+// 16-byte aligned; consecutive lanes touch consecutive 16-byte chunks so each
+// wave instruction covers whole 64-byte segments.
+//
+// Semantics follow the reference DSL: add/sub/mul are plain IEEE f32 ops
+// (xtile/dsl.py:321-325,351-352); softmax is x - max(x), exp, sum, then
+// multiply by reciprocal(sum) exactly as `x / r` is traced
+// (xtile/dsl.py:354-357, kernels/softmax.py:13-18).
+#include "common.h"
+#include "launch.h"
+
+namespace xtk {
+namespace {
+
+struct EwArgs {
+  const float* a;
+  const float* b;
+  float* c;
+  TileOff ta, tb, tc;
+  long long lda, ldb, ldc;
+  int rows, cols;
+  int gx, gy;
+};
+
+template <int OP>
+__device__ __forceinline__ float ew_apply(float x, float y) {
+  if constexpr (OP == 0) return x + y;
+  else if constexpr (OP == 1) return x - y;
+  else return x * y;
+}
+
+template <int OP, int VW>
+__global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
+  int x, y, z;
+  decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  const float* A = p.a + p.ta.at(x, y, z);
+  const float* B = p.b + p.tb.at(x, y, z);
+  float* C = p.c + p.tc.at(x, y, z);
+  const int cv = p.cols / VW;
+  const int n = p.rows * cv;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int r = i / cv;
+    const int col = (i - r * cv) * VW;
+    if constexpr (VW == 4) {
+      float4v va = *reinterpret_cast<const float4v*>(A + r * p.lda + col);
+      float4v vb = *reinterpret_cast<const float4v*>(B + r * p.ldb + col);
+      float4v vc;
+      vc.x = ew_apply<OP>(va.x, vb.x);
+      vc.y = ew_apply<OP>(va.y, vb.y);
+      vc.z = ew_apply<OP>(va.z, vb.z);
+      vc.w = ew_apply<OP>(va.w, vb.w);
+      *reinterpret_cast<float4v*>(C + r * p.ldc + col) = vc;
+    } else {
+      C[r * p.ldc + col] = ew_apply<OP>(A[r * p.lda + col], B[r * p.ldb + col]);
+    }
+  }
+}
+
+struct SoftmaxArgs {
+  const float* x;
+  float* y;
+  TileOff tx, ty;
+  long long ldx, ldy;
+  int rows, cols;
+  int gx, gy;
+  int tpr;  // threads per row (power of two, <= 256)
+};
+
+// Row reduction across the `tpr` threads that share a row.  For tpr <= 64 the
+// group lies inside one wave and a butterfly suffices; wider rows combine the
+// per-wave partials through LDS.
+template <bool IS_MAX>
+__device__ __forceinline__ float row_reduce(float v, int tpr, float* lds) {
+  const int w = min(tpr, 64);
+  v = IS_MAX ? wave_max(v, w) : wave_sum(v, w);
+  if (tpr <= 64) return v;
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds[wave] = v;
+  __syncthreads();
+  const int per_row = tpr >> 6;
+  const int first = (wave / per_row) * per_row;
+  float r = lds[first];
+  for (int k = 1; k < per_row; ++k) r = IS_MAX ? fmaxf(r, lds[first + k]) : r + lds[first + k];
+  __syncthreads();
+  return r;
+}
+
+template <int NV, int VW>
+__global__ __launch_bounds__(256) void row_softmax_kernel(SoftmaxArgs p) {
+  __shared__ float lds[4];
+  int x, y, z;
+  decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  const float* X = p.x + p.tx.at(x, y, z);
+  float* Y = p.y + p.ty.at(x, y, z);
+  const int tpr = p.tpr;
+  const int rpp = 256 / tpr;
+  const int lane = threadIdx.x & (tpr - 1);
+  const int row_in_pass = threadIdx.x / tpr;
+  const int passes = (p.rows + rpp - 1) / rpp;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int r = pass * rpp + row_in_pass;
+    const bool live = r < p.rows;
+    const float* xr = X + (long long)r * p.ldx;
+    float* yr = Y + (long long)r * p.ldy;
+    float v[NV][VW];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int col = (lane + j * tpr) * VW;
+      if (live && col < p.cols) {
+        if constexpr (VW == 4) {
+          float4v t = *reinterpret_cast<const float4v*>(xr + col);
+          v[j][0] = t.x;
+          v[j][1] = t.y;
+          v[j][2] = t.z;
+          v[j][3] = t.w;
+        } else {
+          v[j][0] = xr[col];
+        }
+#pragma unroll
+        for (int k = 0; k < VW; ++k) m = fmaxf(m, v[j][k]);
+      }
+    }
+    m = row_reduce<true>(m, tpr, lds);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int col = (lane + j * tpr) * VW;
+      if (live && col < p.cols) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          v[j][k] = expf(v[j][k] - m);
+          s += v[j][k];
+        }
+      }
+    }
+    s = row_reduce<false>(s, tpr, lds);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int col = (lane + j * tpr) * VW;
+      if (live && col < p.cols) {
+        if constexpr (VW == 4) {
+          float4v t;
+          t.x = v[j][0] * inv;
+          t.y = v[j][1] * inv;
+          t.z = v[j][2] * inv;
+          t.w = v[j][3] * inv;
+          *reinterpret_cast<float4v*>(yr + col) = t;
+        } else {
+          yr[col] = v[j][0] * inv;
+        }
+      }
+    }
+  }
+}
+
+TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
+
+bool aligned4(const xt::Access2D& a, const void* base) {
+  return (reinterpret_cast<uintptr_t>(base) % 16) == 0 && a.ld % 4 == 0 && a.cols % 4 == 0 &&
+         a.addr.c0 % 4 == 0 && a.addr.sx % 4 == 0 && a.addr.sy % 4 == 0 && a.addr.sz % 4 == 0;
+}
+
+int num_blocks(const xt::Plan& p) { return p.grid[0] * p.grid[1] * p.grid[2]; }
+
+}  // namespace
+
+hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why) {
+  EwArgs a;
+  a.a = static_cast<const float*>(bufs[p.a.arg]);
+  a.b = static_cast<const float*>(bufs[p.b.arg]);
+  a.c = static_cast<float*>(bufs[p.c.arg]);
+  a.ta = to_off(p.a.addr);
+  a.tb = to_off(p.b.addr);
+  a.tc = to_off(p.c.addr);
+  a.lda = p.a.ld;
+  a.ldb = p.b.ld;
+  a.ldc = p.c.ld;
+  a.rows = static_cast<int>(p.c.rows);
+  a.cols = static_cast<int>(p.c.cols);
+  a.gx = p.grid[0];
+  a.gy = p.grid[1];
+  if (p.a.rows != p.c.rows || p.b.rows != p.c.rows || p.a.cols != p.c.cols ||
+      p.b.cols != p.c.cols) {
+    why = "elementwise operand tiles differ in shape";
+    return hipErrorInvalidValue;
+  }
+  bool vec = aligned4(p.a, a.a) && aligned4(p.b, a.b) && aligned4(p.c, a.c);
+  dim3 grid(num_blocks(p)), block(256);
+  int op = static_cast<int>(p.ew_op);
+#define XT_EW(OPV, VWV) hipLaunchKernelGGL((ew_binary_kernel<OPV, VWV>), grid, block, 0, s, a)
+  if (vec) {
+    if (op == 0) XT_EW(0, 4);
+    else if (op == 1) XT_EW(1, 4);
+    else XT_EW(2, 4);
+  } else {
+    if (op == 0) XT_EW(0, 1);
+    else if (op == 1) XT_EW(1, 1);
+    else XT_EW(2, 1);
+  }
+#undef XT_EW
+  return hipGetLastError();
+}
+
+hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t s,
+                              std::string& why) {
+  SoftmaxArgs a;
+  a.x = static_cast<const float*>(bufs[p.a.arg]);
+  a.y = static_cast<float*>(bufs[p.c.arg]);
+  a.tx = to_off(p.a.addr);
+  a.ty = to_off(p.c.addr);
+  a.ldx = p.a.ld;
+  a.ldy = p.c.ld;
+  a.rows = static_cast<int>(p.a.rows);
+  a.cols = static_cast<int>(p.a.cols);
+  a.gx = p.grid[0];
+  a.gy = p.grid[1];
+  if (p.c.rows != p.a.rows || p.c.cols != p.a.cols) {
+    why = "softmax input and output tiles differ in shape";
+    return hipErrorInvalidValue;
+  }
+  const int vw = (aligned4(p.a, a.x) && aligned4(p.c, a.y)) ? 4 : 1;
+  // smallest NV in {1,2,4,8} with NV * VW * 256 >= cols, then the narrowest
+  // power-of-two thread group that covers the row
+  int nv = 1;
+  while (nv < 8 && nv * vw * 256 < a.cols) nv *= 2;
+  if (nv * vw * 256 < a.cols) {
+    why = "softmax row too long for the register-resident kernel";
+    return hipErrorInvalidValue;
+  }
+  int need = (a.cols + nv * vw - 1) / (nv * vw);
+  int tpr = 1;
+  while (tpr < need) tpr *= 2;
+  a.tpr = tpr;
+  dim3 grid(num_blocks(p)), block(256);
+#define XT_SM(NVV, VWV) hipLaunchKernelGGL((row_softmax_kernel<NVV, VWV>), grid, block, 0, s, a)
+  if (vw == 4) {
+    switch (nv) {
+      case 1: XT_SM(1, 4); break;
+      case 2: XT_SM(2, 4); break;
+      case 4: XT_SM(4, 4); break;
+      default: XT_SM(8, 4); break;
+    }
+  } else {
+    switch (nv) {
+      case 1: XT_SM(1, 1); break;
+      case 2: XT_SM(2, 1); break;
+      case 4: XT_SM(4, 1); break;
+      default: XT_SM(8, 1); break;
+    }
+  }
+#undef XT_SM
+  return hipGetLastError();
+}
+
+}  // namespace xtk

@@ -1,0 +1,21 @@
+// Host-side launchers of the gfx950 kernels.  Each validates what its kernel
+// assumes about the plan and the buffers (alignment, LDS budget) and returns
+// hipErrorInvalidValue with `why` set instead of launching when it does not
+// hold.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../plan.h"
+
+namespace xtk {
+
+hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
+hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t s,
+                              std::string& why);
+hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
+hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
+
+}  // namespace xtk

@@ -1,0 +1,541 @@
+// Tile-program matcher.  See plan.h for the addressing model.
+//
+// Recognised programs (each maps onto one hand-written gfx950 kernel family):
+//   EwBinary   store(op(load A, load B))             op in {add, sub, mul}, f32
+//              (kernels/add.py:6-13; xtile/dsl.py:321-325,351-352)
+//   RowSoftmax load -> reduce_max -> sub -> exp -> reduce_sum -> reciprocal
+//              -> mul -> store, reductions over axis 1
+//              (kernels/softmax.py:10-19; test/python/dsl_convert.py:25-40)
+//   Gemm       store(matmul(load A, load B))         f16/bf16 in, f32 out
+//              (kernels/matmul.py:6-16 without its epilogue)
+//   Conv2d     store(load_conv2d(S, load F))         f16/bf16 in, f32 out
+//              (kernels/conv2d.py:10-37; conv slice math lib/xt/XTToNova.cpp:110-142)
+#include "plan.h"
+
+#include <map>
+#include <sstream>
+
+namespace xt {
+namespace {
+
+struct Analysis {
+  const Func& f;
+  const int32_t* grid;
+  std::map<int, Coord> coords;          // i32 value -> block id axis / constant
+  std::vector<const Op*> compute;       // everything except bid / constants / return
+  std::vector<int> uses;
+  std::map<int, const Op*> def;
+
+  Analysis(const Func& fn, const int32_t* g) : f(fn), grid(g), uses(fn.values.size(), 0) {
+    for (auto& o : f.blocks[0].ops) {
+      for (int v : o.operands) uses[v]++;
+      for (int r : o.results) def[r] = &o;
+      if (o.name == "xt.get_tile_block_id") {
+        for (int k = 0; k < 3; ++k) coords[o.results[k]] = Coord{k, 0};
+      } else if (o.name == "arith.constant") {
+        const Attr* v = find_attr(o.attrs, "value");
+        if (v && v->kind == Attr::Int) coords[o.results[0]] = Coord{-1, v->i};
+      } else if (o.name != "func.return") {
+        compute.push_back(&o);
+      }
+    }
+  }
+
+  int arg_index(int value) const {
+    for (size_t k = 0; k < f.args.size(); ++k)
+      if (f.args[k] == value) return static_cast<int>(k);
+    return -1;
+  }
+};
+
+bool coord_of(const Analysis& an, int v, int shared, Coord& out, std::string& err) {
+  auto it = an.coords.find(v);
+  if (it == an.coords.end()) {
+    err = "tile coordinates must be xt.get_tile_block_id results or integer constants";
+    return false;
+  }
+  out = it->second;
+  if (out.axis >= 0 && out.axis < shared) out = Coord{-1, 0};  // sharing-group leader
+  return true;
+}
+
+// Element strides of a row-major memref.
+std::vector<int64_t> strides_of(const std::vector<int64_t>& shape) {
+  std::vector<int64_t> s(shape.size(), 1);
+  for (int d = static_cast<int>(shape.size()) - 2; d >= 0; --d) s[d] = s[d + 1] * shape[d + 1];
+  return s;
+}
+
+// Shared by loads and stores: coordinates -> affine tile origin, bounds check.
+bool tile_origin(const Analysis& an, const std::vector<int>& coord_values, int shared,
+                 const std::vector<int64_t>& tile, const std::vector<int64_t>& mem,
+                 const std::string& what, TileAddr& addr, std::vector<Coord>* coords_out,
+                 std::string& err) {
+  std::vector<int64_t> st = strides_of(mem);
+  addr = TileAddr{};
+  for (size_t d = 0; d < tile.size(); ++d) {
+    Coord c;
+    if (!coord_of(an, coord_values[d], shared, c, err)) return false;
+    if (coords_out) coords_out->push_back(c);
+    int64_t lo = c.axis < 0 ? c.value : 0;
+    int64_t hi = c.axis < 0 ? c.value : an.grid[c.axis] - 1;
+    if (lo < 0 || (hi + 1) * tile[d] > mem[d]) {
+      std::ostringstream os;
+      os << what << ": tile coordinate range [" << lo << ", " << hi << "] x " << tile[d]
+         << " exceeds extent " << mem[d] << " of dim " << d;
+      err = os.str();
+      return false;
+    }
+    int64_t step = tile[d] * st[d];
+    if (c.axis < 0) addr.c0 += c.value * step;
+    else if (c.axis == 0) addr.sx += step;
+    else if (c.axis == 1) addr.sy += step;
+    else addr.sz += step;
+  }
+  return true;
+}
+
+// View a tile of `tile` within memref `mem` as rows x cols with row pitch ld.
+bool as_2d(const std::vector<int64_t>& tile, const std::vector<int64_t>& mem, Access2D& a,
+           bool merge_rows, std::string& err) {
+  int r = static_cast<int>(tile.size());
+  std::vector<int64_t> st = strides_of(mem);
+  if (!merge_rows) {
+    // keep the tile's own rows: rank 1 is one row, rank 2 is rows x cols
+    if (r > 2) {
+      err = "tile must be rank 1 or 2";
+      return false;
+    }
+    a.rows = r == 1 ? 1 : tile[0];
+    a.cols = tile[r - 1];
+    a.ld = mem[r - 1];
+    return true;
+  }
+  int64_t cols = tile[r - 1];
+  int d = r - 2;
+  for (; d >= 0; --d) {
+    if (tile[d + 1] != mem[d + 1]) break;
+    cols *= tile[d];
+  }
+  // dims 0..d remain: at most one of them may have extent > 1
+  int64_t rows = 1, ld = cols;
+  int outer = -1;
+  for (int k = 0; k <= d; ++k)
+    if (tile[k] > 1) {
+      if (outer >= 0) {
+        err = "tile is not a 2-D strided block of its memref";
+        return false;
+      }
+      outer = k;
+    }
+  if (outer >= 0) {
+    rows = tile[outer];
+    ld = st[outer];
+    // the run below `outer` must be contiguous: cols == product of inner tile dims
+    int64_t inner = 1;
+    for (int k = outer + 1; k < r; ++k) inner *= tile[k];
+    if (inner != cols) {
+      err = "tile is not a 2-D strided block of its memref";
+      return false;
+    }
+  }
+  a.rows = rows;
+  a.cols = cols;
+  a.ld = ld;
+  return true;
+}
+
+// merge_rows: elementwise programs may treat full-width rows as one long row.
+bool access_of(const Analysis& an, const Op& o, Access2D& a, std::string& err,
+               bool merge_rows = false) {
+  bool is_load = o.name == "xt.load";
+  int mem_v = is_load ? o.operands[0] : o.operands[1];
+  const Type& mem = an.f.type_of(mem_v);
+  const Type& ten = is_load ? an.f.type_of(o.results[0]) : an.f.type_of(o.operands[0]);
+  a.arg = an.arg_index(mem_v);
+  if (a.arg < 0) {
+    err = o.name + " must access a function argument";
+    return false;
+  }
+  a.elem = mem.elem;
+  a.shared = 0;
+  if (is_load)
+    if (const Attr* sh = find_attr(o.attrs, "shared")) a.shared = static_cast<int>(sh->i);
+  std::vector<int> cv(o.operands.begin() + (is_load ? 1 : 2), o.operands.end());
+  std::string what = o.name + " of argument #" + std::to_string(a.arg);
+  if (!tile_origin(an, cv, a.shared, ten.shape, mem.shape, what, a.addr, nullptr, err))
+    return false;
+  return as_2d(ten.shape, mem.shape, a, merge_rows, err);
+}
+
+const Op* only(const Analysis& an, const char* name, int& count) {
+  const Op* found = nullptr;
+  count = 0;
+  for (const Op* o : an.compute)
+    if (o->name == name) {
+      found = o;
+      ++count;
+    }
+  return found;
+}
+
+int count_ops(const Analysis& an) { return static_cast<int>(an.compute.size()); }
+
+const Op* def_of(const Analysis& an, int v) {
+  auto it = an.def.find(v);
+  return it == an.def.end() ? nullptr : it->second;
+}
+
+// -- EwBinary ----------------------------------------------------------------
+
+bool match_ew(const Analysis& an, Plan& p, std::string& err) {
+  int nstore = 0;
+  const Op* st = only(an, "xt.store", nstore);
+  if (nstore != 1 || !st) return false;
+  const Op* bin = def_of(an, st->operands[0]);
+  if (!bin || (bin->name != "xt.add" && bin->name != "xt.sub" && bin->name != "xt.mul"))
+    return false;
+  const Op* la = def_of(an, bin->operands[0]);
+  const Op* lb = def_of(an, bin->operands[1]);
+  if (!la || !lb || la->name != "xt.load" || lb->name != "xt.load") return false;
+  int expected = la == lb ? 3 : 4;
+  if (count_ops(an) != expected) return false;
+  const Type& ta = an.f.type_of(la->results[0]);
+  const Type& tb = an.f.type_of(lb->results[0]);
+  if (ta != tb) {
+    err = "elementwise programs with broadcast operands are not supported by the HIP backend yet";
+    return false;
+  }
+  if (ta.elem != Elem::F32) {
+    err = "elementwise programs currently require f32 tiles";
+    return false;
+  }
+  if (!access_of(an, *la, p.a, err, true) || !access_of(an, *lb, p.b, err, true) ||
+      !access_of(an, *st, p.c, err, true))
+    return false;
+  auto same_view = [&]() {
+    return p.a.rows == p.c.rows && p.a.cols == p.c.cols && p.b.rows == p.c.rows &&
+           p.b.cols == p.c.cols;
+  };
+  if (!same_view()) {
+    // the three memrefs disagree on which rows are full-width: keep tile rows
+    if (ta.rank() > 2) {
+      err = "elementwise tiles of rank > 2 must be contiguous runs in every operand";
+      return false;
+    }
+    if (!access_of(an, *la, p.a, err) || !access_of(an, *lb, p.b, err) ||
+        !access_of(an, *st, p.c, err))
+      return false;
+  }
+  p.kind = PlanKind::EwBinary;
+  p.ew_op = bin->name == "xt.add" ? EwOp::Add : bin->name == "xt.sub" ? EwOp::Sub : EwOp::Mul;
+  double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
+  double tile_bytes = double(ta.numel()) * 4;
+  p.algo_bytes = blocks * tile_bytes * (la == lb ? 2 : 3);
+  return true;
+}
+
+// -- RowSoftmax ----------------------------------------------------------------
+
+bool axis_is(const Op* o, int64_t axis) {
+  const Attr* a = find_attr(o->attrs, "axis");
+  return a && (a->i == axis || a->i == axis - 2);
+}
+
+bool match_softmax(const Analysis& an, Plan& p, std::string& err) {
+  if (count_ops(an) != 8) return false;
+  int n;
+  const Op* st = only(an, "xt.store", n);
+  if (n != 1) return false;
+  const Op* mul = def_of(an, st->operands[0]);
+  if (!mul || mul->name != "xt.mul") return false;
+  const Op* e = def_of(an, mul->operands[0]);
+  const Op* inv = def_of(an, mul->operands[1]);
+  if (e && e->name == "xt.reciprocal") std::swap(e, inv);
+  if (!e || !inv || e->name != "xt.exp" || inv->name != "xt.reciprocal") return false;
+  const Op* rsum = def_of(an, inv->operands[0]);
+  if (!rsum || rsum->name != "xt.reduce_sum" || rsum->operands[0] != e->results[0] ||
+      !axis_is(rsum, 1))
+    return false;
+  const Op* sub = def_of(an, e->operands[0]);
+  if (!sub || sub->name != "xt.sub") return false;
+  const Op* ld = def_of(an, sub->operands[0]);
+  const Op* rmax = def_of(an, sub->operands[1]);
+  if (!ld || !rmax || ld->name != "xt.load" || rmax->name != "xt.reduce_max" ||
+      rmax->operands[0] != ld->results[0] || !axis_is(rmax, 1))
+    return false;
+  const Type& t = an.f.type_of(ld->results[0]);
+  if (t.elem != Elem::F32 || t.rank() != 2) {
+    err = "row softmax requires a rank-2 f32 tile";
+    return false;
+  }
+  if (!access_of(an, *ld, p.a, err) || !access_of(an, *st, p.c, err)) return false;
+  if (t.shape[1] > 8192) {
+    err = "row softmax supports rows of at most 8192 elements";
+    return false;
+  }
+  p.kind = PlanKind::RowSoftmax;
+  double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
+  p.algo_bytes = blocks * double(t.numel()) * 8;
+  return true;
+}
+
+// -- Gemm ----------------------------------------------------------------------
+
+bool match_gemm(const Analysis& an, Plan& p, std::string& err) {
+  int nmm, nst;
+  const Op* mm = only(an, "xt.matmul", nmm);
+  const Op* st = only(an, "xt.store", nst);
+  if (nmm != 1 || nst != 1 || count_ops(an) != 4) {
+    if (nmm >= 1)
+      err = "matmul programs must be store(matmul(load, load)); epilogues are not supported yet";
+    return false;
+  }
+  if (st->operands[0] != mm->results[0]) {
+    err = "matmul programs must store the matmul result";
+    return false;
+  }
+  const Op* la = def_of(an, mm->operands[0]);
+  const Op* lb = def_of(an, mm->operands[1]);
+  if (!la || !lb || la->name != "xt.load" || lb->name != "xt.load") {
+    err = "matmul operands must be loaded tiles";
+    return false;
+  }
+  const Type& ta = an.f.type_of(la->results[0]);
+  const Type& tb = an.f.type_of(lb->results[0]);
+  const Type& tc = an.f.type_of(mm->results[0]);
+  if (!((ta.elem == Elem::F16 || ta.elem == Elem::BF16) && tb.elem == ta.elem &&
+        tc.elem == Elem::F32)) {
+    err = "the HIP matmul kernel takes f16 x f16 or bf16 x bf16 tiles with an f32 result";
+    return false;
+  }
+  if (!access_of(an, *la, p.a, err) || !access_of(an, *lb, p.b, err) ||
+      !access_of(an, *st, p.c, err))
+    return false;
+  int64_t M = ta.shape[0], K = ta.shape[1], N = tb.shape[1];
+  if (M % 64 || N % 64 || K % 64) {
+    err = "the HIP matmul kernel needs tile M, N and K to be multiples of 64";
+    return false;
+  }
+  if (p.a.ld % 8 || p.b.ld % 8 || p.c.ld % 4) {
+    err = "the HIP matmul kernel needs 16-byte aligned rows";
+    return false;
+  }
+  p.kind = PlanKind::Gemm;
+  p.gemm_k = K;
+  double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
+  p.algo_flops = blocks * 2.0 * double(M) * double(N) * double(K);
+  // minimum HBM traffic: each argument once
+  double bytes = 0;
+  for (int arg : {p.a.arg, p.b.arg, p.c.arg}) {
+    const Type& t = an.f.type_of(an.f.args[arg]);
+    bytes += double(t.numel()) * elem_bytes(t.elem);
+  }
+  p.algo_bytes = bytes;
+  return true;
+}
+
+// -- Conv2d ----------------------------------------------------------------------
+
+bool match_conv(const Analysis& an, Plan& p, std::string& err) {
+  int nc, nst;
+  const Op* cv = only(an, "xt.load_conv2d", nc);
+  const Op* st = only(an, "xt.store", nst);
+  if (nc != 1) return false;
+  if (nst != 1 || count_ops(an) != 3 || st->operands[0] != cv->results[0]) {
+    err = "conv2d programs must be store(load_conv2d(src, load filter))";
+    return false;
+  }
+  const Op* lf = def_of(an, cv->operands[1]);
+  if (!lf || lf->name != "xt.load") {
+    err = "the load_conv2d filter must be a loaded tile";
+    return false;
+  }
+  ConvPlan& c = p.conv;
+  const Type& src = an.f.type_of(cv->operands[0]);
+  const Type& ft = an.f.type_of(lf->results[0]);
+  const Type& fm = an.f.type_of(lf->operands[0]);
+  const Type& res = an.f.type_of(cv->results[0]);
+  const Type& outm = an.f.type_of(st->operands[1]);
+  if (!((src.elem == Elem::F16 || src.elem == Elem::BF16) && res.elem == Elem::F32)) {
+    err = "the HIP conv2d kernel takes f16 or bf16 source/filter with an f32 result";
+    return false;
+  }
+  if (ft.shape != fm.shape) {
+    err = "the HIP conv2d kernel needs the filter tile to be the whole filter array";
+    return false;
+  }
+  if (const Attr* g = find_attr(cv->attrs, "group"))
+    if (g->i != 1) {
+      err = "the HIP conv2d kernel supports group = 1 only";
+      return false;
+    }
+  c.src_arg = an.arg_index(cv->operands[0]);
+  c.filt_arg = an.arg_index(lf->operands[0]);
+  c.out_arg = an.arg_index(st->operands[1]);
+  if (c.src_arg < 0 || c.filt_arg < 0 || c.out_arg < 0) {
+    err = "conv2d operands must be function arguments";
+    return false;
+  }
+  c.elem = src.elem;
+  c.N = src.shape[0];
+  c.H = src.shape[1];
+  c.W = src.shape[2];
+  c.C = src.shape[3];
+  c.KH = ft.shape[0];
+  c.KW = ft.shape[1];
+  c.CO = ft.shape[3];
+  c.TB = res.shape[0];
+  c.TH = res.shape[1];
+  c.TW = res.shape[2];
+  if (res.shape[3] != c.CO) {
+    err = "the HIP conv2d kernel needs the result tile to cover all output channels";
+    return false;
+  }
+  if (c.TB != 1) {
+    err = "the HIP conv2d kernel needs a batch tile of 1";
+    return false;
+  }
+  if (c.C % 32 || c.CO % 16 || c.CO > 256) {
+    err = "the HIP conv2d kernel needs Cin % 32 == 0 and Cout % 16 == 0 (Cout <= 256)";
+    return false;
+  }
+  const Attr* pad = find_attr(cv->attrs, "pad");
+  const Attr* stride = find_attr(cv->attrs, "stride");
+  const Attr* dil = find_attr(cv->attrs, "dilation");
+  c.pad_top = pad->ints[0];
+  c.pad_left = pad->ints[1];
+  c.stride_h = stride->ints[0];
+  c.stride_w = stride->ints[1];
+  c.dil_h = dil->ints[0];
+  c.dil_w = dil->ints[1];
+  // conv tile coordinates; the channel coordinate selects input channels
+  // [idx_c * Cin, ...) (lib/xt/XTToNova.cpp:396-401), which is in range only for 0.
+  if (!coord_of(an, cv->operands[2], 0, c.cb, err) || !coord_of(an, cv->operands[3], 0, c.ch, err) ||
+      !coord_of(an, cv->operands[4], 0, c.cw, err))
+    return false;
+  Coord cc;
+  if (!coord_of(an, cv->operands[5], 0, cc, err)) return false;
+  if (cc.axis >= 0 || cc.value != 0) {
+    err = "load_conv2d channel tile coordinate must be the constant 0";
+    return false;
+  }
+  // batch coordinate must stay inside the source
+  int64_t bhi = c.cb.axis < 0 ? c.cb.value : p.grid[c.cb.axis] - 1;
+  int64_t blo = c.cb.axis < 0 ? c.cb.value : 0;
+  if (blo < 0 || (bhi + 1) * c.TB > c.N) {
+    err = "load_conv2d batch tile coordinate exceeds the source batch";
+    return false;
+  }
+  for (const Coord* k : {&c.ch, &c.cw})
+    if (k->axis < 0 && k->value < 0) {
+      err = "load_conv2d tile coordinates must be non-negative";
+      return false;
+    }
+  // filter tile origin (shared loads take the group leader's coordinates)
+  int fshared = 0;
+  if (const Attr* sh = find_attr(lf->attrs, "shared")) fshared = static_cast<int>(sh->i);
+  std::vector<int> fcv(lf->operands.begin() + 1, lf->operands.end());
+  if (!tile_origin(an, fcv, fshared, ft.shape, fm.shape, "filter load", c.filt_addr, nullptr, err))
+    return false;
+  std::vector<int> scv(st->operands.begin() + 2, st->operands.end());
+  if (!tile_origin(an, scv, 0, res.shape, outm.shape, "conv2d store", c.out_addr, nullptr, err))
+    return false;
+  c.out_H = outm.shape[1];
+  c.out_W = outm.shape[2];
+  c.out_C = outm.shape[3];
+  if (c.out_C % 4) {
+    err = "the HIP conv2d kernel needs the output channel count to be a multiple of 4";
+    return false;
+  }
+  p.kind = PlanKind::Conv2d;
+  double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
+  double pixels = blocks * double(c.TB * c.TH * c.TW);
+  p.algo_flops = 2.0 * pixels * double(c.CO) * double(c.KH * c.KW * c.C);
+  p.algo_bytes = double(src.numel()) * elem_bytes(src.elem) +
+                 double(fm.numel()) * elem_bytes(fm.elem) + pixels * double(c.CO) * 4.0;
+  return true;
+}
+
+}  // namespace
+
+std::string Plan::describe() const {
+  std::ostringstream os;
+  auto tile = [&](const Access2D& a) {
+    std::ostringstream t;
+    t << a.rows << "x" << a.cols;
+    return t.str();
+  };
+  switch (kind) {
+    case PlanKind::EwBinary:
+      os << "ew_binary op=" << (ew_op == EwOp::Add ? "add" : ew_op == EwOp::Sub ? "sub" : "mul")
+         << " f32 tile=" << tile(c);
+      break;
+    case PlanKind::RowSoftmax:
+      os << "row_softmax f32 tile=" << tile(a);
+      break;
+    case PlanKind::Gemm:
+      os << "gemm " << elem_name(a.elem) << "->f32 tile=" << a.rows << "x" << b.cols
+         << " k=" << gemm_k;
+      break;
+    case PlanKind::Conv2d:
+      os << "conv2d_nhwc " << elem_name(conv.elem) << "->f32 tile=" << conv.TB << "x" << conv.TH
+         << "x" << conv.TW << "x" << conv.CO << " filter=" << conv.KH << "x" << conv.KW << "x"
+         << conv.C << "x" << conv.CO;
+      break;
+  }
+  os << " grid=(" << grid[0] << "," << grid[1] << "," << grid[2] << ")";
+  return os.str();
+}
+
+bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& err) {
+  const Func* f = nullptr;
+  if (func.empty()) {
+    if (m.funcs.size() != 1) {
+      err = "module has " + std::to_string(m.funcs.size()) + " functions; name one";
+      return false;
+    }
+    f = &m.funcs[0];
+  } else {
+    f = find_func(m, func);
+    if (!f) {
+      err = "no function named @" + func;
+      return false;
+    }
+  }
+  p = Plan{};
+  p.func = f->name;
+  if (!find_attr(f->attrs, "xt.grid") || !get_grid(*f, p.grid)) {
+    err = "@" + f->name + " has no xt.grid attribute";
+    return false;
+  }
+  if (!f->result_types.empty() || f->blocks.size() != 1) {
+    err = "@" + f->name + " must be a void single-block function";
+    return false;
+  }
+  for (int a : f->args) {
+    if (!f->type_of(a).is_memref()) {
+      err = "@" + f->name + " arguments must all be memrefs";
+      return false;
+    }
+    p.arg_types.push_back(f->type_of(a));
+  }
+  Analysis an(*f, p.grid);
+  for (const Op* o : an.compute)
+    if (o->name == "xt.store" && an.def.count(o->operands[0]) == 0) {
+      err = "stored values must be computed in the function";
+      return false;
+    }
+  err.clear();
+  if (match_ew(an, p, err) || !err.empty()) return err.empty();
+  if (match_softmax(an, p, err) || !err.empty()) return err.empty();
+  if (match_gemm(an, p, err) || !err.empty()) return err.empty();
+  if (match_conv(an, p, err) || !err.empty()) return err.empty();
+  std::ostringstream os;
+  os << "unsupported tile program for the HIP backend: @" << f->name << " uses";
+  for (const Op* o : an.compute) os << " " << o->name;
+  err = os.str();
+  return false;
+}
+
+}  // namespace xt

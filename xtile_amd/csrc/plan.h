@@ -1,0 +1,79 @@
+// Launch planner: recognises the tile program of an `xt` function and turns
+// it into a kernel descriptor for the HIP runtime.  Host-only (no HIP types),
+// so the matcher and its error paths are testable without a GPU.
+//
+// Tile addressing follows the reference lowering: a tile at tile coordinate c
+// of shape S starts at element offset c * S (lib/xt/XTToNova.cpp:82-101).  A
+// load with `shared = k` takes the value of the first block of its sharing
+// group, which equals evaluating its coordinates with block-id axes < k set
+// to 0 (lib/xt/XTSerialize.cpp:86-101).  Because every coordinate is either a
+// block id or a constant, the element offset of a tile origin is affine in the
+// block id: off(x, y, z) = c0 + x*sx + y*sy + z*sz.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "ir.h"
+
+namespace xt {
+
+// Element offset of a tile origin as a function of the block id.
+struct TileAddr {
+  int64_t c0 = 0, sx = 0, sy = 0, sz = 0;
+};
+
+// One tile access (load or store) against a memref argument, viewed as a
+// 2-D strided block: `rows` rows of `cols` contiguous elements, row pitch `ld`.
+struct Access2D {
+  int arg = -1;
+  Elem elem = Elem::None;
+  TileAddr addr;
+  int64_t rows = 0, cols = 0, ld = 0;
+  int shared = 0;
+};
+
+// Tile coordinate source: a block-id axis (0..2) or a constant.
+struct Coord {
+  int axis = -1;  // -1: constant
+  int64_t value = 0;
+};
+
+enum class PlanKind { EwBinary, RowSoftmax, Gemm, Conv2d };
+enum class EwOp { Add = 0, Sub = 1, Mul = 2 };
+
+struct ConvPlan {
+  int src_arg = -1, filt_arg = -1, out_arg = -1;
+  Elem elem = Elem::None;                 // source / filter element type
+  int64_t N = 0, H = 0, W = 0, C = 0;     // source memref
+  int64_t KH = 0, KW = 0, CO = 0;         // filter
+  int64_t TB = 0, TH = 0, TW = 0;         // output tile per block
+  int64_t pad_top = 0, pad_left = 0, stride_h = 1, stride_w = 1, dil_h = 1, dil_w = 1;
+  Coord cb, ch, cw;                       // conv tile coordinates (batch, row, col)
+  TileAddr filt_addr;                     // filter tile origin
+  TileAddr out_addr;                      // stored tile origin in the output
+  int64_t out_H = 0, out_W = 0, out_C = 0;  // output memref dims 1..3
+};
+
+struct Plan {
+  PlanKind kind = PlanKind::EwBinary;
+  std::string func;
+  int32_t grid[3] = {1, 1, 1};
+  std::vector<Type> arg_types;   // memref argument types, in order
+  // EwBinary: a op b -> c.   RowSoftmax: a -> c.   Gemm: a @ b -> c.
+  Access2D a, b, c;
+  EwOp ew_op = EwOp::Add;
+  int64_t gemm_k = 0;
+  ConvPlan conv;
+  double algo_bytes = 0;  // algorithmic HBM bytes per launch
+  double algo_flops = 0;  // algorithmic FLOPs per launch
+  std::string describe() const;
+};
+
+// Builds the plan of function `func` (empty name: the only function).
+// Returns false and sets `error` when the program is not one the HIP
+// backend runs.
+bool build_plan(const Module& m, const std::string& func, Plan& plan, std::string& error);
+
+}  // namespace xt

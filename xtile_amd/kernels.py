@@ -1,0 +1,188 @@
+"""Example tile programs: the reference's kernels/*.py, written with this DSL.
+
+Each builder returns a parsed Module for one configuration.  They reproduce
+the reference programs (kernels/add.py:6-30, kernels/softmax.py:10-36,
+kernels/matmul.py:6-38 without the int8 epilogue, kernels/conv2d.py:10-59) with
+the tile sizes of the five benchmark configurations:
+
+  C1 add      fp32 1024x1024, 32x64 tiles, grid (32, 16, 1)
+  C2 softmax  fp32 8192x4096, one 1x4096 row per Block, grid (8192, 1, 1)
+  C3 matmul   f16 4096^3 -> f32, 128x128 Block tiles (full K), B shared along axis 0
+  C4 conv2d   f16 NHWC 32x56x56x64, 3x3x64x64 filter, stride 1, pad 1 -> f32
+  C5 matmul   bf16 4096x11008x4096 -> f32, 256x128 tiles, grid (86, 16, 1),
+              A shared along axis 0 (`shared = 1`)
+"""
+
+from __future__ import annotations
+
+from . import (
+    Array,
+    bfloat16,
+    bid,
+    cdiv,
+    convert,
+    exp,
+    float16,
+    float32,
+    kernel,
+    load,
+    load_conv2d,
+    matmul,
+    max as tile_max,
+    store,
+    sum as tile_sum,
+)
+
+
+# -- add ---------------------------------------------------------------------
+
+
+@kernel
+def add_kernel(lhs, rhs, out, tile_h, tile_w):
+    b0 = bid(0)
+    b1 = bid(1)
+    a = load(lhs, index=(b0, b1), shape=(tile_h, tile_w))
+    b = load(rhs, index=(b0, b1), shape=(tile_h, tile_w))
+    store(out, index=(b0, b1), tile=a + b)
+
+
+def add(rows: int, cols: int, tile_h: int = 32, tile_w: int = 64):
+    arr = Array(shape=(rows, cols), dtype=float32)
+    grid = (cdiv(rows, tile_h), cdiv(cols, tile_w), 1)
+    return convert(add_kernel, args=(arr, arr, arr, tile_h, tile_w), grid=grid, double_buffering=True)
+
+
+@kernel
+def add_rows_kernel(lhs, rhs, out, trow, col):
+    """The reference's kernels/add.py program: full-width row tiles."""
+    bid_x = bid(0)
+    a = load(lhs, index=(bid_x, 0), shape=(trow, col))
+    b = load(rhs, index=(bid_x, 0), shape=(trow, col))
+    store(out, index=(bid_x, 0), tile=a + b)
+
+
+def add_rows(rows: int, cols: int, trow: int = 64):
+    arr = Array(shape=(rows, cols), dtype=float32)
+    return convert(
+        add_rows_kernel,
+        args=(arr, arr, arr, trow, cols),
+        grid=(cdiv(rows, trow), 1, 1),
+        double_buffering=True,
+    )
+
+
+# -- softmax -----------------------------------------------------------------
+
+
+@kernel
+def softmax_kernel(inp, out, trow, col):
+    bid_x = bid(0)
+    x = load(inp, index=(bid_x, 0), shape=(trow, col))
+    x = x - tile_max(x, axis=-1)
+    x = exp(x)
+    r = tile_sum(x, axis=-1)
+    x = x / r
+    store(out, index=(bid_x, 0), tile=x)
+
+
+def softmax(rows: int, cols: int, trow: int = 1):
+    arr = Array(shape=(rows, cols), dtype=float32)
+    return convert(
+        softmax_kernel,
+        args=(arr, arr, trow, cols),
+        grid=(cdiv(rows, trow), 1, 1),
+        double_buffering=True,
+    )
+
+
+# -- matmul ------------------------------------------------------------------
+
+
+@kernel
+def matmul_kernel(lhs, rhs, res, tm, tn, tk):
+    """A row panel per bid(0), B column panel per bid(1) shared along axis 0."""
+    bid_m = bid(0)
+    bid_n = bid(1)
+    a = load(lhs, index=(bid_m, 0), shape=(tm, tk))
+    b = load(rhs, index=(0, bid_n), shape=(tk, tn), shared=1)
+    store(res, index=(bid_m, bid_n), tile=matmul(a, b))
+
+
+@kernel
+def matmul_nm_kernel(lhs, rhs, res, tm, tn, tk):
+    """Grid (N/tn, M/tm): bid(0) walks N, so the A panel is `shared = 1`."""
+    bid_n = bid(0)
+    bid_m = bid(1)
+    a = load(lhs, index=(bid_m, 0), shape=(tm, tk), shared=1)
+    b = load(rhs, index=(0, bid_n), shape=(tk, tn))
+    store(res, index=(bid_m, bid_n), tile=matmul(a, b))
+
+
+def matmul_f16(m: int, n: int, k: int, tm: int = 128, tn: int = 128):
+    a = Array(shape=(m, k), dtype=float16)
+    b = Array(shape=(k, n), dtype=float16)
+    c = Array(shape=(m, n), dtype=float32)
+    return convert(
+        matmul_kernel,
+        args=(a, b, c, tm, tn, k),
+        grid=(cdiv(m, tm), cdiv(n, tn), 1),
+        double_buffering=True,
+    )
+
+
+def matmul_bf16(m: int, n: int, k: int, tm: int = 256, tn: int = 128):
+    a = Array(shape=(m, k), dtype=bfloat16)
+    b = Array(shape=(k, n), dtype=bfloat16)
+    c = Array(shape=(m, n), dtype=float32)
+    return convert(
+        matmul_nm_kernel,
+        args=(a, b, c, tm, tn, k),
+        grid=(cdiv(n, tn), cdiv(m, tm), 1),
+        double_buffering=True,
+    )
+
+
+# -- conv2d ------------------------------------------------------------------
+
+
+@kernel
+def conv2d_kernel(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw):
+    bid_n = bid(0)
+    bid_h = bid(1)
+    bid_w = bid(2)
+    zero = 0
+    f = load(filt, index=(zero, zero, zero, zero), shape=(kh, kw, cin, cout), shared=2)
+    t = load_conv2d(
+        inp,
+        f,
+        index=(bid_n, bid_h, bid_w, zero),
+        shape=(1, tile_h, tile_w, cout),
+        group=1,
+        pad=(kh // 2, kw // 2, kh // 2, kw // 2),
+        stride=(1, 1),
+        dilation=(1, 1),
+    )
+    store(out, index=(bid_n, bid_h, bid_w, zero), tile=t)
+
+
+def conv2d(n, h, w, cin, cout, kh=3, kw=3, tile_h=4, tile_w=56, dtype=float16):
+    if h % tile_h or w % tile_w:
+        raise ValueError("tile_h / tile_w must divide h / w")
+    inp = Array(shape=(n, h, w, cin), dtype=dtype)
+    filt = Array(shape=(kh, kw, cin, cout), dtype=dtype)
+    out = Array(shape=(n, h, w, cout), dtype=float32)
+    return convert(
+        conv2d_kernel,
+        args=(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw),
+        grid=(n, h // tile_h, w // tile_w),
+        double_buffering=True,
+    )
+
+
+CONFIGS = {
+    "c1_add": lambda: add(1024, 1024, 32, 64),
+    "c2_softmax": lambda: softmax(8192, 4096, 1),
+    "c3_matmul_f16": lambda: matmul_f16(4096, 4096, 4096, 128, 128),
+    "c4_conv2d_f16": lambda: conv2d(32, 56, 56, 64, 64, 3, 3, 4, 56),
+    "c5_matmul_bf16": lambda: matmul_bf16(4096, 11008, 4096, 256, 128),
+}
