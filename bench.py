@@ -125,12 +125,12 @@ def make_config(name: str):
 
 
 def _traffic(name: str):
-    """HBM bytes per launch from profiles/traffic_<config>.txt (fetch + write)."""
-    path = ROOT / "profiles" / f"traffic_{name}.txt"
-    if not path.exists():
+    """HBM bytes per launch from the profiles/<config>_*.txt summary (fetch + write)."""
+    paths = sorted((ROOT / "profiles").glob(f"{name}_*.txt"))
+    if not paths:
         return None
     vals = {}
-    for line in path.read_text().splitlines():
+    for line in paths[0].read_text().splitlines():
         m = re.match(r"\s*(fetch_bytes|write_bytes)\s*[:=]\s*([0-9.eE+]+)", line)
         if m:
             vals[m.group(1)] = float(m.group(2))
@@ -268,7 +268,26 @@ def main(argv=None) -> int:
     ap.add_argument("--config", default="all", help="all, or one of c1..c5")
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument(
+        "--copy-probe",
+        type=float,
+        default=0.0,
+        metavar="MIB",
+        help="only run a plain device copy of MIB MiB `steps` times (calibrates the "
+        "rocprofv3 FETCH_SIZE / WRITE_SIZE counters against known bytes)",
+    )
     args = ap.parse_args(argv)
+    if args.copy_probe > 0:
+        import torch
+
+        n = int(args.copy_probe * (1 << 20)) // 4
+        src = torch.arange(n, device="cuda:0", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n * 4, "launches": args.steps}), flush=True)
+        return 0
     if args.gpus != 1:
         print(
             "bench.py measures one MI355X: the xtile tile programs run on a single GPU "

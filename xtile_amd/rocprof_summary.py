@@ -1,0 +1,103 @@
+"""Summarise rocprofv3 (rocpd SQLite) output for xtile_amd kernels.
+
+    python -m xtile_amd.rocprof_summary --trace T.db [--fetch F.db --write W.db
+        --copy-fetch CF.db --copy-write CW.db --copy-mib 256] [--kernel REGEX]
+        [--command "..."] > profiles/<config>_<kernel>.txt
+
+Kernel-trace databases give per-kernel dispatch counts and durations.  The
+FETCH_SIZE / WRITE_SIZE databases (one counter per pass) give KiB per
+dispatch; each counter is scaled by the factor that makes it read the true
+byte count of a plain device copy of --copy-mib MiB (which reads and writes
+exactly that many bytes).  The scaled bytes are printed as `fetch_bytes` /
+`write_bytes` lines, which bench.py reads as roofline.traffic.
+"""
+
+from __future__ import annotations
+
+import argparse
+import re
+import sqlite3
+import statistics
+
+
+def _kernels(db_path: str, pattern: str | None):
+    db = sqlite3.connect(db_path)
+    rows = db.execute("select name, duration, grid_x, workgroup_x, dispatch_id from kernels").fetchall()
+    if pattern:
+        rows = [r for r in rows if re.search(pattern, r[0])]
+    return rows
+
+
+def _counter(db_path: str, counter: str, pattern: str | None):
+    db = sqlite3.connect(db_path)
+    rows = db.execute(
+        "select k.name, p.counter_value from pmc_events p join kernels k "
+        "on p.dispatch_id = k.dispatch_id where p.counter_name = ?",
+        (counter,),
+    ).fetchall()
+    if pattern:
+        rows = [r for r in rows if re.search(pattern, r[0])]
+    return [float(v) for _, v in rows]
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--trace", required=True)
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--copy-fetch")
+    ap.add_argument("--copy-write")
+    ap.add_argument("--copy-mib", type=float, default=256.0)
+    ap.add_argument("--kernel", default=None, help="regex selecting the kernel of interest")
+    ap.add_argument("--command", action="append", default=[], help="command lines to record")
+    args = ap.parse_args(argv)
+
+    out = []
+    for c in args.command:
+        out.append(f"# command: {c}")
+    rows = _kernels(args.trace, None)
+    by_name: dict[str, list] = {}
+    for name, dur, gx, wx, _ in rows:
+        by_name.setdefault(name, []).append((dur, gx, wx))
+    out.append("# kernel-trace (durations in microseconds)")
+    out.append(f"{'kernel':44s} {'calls':>6s} {'avg_us':>9s} {'median_us':>9s} {'min_us':>9s} {'max_us':>9s}  grid(threads)")
+    for name, items in sorted(by_name.items(), key=lambda kv: -sum(d for d, _, _ in kv[1])):
+        durs = [d / 1000.0 for d, _, _ in items]
+        grids = sorted({g for _, g, _ in items})
+        out.append(
+            f"{name[:44]:44s} {len(durs):6d} {statistics.mean(durs):9.2f} {statistics.median(durs):9.2f} "
+            f"{min(durs):9.2f} {max(durs):9.2f}  {','.join(map(str, grids))}"
+        )
+    if args.kernel:
+        sel = [d / 1000.0 for n, d, *_ in rows if re.search(args.kernel, n)]
+        if sel:
+            out.append(f"selected_kernel: {args.kernel}")
+            out.append(f"selected_avg_us: {statistics.mean(sel):.3f}")
+    if args.fetch and args.write:
+        fetch = _counter(args.fetch, "FETCH_SIZE", args.kernel)
+        write = _counter(args.write, "WRITE_SIZE", args.kernel)
+        f_scale = w_scale = 1.0
+        true_kib = args.copy_mib * 1024.0
+        if args.copy_fetch and args.copy_write:
+            cf = _counter(args.copy_fetch, "FETCH_SIZE", "copyBuffer")
+            cw = _counter(args.copy_write, "WRITE_SIZE", "copyBuffer")
+            if cf and cw:
+                f_scale = true_kib / statistics.mean(cf)
+                w_scale = true_kib / statistics.mean(cw)
+                out.append(
+                    f"# copy calibration: {args.copy_mib:g} MiB device copy reads FETCH_SIZE="
+                    f"{statistics.mean(cf):.1f} KiB (factor {f_scale:.4f}), WRITE_SIZE="
+                    f"{statistics.mean(cw):.1f} KiB (factor {w_scale:.4f})"
+                )
+        if fetch and write:
+            fk, wk = statistics.mean(fetch), statistics.mean(write)
+            out.append(f"fetch_kib_per_dispatch: {fk:.1f}  (raw, {len(fetch)} dispatches)")
+            out.append(f"write_kib_per_dispatch: {wk:.1f}  (raw, {len(write)} dispatches)")
+            out.append(f"fetch_bytes: {fk * 1024.0 * f_scale:.0f}")
+            out.append(f"write_bytes: {wk * 1024.0 * w_scale:.0f}")
+    print("\n".join(out))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
