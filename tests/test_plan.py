@@ -1,0 +1,93 @@
+"""Launch planner: which kernel a tile program gets, and the host-side checks
+that keep every kernel inside its buffers (runs without a GPU)."""
+
+from __future__ import annotations
+
+import pytest
+
+import xtile_amd as xt
+from xtile_amd import kernels as K
+
+
+@pytest.mark.parametrize(
+    "name,kernel,nbytes,nflops",
+    [
+        ("c1_add", "ew_binary op=add f32 tile=32x64 grid=(32,16,1)", 12582912, 0),
+        ("c2_softmax", "row_softmax f32 tile=1x4096 grid=(8192,1,1)", 268435456, 0),
+        ("c3_matmul_f16", "gemm f16->f32 tile=128x128 k=4096 grid=(32,32,1)", 134217728, 137438953472),
+        ("c4_conv2d_f16", "conv2d_nhwc f16->f32 tile=1x4x56x64 filter=3x3x64x64 grid=(32,14,1)", 38608896, 7398752256),
+        ("c5_matmul_bf16", "gemm bf16->f32 tile=256x128 k=4096 grid=(86,16,1)", 304087040, 369367187456),
+    ],
+)
+def test_benchmark_configs_plan(name, kernel, nbytes, nflops):
+    """Algorithmic work per launch matches BASELINE.md's per-config table."""
+    p = xt.plan(K.CONFIGS[name]())
+    assert p["kernel"] == kernel
+    assert p["bytes"] == nbytes
+    assert p["flops"] == nflops
+
+
+def test_reference_kernel_forms_plan():
+    assert xt.plan(K.add_rows(128, 128, 64))["kernel"].startswith("ew_binary")
+    assert xt.plan(K.softmax(128, 64, 64))["kernel"] == "row_softmax f32 tile=64x64 grid=(2,1,1)"
+
+
+def test_compile_returns_module_and_keeps_text():
+    m = K.softmax(16, 256, 1)
+    before = str(m)
+    assert xt.compile(m) is m
+    assert str(m) == before
+
+
+def test_out_of_bounds_tiles_are_rejected():
+    # kernels/add.py with rows not a multiple of the 64-row tile: the last tile overruns
+    with pytest.raises(NotImplementedError, match="exceeds extent"):
+        xt.plan(K.add_rows(100, 128, 64))
+
+
+def test_unsupported_program_names_its_ops():
+    from tests.golden.dsl_programs import programs
+    from xtile_amd import dsl
+
+    kernel, args, grid, db = programs(dsl)["unary_and_shape"]
+    m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
+    with pytest.raises(NotImplementedError, match="unsupported tile program.*xt.cos"):
+        xt.plan(m)
+
+
+def test_epilogue_matmul_is_reported():
+    from tests.golden.dsl_programs import programs
+    from xtile_amd import dsl
+
+    kernel, args, grid, db = programs(dsl)["matmul_int8_epilogue"]
+    m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
+    with pytest.raises(NotImplementedError, match="epilogues are not supported"):
+        xt.plan(m)
+
+
+def test_nova_stages_raise():
+    with pytest.raises(NotImplementedError, match="x1 NPU lowering"):
+        xt.xt_to_nova(K.add(64, 64, 32, 32))
+
+
+def test_save_compile_results(tmp_path, capsys):
+    m = K.add(64, 128, 32, 64)
+    xt.save_compile_results(m, str(tmp_path / "add"))
+    files = sorted(p.name for p in (tmp_path / "add").iterdir())
+    assert files == ["0_xt.mlir", "1_hip_plan.txt", "2_xt_serialize.mlir"]
+    assert "ew_binary" in (tmp_path / "add" / "1_hip_plan.txt").read_text()
+    assert "compiled kernel ->" in capsys.readouterr().out
+
+
+def test_shared_load_of_moving_tile_plans():
+    """shared=1 with an index that moves along axis 0: the group leader's tile is used."""
+    text = """
+func.func @s(%a: memref<64x64xf32>, %b: memref<64x64xf32>, %c: memref<64x64xf32>) attributes {xt.grid = array<i32: 2, 2, 1>} {
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %0 = xt.load(%a, %bid#0, %bid#1) {shared = 1 : i64} : (memref<64x64xf32>, i32, i32) -> tensor<32x32xf32>
+  %1 = xt.load(%b, %bid#0, %bid#1) : (memref<64x64xf32>, i32, i32) -> tensor<32x32xf32>
+  %2 = xt.add(%0, %1) : tensor<32x32xf32>, tensor<32x32xf32> -> tensor<32x32xf32>
+  xt.store(%2, %c, %bid#0, %bid#1) : (tensor<32x32xf32>, memref<64x64xf32>, i32, i32) -> ()
+  func.return
+}"""
+    assert xt.plan(xt.parse(text))["kernel"].startswith("ew_binary")
