@@ -15,7 +15,7 @@
 // Two kernel families:
 //   gemm256_kernel  BM x BN x BK = 256 x 256 x 64, 4 waves of 128 x 128 using
 //                   v_mfma_f32_32x32x16_{f16,bf16}; one workgroup per CU
-//                   (147 KB of LDS), 256 accumulators per lane in AGPRs.
+//                   (128 KB of LDS), 256 accumulators per lane in AGPRs.
 //                   Per 16-wide K step a wave reads 8 LDS fragments for 16
 //                   MFMAs, half the LDS bytes per FLOP of a 64 x 64 wave tile.
 //   gemm_kernel     BM, BN in {64, 128} x BK = 64, 4 waves of (BM/2) x (BN/2)
@@ -177,6 +177,60 @@ struct Stager {
   }
 };
 
+// Stager of the 256 family.  LDS tiles are unpadded [rows][64] arrays whose
+// 16-byte chunks are XOR-swizzled: chunk c of row r lives at c ^ swz(r) with
+// swz(r) = (r ^ r >> 3) & 7.  Eight consecutive rows then spread one chunk
+// index over all eight chunk positions (fragment reads), and rows 8 apart get
+// different positions too (transposed B stores): every access below runs at
+// the bank-conflict-free rate.  B is staged as 8(k) x 8(n) sub-blocks: a
+// half-wave reads 512 contiguous bytes of one B row per instruction.
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+struct Stager256 {
+  static constexpr int BM = 256, BN = 256;
+  uint4v ra[BM * BK / 8 / 256];  // 8 row chunks of A
+  uint4v rb[8];                  // one 8(k) x 8(n) sub-block of B
+
+  __device__ __forceinline__ void load(const unsigned short* A, const unsigned short* B,
+                                       long long lda, long long ldb, int kt, int tid) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int v = tid + i * 256;
+      const int row = v >> 3, cv = v & 7;
+      ra[i] = *reinterpret_cast<const uint4v*>(A + (long long)row * lda + kt * BK + cv * 8);
+    }
+    const int nb = tid & 31, kb = tid >> 5;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      rb[i] = *reinterpret_cast<const uint4v*>(B + (long long)(kt * BK + kb * 8 + i) * ldb + nb * 8);
+  }
+
+  __device__ __forceinline__ void store(unsigned short (*As)[BK], unsigned short (*Bs)[BK],
+                                        int tid) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int v = tid + i * 256;
+      const int row = v >> 3, cv = v & 7;
+      *reinterpret_cast<uint4v*>(&As[row][(cv ^ swz(row)) * 8]) = ra[i];
+    }
+    const int nb = tid & 31, kb = tid >> 5;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // columns n = 2j (low halves) and 2j+1 (high halves) of the 8 loaded rows
+      uint4v even, odd;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned int lo = rb[2 * q][j], hi = rb[2 * q + 1][j];
+        even[q] = (lo & 0xFFFFu) | (hi << 16);
+        odd[q] = (lo >> 16) | (hi & 0xFFFF0000u);
+      }
+      const int r0 = nb * 8 + 2 * j, r1 = r0 + 1;
+      *reinterpret_cast<uint4v*>(&Bs[r0][(kb ^ swz(r0)) * 8]) = even;
+      *reinterpret_cast<uint4v*>(&Bs[r1][(kb ^ swz(r1)) * 8]) = odd;
+    }
+  }
+};
+
 // --- 256 x 256 family ---------------------------------------------------------
 
 template <bool BF16>
@@ -184,8 +238,8 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(GemmArgs p) {
   constexpr int BM = 256, BN = 256;
   constexpr int WM = 128, WN = 128;  // 2 x 2 waves
   constexpr int MI = WM / 32, NI = WN / 32;
-  __shared__ __attribute__((aligned(16))) unsigned short As[2][BM][LDK];
-  __shared__ __attribute__((aligned(16))) unsigned short Bs[2][BN][LDK];
+  __shared__ __attribute__((aligned(16))) unsigned short As[2][BM][BK];
+  __shared__ __attribute__((aligned(16))) unsigned short Bs[2][BN][BK];
 
   const TilePtrs t = gemm_tile_of<BM, BN>(p);
   const int tid = threadIdx.x;
@@ -196,7 +250,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(GemmArgs p) {
   // Two register staging sets keep two K slices in flight: slice kt+2 is
   // requested while slice kt feeds the MFMAs and slice kt+1 (requested one
   // iteration earlier) is moved to LDS.
-  Stager<BM, BN> st0, st1;
+  Stager256 st0, st1;
   float16v acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -211,22 +265,27 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(GemmArgs p) {
   st0.store(As[0], Bs[0], tid);
   __syncthreads();
   const int lrow = lane & 31;
-  const int lk = (lane >> 5) * 8;
   // Fragments of K step ks+1 are read from LDS while the 16 MFMAs of step ks
   // run (two register sets), so only the first read of each slice is exposed.
   short8 af[2][MI], bfr[2][NI];
+  // chunk index of this lane's 8 K values in step ks: 2*ks + lane/32
   auto read_frags = [&](int buf, int ks, int set) {
+    const int c = ks * 2 + (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
-      af[set][i] = *reinterpret_cast<const short8*>(&As[buf][wm * WM + i * 32 + lrow][ks * 16 + lk]);
+    for (int i = 0; i < MI; ++i) {
+      const int r = wm * WM + i * 32 + lrow;
+      af[set][i] = *reinterpret_cast<const short8*>(&As[buf][r][(c ^ swz(r)) * 8]);
+    }
 #pragma unroll
-    for (int j = 0; j < NI; ++j)
-      bfr[set][j] = *reinterpret_cast<const short8*>(&Bs[buf][wn * WN + j * 32 + lrow][ks * 16 + lk]);
+    for (int j = 0; j < NI; ++j) {
+      const int r = wn * WN + j * 32 + lrow;
+      bfr[set][j] = *reinterpret_cast<const short8*>(&Bs[buf][r][(c ^ swz(r)) * 8]);
+    }
   };
   // One K slice: compute from LDS[cur], request slice kt+2 into `next2`, move
   // slice kt+1 from `next1` into LDS[cur^1].  Branch-free: slice indices are
   // clamped to the last slice, whose repeated copies land in the idle buffer.
-  auto slice = [&](int kt, Stager<BM, BN>& next2, const Stager<BM, BN>& next1) {
+  auto slice = [&](int kt, Stager256& next2, const Stager256& next1) {
     const int cur = kt & 1;
     read_frags(cur, 0, 0);
     next2.load(t.A, t.B, p.lda, p.ldb, min(kt + 2, nk - 1), tid);
