@@ -263,8 +263,8 @@ def measure(name: str, steps: int, warmup: int, cpu_seconds: float, use_graph: b
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="all", help="all, or one of c1..c5")
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-graph", action="store_true")

@@ -32,8 +32,19 @@ __device__ __forceinline__ float ew_apply(float x, float y) {
   else return x * y;
 }
 
+// Streaming accesses: tiles are read and written exactly once per launch, so
+// loads and stores are non-temporal (they do not displace reusable lines).
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void st_nt(T v, T* p) { __builtin_nontemporal_store(v, p); }
+
+// Each thread handles U vectors per step.  All U loads are issued before any
+// is consumed (indices past the end are clamped to element 0 and their results
+// discarded), so a step costs one memory round trip, not U.
 template <int OP, int VW>
 __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
+  constexpr int U = 4;
   int x, y, z;
   decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
   const float* A = p.a + p.ta.at(x, y, z);
@@ -41,20 +52,46 @@ __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
   float* C = p.c + p.tc.at(x, y, z);
   const int cv = p.cols / VW;
   const int n = p.rows * cv;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const int r = i / cv;
-    const int col = (i - r * cv) * VW;
+  for (int base = threadIdx.x; base < n; base += 256 * U) {
+    long long offa[U], offb[U], offc[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * 256;
+      ok[u] = i < n;
+      const int ic = ok[u] ? i : 0;
+      const int r = ic / cv;
+      const int col = (ic - r * cv) * VW;
+      offa[u] = r * p.lda + col;
+      offb[u] = r * p.ldb + col;
+      offc[u] = r * p.ldc + col;
+    }
     if constexpr (VW == 4) {
-      float4v va = *reinterpret_cast<const float4v*>(A + r * p.lda + col);
-      float4v vb = *reinterpret_cast<const float4v*>(B + r * p.ldb + col);
-      float4v vc;
-      vc.x = ew_apply<OP>(va.x, vb.x);
-      vc.y = ew_apply<OP>(va.y, vb.y);
-      vc.z = ew_apply<OP>(va.z, vb.z);
-      vc.w = ew_apply<OP>(va.w, vb.w);
-      *reinterpret_cast<float4v*>(C + r * p.ldc + col) = vc;
+      float4v va[U], vb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        va[u] = ld_nt(reinterpret_cast<const float4v*>(A + offa[u]));
+        vb[u] = ld_nt(reinterpret_cast<const float4v*>(B + offb[u]));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float4v vc;
+        vc.x = ew_apply<OP>(va[u].x, vb[u].x);
+        vc.y = ew_apply<OP>(va[u].y, vb[u].y);
+        vc.z = ew_apply<OP>(va[u].z, vb[u].z);
+        vc.w = ew_apply<OP>(va[u].w, vb[u].w);
+        if (ok[u]) st_nt(vc, reinterpret_cast<float4v*>(C + offc[u]));
+      }
     } else {
-      C[r * p.ldc + col] = ew_apply<OP>(A[r * p.lda + col], B[r * p.ldb + col]);
+      float va[U], vb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        va[u] = ld_nt(A + offa[u]);
+        vb[u] = ld_nt(B + offb[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) st_nt(ew_apply<OP>(va[u], vb[u]), C + offc[u]);
     }
   }
 }
@@ -71,88 +108,101 @@ struct SoftmaxArgs {
 
 // Row reduction across the `tpr` threads that share a row.  For tpr <= 64 the
 // group lies inside one wave and a butterfly suffices; wider rows combine the
-// per-wave partials through LDS.
-template <bool IS_MAX>
-__device__ __forceinline__ float row_reduce(float v, int tpr, float* lds) {
-  const int w = min(tpr, 64);
-  v = IS_MAX ? wave_max(v, w) : wave_sum(v, w);
-  if (tpr <= 64) return v;
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) lds[wave] = v;
-  __syncthreads();
-  const int per_row = tpr >> 6;
-  const int first = (wave / per_row) * per_row;
-  float r = lds[first];
-  for (int k = 1; k < per_row; ++k) r = IS_MAX ? fmaxf(r, lds[first + k]) : r + lds[first + k];
-  __syncthreads();
-  return r;
+// per-wave partials through LDS with a single barrier.  Max and sum use
+// separate LDS slots, so the barrier of each reduction also orders the
+// previous reduction's reads before the next writes of the same slot.
+template <bool IS_MAX, int TPR>
+__device__ __forceinline__ float row_reduce(float v, float* lds) {
+  constexpr int W = TPR < 64 ? TPR : 64;
+#pragma unroll
+  for (int o = W >> 1; o > 0; o >>= 1) {
+    const float t = __shfl_xor(v, o, 64);
+    v = IS_MAX ? fmaxf(v, t) : v + t;
+  }
+  if constexpr (TPR <= 64) {
+    return v;
+  } else {
+    constexpr int PER_ROW = TPR / 64;
+    float* slot = lds + (IS_MAX ? 0 : 4);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) slot[wave] = v;
+    __syncthreads();
+    const int first = (wave / PER_ROW) * PER_ROW;
+    float r = slot[first];
+#pragma unroll
+    for (int k = 1; k < PER_ROW; ++k) r = IS_MAX ? fmaxf(r, slot[first + k]) : r + slot[first + k];
+    return r;
+  }
 }
 
-template <int NV, int VW>
+// All NV row loads of a pass are unconditional (out-of-range columns and rows
+// read element 0 of the tile and are masked out afterwards) so they are in
+// flight together; only the stores are predicated.
+// EXACT: the row is exactly NV*VW*TPR elements and the tile has a multiple of
+// 256/TPR rows, so no lane or row needs masking.
+template <int NV, int VW, int TPR, bool EXACT>
 __global__ __launch_bounds__(256) void row_softmax_kernel(SoftmaxArgs p) {
-  __shared__ float lds[4];
+  __shared__ float lds[8];
   int x, y, z;
   decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
   const float* X = p.x + p.tx.at(x, y, z);
   float* Y = p.y + p.ty.at(x, y, z);
-  const int tpr = p.tpr;
-  const int rpp = 256 / tpr;
-  const int lane = threadIdx.x & (tpr - 1);
-  const int row_in_pass = threadIdx.x / tpr;
+  constexpr int tpr = TPR;
+  constexpr int rpp = 256 / TPR;
+  const int lane = threadIdx.x & (TPR - 1);
+  const int row_in_pass = threadIdx.x / TPR;
   const int passes = (p.rows + rpp - 1) / rpp;
   for (int pass = 0; pass < passes; ++pass) {
     const int r = pass * rpp + row_in_pass;
-    const bool live = r < p.rows;
-    const float* xr = X + (long long)r * p.ldx;
+    const bool live = EXACT || r < p.rows;
+    const float* xr = X + (long long)(live ? r : 0) * p.ldx;
     float* yr = Y + (long long)r * p.ldy;
     float v[NV][VW];
+    bool ok[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int col = (lane + j * tpr) * VW;
+      ok[j] = EXACT || (live && col < p.cols);
+      const int cc = ok[j] ? col : 0;
+      if constexpr (VW == 4) {
+        float4v t = ld_nt(reinterpret_cast<const float4v*>(xr + cc));
+        v[j][0] = t.x;
+        v[j][1] = t.y;
+        v[j][2] = t.z;
+        v[j][3] = t.w;
+      } else {
+        v[j][0] = ld_nt(xr + cc);
+      }
+    }
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int col = (lane + j * tpr) * VW;
-      if (live && col < p.cols) {
-        if constexpr (VW == 4) {
-          float4v t = *reinterpret_cast<const float4v*>(xr + col);
-          v[j][0] = t.x;
-          v[j][1] = t.y;
-          v[j][2] = t.z;
-          v[j][3] = t.w;
-        } else {
-          v[j][0] = xr[col];
-        }
+    for (int j = 0; j < NV; ++j)
 #pragma unroll
-        for (int k = 0; k < VW; ++k) m = fmaxf(m, v[j][k]);
-      }
-    }
-    m = row_reduce<true>(m, tpr, lds);
+      for (int k = 0; k < VW; ++k) m = ok[j] ? fmaxf(m, v[j][k]) : m;
+    m = row_reduce<true, TPR>(m, lds);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int col = (lane + j * tpr) * VW;
-      if (live && col < p.cols) {
+    for (int j = 0; j < NV; ++j)
 #pragma unroll
-        for (int k = 0; k < VW; ++k) {
-          v[j][k] = expf(v[j][k] - m);
-          s += v[j][k];
-        }
+      for (int k = 0; k < VW; ++k) {
+        v[j][k] = ok[j] ? expf(v[j][k] - m) : 0.0f;
+        s += v[j][k];
       }
-    }
-    s = row_reduce<false>(s, tpr, lds);
+    s = row_reduce<false, TPR>(s, lds);
     const float inv = 1.0f / s;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
+      if (!ok[j]) continue;
       const int col = (lane + j * tpr) * VW;
-      if (live && col < p.cols) {
-        if constexpr (VW == 4) {
-          float4v t;
-          t.x = v[j][0] * inv;
-          t.y = v[j][1] * inv;
-          t.z = v[j][2] * inv;
-          t.w = v[j][3] * inv;
-          *reinterpret_cast<float4v*>(yr + col) = t;
-        } else {
-          yr[col] = v[j][0] * inv;
-        }
+      if constexpr (VW == 4) {
+        float4v t;
+        t.x = v[j][0] * inv;
+        t.y = v[j][1] * inv;
+        t.z = v[j][2] * inv;
+        t.w = v[j][3] * inv;
+        st_nt(t, reinterpret_cast<float4v*>(yr + col));
+      } else {
+        st_nt(v[j][0] * inv, yr + col);
       }
     }
   }
@@ -236,23 +286,44 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
   int tpr = 1;
   while (tpr < need) tpr *= 2;
   a.tpr = tpr;
+  const bool exact = a.cols == nv * vw * tpr && a.rows % (256 / tpr) == 0;
   dim3 grid(num_blocks(p)), block(256);
-#define XT_SM(NVV, VWV) hipLaunchKernelGGL((row_softmax_kernel<NVV, VWV>), grid, block, 0, s, a)
+#define XT_SM(NVV, VWV, TPRV)                                                               \
+  do {                                                                                      \
+    if (VWV == 4 && TPRV >= 64 && exact)                                                    \
+      hipLaunchKernelGGL((row_softmax_kernel<NVV, VWV, TPRV, (VWV == 4 && TPRV >= 64)>),    \
+                         grid, block, 0, s, a);                                             \
+    else                                                                                    \
+      hipLaunchKernelGGL((row_softmax_kernel<NVV, VWV, TPRV, false>), grid, block, 0, s, a); \
+  } while (0)
+#define XT_SM_TPR(NVV, VWV)                          \
+  switch (tpr) {                                     \
+    case 1: XT_SM(NVV, VWV, 1); break;               \
+    case 2: XT_SM(NVV, VWV, 2); break;               \
+    case 4: XT_SM(NVV, VWV, 4); break;               \
+    case 8: XT_SM(NVV, VWV, 8); break;               \
+    case 16: XT_SM(NVV, VWV, 16); break;             \
+    case 32: XT_SM(NVV, VWV, 32); break;             \
+    case 64: XT_SM(NVV, VWV, 64); break;             \
+    case 128: XT_SM(NVV, VWV, 128); break;           \
+    default: XT_SM(NVV, VWV, 256); break;            \
+  }
   if (vw == 4) {
     switch (nv) {
-      case 1: XT_SM(1, 4); break;
-      case 2: XT_SM(2, 4); break;
-      case 4: XT_SM(4, 4); break;
-      default: XT_SM(8, 4); break;
+      case 1: XT_SM_TPR(1, 4); break;
+      case 2: XT_SM_TPR(2, 4); break;
+      case 4: XT_SM_TPR(4, 4); break;
+      default: XT_SM_TPR(8, 4); break;
     }
   } else {
     switch (nv) {
-      case 1: XT_SM(1, 1); break;
-      case 2: XT_SM(2, 1); break;
-      case 4: XT_SM(4, 1); break;
-      default: XT_SM(8, 1); break;
+      case 1: XT_SM_TPR(1, 1); break;
+      case 2: XT_SM_TPR(2, 1); break;
+      case 4: XT_SM_TPR(4, 1); break;
+      default: XT_SM_TPR(8, 1); break;
     }
   }
+#undef XT_SM_TPR
 #undef XT_SM
   return hipGetLastError();
 }
