@@ -140,3 +140,50 @@ def test_conv2d_f16(cuda, n, h, w, cin, cout, th, tw):
     got = run_gpu(mod, [x, f, o], ["f16", "f16", "f32"], cuda, case=f"conv {n}x{h}x{w}x{cin}->{cout}")[2]
     want = run_oracle(mod, [x, f, o], oracle_threads())[2]
     assert frob_rel(got, want) <= MM_FROB
+
+
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil,dt",
+    [
+        (2, 16, 16, 64, 64, 3, 3, 2, 8, (1, 1, 1, 1), (2, 2), (1, 1), "f16"),
+        (2, 12, 12, 32, 48, 3, 3, 4, 12, (2, 2, 2, 2), (1, 1), (2, 2), "f16"),
+        (1, 10, 14, 32, 32, 5, 5, 2, 14, (2, 2, 2, 2), (1, 1), (1, 1), "f16"),
+        (2, 8, 16, 32, 80, 3, 3, 4, 16, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),
+        (3, 9, 9, 96, 32, 1, 1, 3, 9, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),
+        (2, 11, 13, 32, 64, 3, 3, 3, 7, (0, 1, 2, 1), (2, 2), (1, 1), "f16"),
+        (2, 14, 14, 64, 64, 3, 3, 7, 14, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),
+        (1, 8, 8, 32, 128, 3, 3, 4, 8, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),
+    ],
+)
+def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
+    """Strides, dilations, asymmetric padding, 1x1 / 5x5 filters, Cout with a
+    partial 32-channel N tile (48, 80) and bf16 operands."""
+    rng = np.random.default_rng(5)
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
+                   pad=pad, stride=stride, dilation=dil)
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+    if dt == "bf16":
+        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    else:
+        x, f = x.astype(np.float16), f.astype(np.float16)
+    o = np.zeros((n, oh, ow, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
+                  case=f"conv {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil} {dt}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+
+
+def test_conv2d_filter_too_large_is_refused(cuda):
+    """The whole filter lives in LDS; a 5x5x64x80 filter (411 KB transposed)
+    cannot, and the launch is refused on the host before any kernel runs."""
+    import torch
+
+    mod = K.conv2d(1, 10, 14, 64, 80, 5, 5, 2, 14)
+    x = torch.zeros((1, 10, 14, 64), dtype=torch.float16, device=cuda)
+    f = torch.zeros((5, 5, 64, 80), dtype=torch.float16, device=cuda)
+    o = torch.zeros((1, 10, 14, 80), dtype=torch.float32, device=cuda)
+    with pytest.raises(ValueError, match="does not fit the LDS budget"):
+        xt.launch(mod, x, f, o)

@@ -17,13 +17,20 @@
 //     layout).  It is the `shared = 2` tile of the reference kernel
 //     (kernels/conv2d.py:19-24): every Block reads the same filter.
 //   * The receptive-field halo of a unit (rf_h x rf_w x Cin, NHWC so channels
-//     are contiguous) lives in one of two LDS buffers, zero-filled outside the
-//     image.  The next unit's halo is loaded into registers while the current
-//     unit computes, then written to the other buffer; one barrier per unit.
-//   * Waves take the unit's 16-pixel M tiles round-robin and all Cout/16 N
-//     tiles, v_mfma_f32_16x16x32_{f16,bf16}; each B fragment read from LDS
-//     feeds every M tile of the wave.
-//   * Outputs are written once and never re-read: non-temporal stores.
+//     are contiguous) lives in LDS, zero-filled outside the image.  The next
+//     unit's halo is loaded into registers while the current unit computes and
+//     written to LDS between two barriers.
+//   * v_mfma_f32_32x32x16_{f16,bf16}: waves take the unit's 32-pixel M tiles
+//     in pairs (w, w+4) against every 32-channel N tile, so each fragment read
+//     from LDS feeds two MFMAs.  The filter fragment is the A operand, so each
+//     lane ends up holding runs of consecutive channels of one pixel.  Fragments of step s+1 are read while the
+//     MFMAs of step s run.  LDS rows are padded by 16 bytes: the pitch is an
+//     odd number of 16-byte chunks, so 16 consecutive pixels (or filter rows)
+//     hit 16 distinct 4-bank groups.
+//   * Outputs are written once and never re-read: non-temporal 16-byte buffer
+//     stores; halo loads and output stores go through buffer descriptors whose
+//     range check supplies the zero padding and drops the ragged edge.
+//   * Waves 0-3 compute; waves 4-7 only fetch halos (see conv2d_kernel).
 #include <algorithm>
 #include <atomic>
 
@@ -34,8 +41,17 @@ namespace xtk {
 namespace {
 
 constexpr int HV = 12;  // halo 16-byte vectors per thread per unit (at most)
-constexpr int MT = 2;   // M tiles per wave per round
-constexpr int FB = 4;   // filter sub-blocks per thread per batch
+constexpr int FB = 6;   // filter sub-blocks per thread per batch
+constexpr int CT = 256; // compute threads (waves 0-3); they also stage the filter
+constexpr int WG = 512; // threads: waves 0-3 compute, waves 4-7 load halos
+constexpr int HT = 256; // halo loader threads
+constexpr int kOutPitch = 144;  // LDS bytes per staged output pixel (32 floats + 16-byte pad)
+
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+struct Magic {
+  unsigned m, k;
+};
 
 struct ConvArgs {
   const unsigned short* src;
@@ -54,18 +70,41 @@ struct ConvArgs {
   int units_per_block;  // TH / UR
   int total_units;
   int rf_h, rf_w;       // receptive field of one unit
-  int cpad;             // LDS pitch of one halo pixel (Cin + 8)
-  int kpad;             // LDS pitch of one filter row (K + 8)
+  int pitch;            // LDS bytes per halo pixel (2*Cin + 16)
+  int kpitch;           // LDS bytes per filter row (2*K + 16)
   int halo_vecs;        // rf_h * rf_w * Cin / 8
+  int halo_bytes;       // rf_h * rf_w * pitch
+  int nmt;              // 32-pixel M tiles per unit
+  int steps;            // K / 16 (even: Cin % 32 == 0)
+  // Multiply-high reciprocals of the divisors used per thread (see udiv).
+  Magic m_cv, m_rfw, m_tw, m_cg;  // Cin/8, rf_w, TW, Cout/8
+  unsigned image_bytes;              // H*W*Cin*2: one batch entry of the source
+  unsigned unit_out_bytes;           // UR*out_W*out_C*4: the output rows of one unit
 };
 
+// n / d for n, d < 2^16 as umulhi(n, ceil(2^32 / d)) + (n & k), where k is
+// all ones for d == 1 (m = 0) and zero otherwise, so there is no branch.
+// Exact: with m*d = 2^32 + r (0 <= r < d) and n = q*d + s, n*m / 2^32 =
+// q + (s + n*r / 2^32) / d and n*r < 2^32, so the fraction stays below 1.
+__host__ __device__ __forceinline__ unsigned udiv(unsigned n, Magic m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __umulhi(n, m.m) + (n & m.k);
+#else
+  return unsigned((unsigned long long)n * m.m >> 32) + (n & m.k);
+#endif
+}
+
+inline Magic udiv_magic(unsigned d) {
+  return d == 1 ? Magic{0u, ~0u} : Magic{unsigned(((1ull << 32) + d - 1) / d), 0u};
+}
+
 template <bool BF16>
-__device__ __forceinline__ float4v mfma16(short8 a, short8 b, float4v c) {
+__device__ __forceinline__ float16v mfma32(short8 a, short8 b, float16v c) {
   if constexpr (BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
                                                   __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 
@@ -95,62 +134,88 @@ __device__ __forceinline__ Unit unit_of(const ConvArgs& p, int u) {
   return t;
 }
 
-// Halo of unit `t` -> registers.  Every load is issued (out-of-range vectors
-// read the image base and are zeroed), so the whole halo is one round trip.
-__device__ __forceinline__ void load_halo(const ConvArgs& p, const Unit& t, int tid, uint4v (&hv)[HV]) {
+// Loader thread `tid` owns the halo's 16-byte vectors tid + i*HT.  Their
+// coordinates are recomputed per unit (a few multiply-highs) rather than kept
+// in registers: every wave of the workgroup holds the same register budget.
+struct HaloSlot {
+  int r, c, src, dst;  // halo row / column, element offset from the halo origin, LDS byte offset
+};
+
+__device__ __forceinline__ HaloSlot halo_slot(const ConvArgs& p, int v) {
   const int cv = p.C / 8;
+  const int pix = udiv(v, p.m_cv);
+  const int c8 = v - pix * cv;
+  HaloSlot h;
+  h.r = udiv(pix, p.m_rfw);
+  h.c = pix - h.r * p.rf_w;
+  h.src = (h.r * p.W + h.c) * p.C + c8 * 8;
+  h.dst = pix * p.pitch + c8 * 16;
+  return h;
+}
+
+// Buffer descriptors (gfx9 raw buffers: stride 0, word3 0x00020000).  A
+// buffer load whose offset lies past num_records returns zero and such a store
+// is dropped, so halo padding and the unit's ragged edge need no branches.
+constexpr unsigned kOutOfRange = 0x80000000u;  // every buffer here is < 2 GiB
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Halo of unit `t` -> registers, every load issued back to back (one round
+// trip).  Vectors outside the image read as zero through the descriptor.
+// dst[i] receives vector i's LDS offset (or -1 past the halo) for store_halo.
+__device__ __forceinline__ void load_halo(const ConvArgs& p, const Unit& t, int tid, uint4v (&hv)[HV],
+                                          int (&dst)[HV]) {
+  const __amdgpu_buffer_rsrc_t img = buffer_of(t.S, p.image_bytes);
+  const int org = (t.ih0 * p.W + t.iw0) * p.C;  // may be negative; only in-image sums are used
 #pragma unroll
   for (int i = 0; i < HV; ++i) {
-    const int v = tid + i * 256;
-    const int vc = v < p.halo_vecs ? v : 0;
-    const int c8 = vc % cv;
-    const int pix = vc / cv;
-    const int r = pix / p.rf_w, c = pix - r * p.rf_w;
-    const int ih = t.ih0 + r, iw = t.iw0 + c;
-    const bool inside = v < p.halo_vecs && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
-    const unsigned short* addr = inside ? t.S + ((long long)ih * p.W + iw) * p.C + c8 * 8 : t.S;
-    const uint4v val = *reinterpret_cast<const uint4v*>(addr);
-    hv[i] = inside ? val : uint4v{0u, 0u, 0u, 0u};
+    const int v = tid + i * HT;
+    const HaloSlot h = halo_slot(p, v < p.halo_vecs ? v : 0);
+    const int ih = t.ih0 + h.r, iw = t.iw0 + h.c;
+    const bool inside = v < p.halo_vecs && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+    const unsigned off = inside ? unsigned(org + h.src) * 2u : kOutOfRange;
+    hv[i] = __builtin_amdgcn_raw_buffer_load_b128(img, off, 0, 0);
+    dst[i] = v < p.halo_vecs ? h.dst : -1;
   }
 }
 
-__device__ __forceinline__ void store_halo(const ConvArgs& p, unsigned short* Is, int tid,
-                                           const uint4v (&hv)[HV]) {
-  const int cv = p.C / 8;
+__device__ __forceinline__ void store_halo(unsigned char* Is, const uint4v (&hv)[HV], const int (&dst)[HV]) {
 #pragma unroll
-  for (int i = 0; i < HV; ++i) {
-    const int v = tid + i * 256;
-    if (v < p.halo_vecs) {
-      const int c8 = v % cv;
-      const int pix = v / cv;
-      *reinterpret_cast<uint4v*>(&Is[pix * p.cpad + c8 * 8]) = hv[i];
-    }
-  }
+  for (int i = 0; i < HV; ++i)
+    if (dst[i] >= 0) *reinterpret_cast<uint4v*>(Is + dst[i]) = hv[i];
 }
 
 // Filter -> LDS, transposed by 4(k) x 8(cout) register blocks; FB blocks per
 // thread per batch, all of a batch's loads issued before the first use.
+// Consecutive threads take consecutive 8-channel groups of the same K rows, so
+// a wave's load covers whole 128-byte lines (every workgroup reads the same
+// filter at the same moment; scattered 16-byte reads would multiply the L2
+// requests by 8).  Rows Cout..rows-1 (the tail of the last 32-wide N tile)
+// are zeroed.
 __device__ __forceinline__ void stage_filter(const ConvArgs& p, const unsigned short* F,
-                                             unsigned short* Fs, int tid) {
+                                             unsigned char* Fs, int rows, int tid) {
   const int K = p.KH * p.KW * p.C;
   const int kgroups = K / 4;
-  const int nsub = kgroups * (p.CO / 8);
-  for (int base = tid; base < nsub; base += 256 * FB) {
+  const int cgroups = p.CO / 8;
+  const int nsub = kgroups * cgroups;
+  for (int base = tid; base < nsub; base += CT * FB) {
     uint4v r[FB][4];
 #pragma unroll
     for (int b = 0; b < FB; ++b) {
-      const int sb = base + b * 256;
+      const int sb = base + b * CT;
       const int sbc = sb < nsub ? sb : 0;
-      const int kg = sbc % kgroups, cg = sbc / kgroups;
+      const int kg = udiv(sbc, p.m_cg), cg = sbc - kg * cgroups;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         r[b][i] = *reinterpret_cast<const uint4v*>(F + (long long)(kg * 4 + i) * p.CO + cg * 8);
     }
 #pragma unroll
     for (int b = 0; b < FB; ++b) {
-      const int sb = base + b * 256;
+      const int sb = base + b * CT;
       if (sb >= nsub) continue;
-      const int kg = sb % kgroups, cg = sb / kgroups;
+      const int kg = udiv(sb, p.m_cg), cg = sb - kg * cgroups;
       const int k0 = kg * 4, c0 = cg * 8;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -159,106 +224,218 @@ __device__ __forceinline__ void stage_filter(const ConvArgs& p, const unsigned s
         even.y = (r[b][2][j] & 0xFFFFu) | (r[b][3][j] << 16);
         odd.x = (r[b][0][j] >> 16) | (r[b][1][j] & 0xFFFF0000u);
         odd.y = (r[b][2][j] >> 16) | (r[b][3][j] & 0xFFFF0000u);
-        *reinterpret_cast<uint2v*>(&Fs[(c0 + 2 * j) * p.kpad + k0]) = even;
-        *reinterpret_cast<uint2v*>(&Fs[(c0 + 2 * j + 1) * p.kpad + k0]) = odd;
+        *reinterpret_cast<uint2v*>(Fs + (c0 + 2 * j) * p.kpitch + k0 * 2) = even;
+        *reinterpret_cast<uint2v*>(Fs + (c0 + 2 * j + 1) * p.kpitch + k0 * 2) = odd;
       }
     }
   }
+  const int tail = (rows - p.CO) * (K / 8);  // 16-byte vectors of zero rows
+  for (int v = tid; v < tail; v += CT) {
+    const int row = p.CO + v / (K / 8), ch = v % (K / 8);
+    *reinterpret_cast<uint4v*>(Fs + row * p.kpitch + ch * 16) = uint4v{0u, 0u, 0u, 0u};
+  }
 }
 
-template <int NT, bool BF16>
-__device__ __forceinline__ void compute_unit(const ConvArgs& p, const Unit& t,
-                                             const unsigned short* Fs, const unsigned short* Is,
-                                             int tid) {
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int lrow = lane & 15;
-  const int lk = (lane >> 4) * 8;
+// M tiles mt0 and mt0+4 (MT == 2) or mt0 alone (MT == 1) of the unit against
+// all NT N tiles.  Step s covers K [16s, 16s+16): tap (kh, kw) = s / (Cin/16),
+// channels 16 * (s % (Cin/16)) ... + 16; lane l reads 8 of them (l/32 picks the
+// half) for pixel / filter row l%32.
+template <int MT, int NT, bool BF16>
+__device__ __forceinline__ void conv_tiles(const ConvArgs& p, const Unit& t, const unsigned char* Fs,
+                                           const unsigned char* Is, unsigned char* Os, int mt0, int lane) {
+  const int lr = lane & 31, hi = lane >> 5;
   const int M = p.UR * p.TW;
-  const int nmt = (M + 15) / 16;
-  // wave w owns M tiles w, w+4, w+8, ...; MT of them per round
-  for (int mt0 = wave; mt0 < nmt; mt0 += 4 * MT) {
-    float4v acc[MT][NT];
-    int base[MT];
+  int abase[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int pix = (mt0 + 4 * i) * 16 + lrow;
-      const bool valid = (mt0 + 4 * i) < nmt && pix < M;
-      const int ph = valid ? pix / p.TW : 0;
-      const int pw = valid ? pix - ph * p.TW : 0;
-      base[i] = ph * p.sh * p.rf_w + pw * p.sw;
+  for (int i = 0; i < MT; ++i) {
+    const int pix = min((mt0 + 4 * i) * 32 + lr, M - 1);
+    const int ph = udiv(pix, p.m_tw), pw = pix - ph * p.TW;
+    abase[i] = (ph * p.sh * p.rf_w + pw * p.sw) * p.pitch + hi * 16;
+  }
+  int bbase[NT];
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int kh = 0; kh < p.KH; ++kh)
-      for (int kw = 0; kw < p.KW; ++kw) {
-        const int tap = kh * p.dh * p.rf_w + kw * p.dw;
-        const int kbase = (kh * p.KW + kw) * p.C;
-        for (int cc = 0; cc < p.C; cc += 32) {
-          short8 bfr[NT];
+  for (int j = 0; j < NT; ++j) bbase[j] = (j * 32 + lr) * p.kpitch + hi * 16;
+
+  float16v acc[MT][NT];
 #pragma unroll
-          for (int j = 0; j < NT; ++j)
-            bfr[j] = *reinterpret_cast<const short8*>(&Fs[(j * 16 + lrow) * p.kpad + kbase + cc + lk]);
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int i = 0; i < MT; ++i) {
-            const short8 af = *reinterpret_cast<const short8*>(&Is[(base[i] + tap) * p.cpad + cc + lk]);
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
-            for (int j = 0; j < NT; ++j) acc[i][j] = mfma16<BF16>(af, bfr[j], acc[i][j]);
-          }
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // Steps run tap by tap, two channel steps per inner iteration (Cin/16 is
+  // even).  Per-lane LDS pointers advance by one uniform delta per iteration:
+  // +64 bytes inside a tap, the tap-to-tap distance at its end, so the loop
+  // carries a handful of scalar ops for its eight reads and MFMAs.
+  //   A: pa = abase + kh*dh*rf_w*pitch + kw*dw*pitch + 32*c
+  //   B: pb = bbase + 32*s (K is contiguous across taps)
+  const int cs = p.C / 16;
+  const int taps = p.KH * p.KW;
+  const int acol = p.dw * p.pitch;
+  const int arow = p.dh * p.rf_w * p.pitch - (p.KW - 1) * acol;  // last tap of a row -> next row
+  int pa[MT], pb[NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) pa[i] = abase[i];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) pb[j] = bbase[j];
+  short8 af[2][MT], bf[2][NT];
+  auto rd = [&](int set, int imm) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af[set][i] = *reinterpret_cast<const short8*>(Is + pa[i] + imm);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) bf[set][j] = *reinterpret_cast<const short8*>(Fs + pb[j] + imm);
+  };
+  auto mma = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[i][j] = mfma32<BF16>(bf[set][j], af[set][i], acc[i][j]);
+  };
+  rd(0, 0);
+  int kw = 0;
+  for (int tap = 0; tap < taps; ++tap) {
+    const bool last = tap + 1 == taps;
+    const bool row_end = ++kw == p.KW;
+    kw = row_end ? 0 : kw;
+    // bytes from this tap's first step to the next tap's; the last tap stays
+    // on its final pair so the trailing reads are in bounds (and unused)
+    const int to_next = last ? (cs - 2) * 32 : row_end ? arow : acol;
+    for (int c = 0; c < cs; c += 2) {
+      rd(1, 32);  // step c+1 of this tap
+      mma(0);
+      const bool in_tap = c + 2 < cs;
+      const int da = in_tap ? 64 : to_next - c * 32;
+      const int db = in_tap || !last ? 64 : 0;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) pa[i] += da;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) pb[j] += db;
+      rd(0, 0);  // step c+2, or the next tap's first
+      mma(1);
+      // Issue order per half (one step of MFMAs): the other set's reads go in
+      // front and between the first MFMAs, the last two MFMAs carry none, so
+      // the reads have two MFMAs of time to land before the next half.
+      constexpr int F = MT * NT, R = MT + NT;
+      constexpr int lead = R - (F - 2) > 1 ? R - (F - 2) : 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        __builtin_amdgcn_sched_group_barrier(0x100, lead < R ? lead : R, 0);
+#pragma unroll
+        for (int g = 0; g < F; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (lead + g < R) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
       }
-    // D layout: lane holds pixel rows 4*(lane/16)+v of the M tile, column lane%16.
+    }
+  }
+
+  // The MFMAs compute D = F x P (A = filter fragment, B = pixel fragment), so
+  // lane l holds pixel l%32 of the tile and register v holds output channel
+  // 8*(v/4) + 4*(l/32) + v%4: four runs of four consecutive channels.  Each
+  // 32x32 tile goes through the wave's own LDS staging rows (pixel-major,
+  // 144-byte pitch) and leaves as four 16-byte stores per lane where eight
+  // consecutive lanes cover one pixel's 128 channel bytes, so every store
+  // instruction writes whole 128-byte lines.  Pixel q of the unit (row q / TW,
+  // column q % TW) starts at q*out_C + (q / TW)*(out_W - TW)*out_C floats from
+  // the unit origin; pixels past the unit and channels past Cout get an
+  // out-of-range offset.
+  const __amdgpu_buffer_rsrc_t ob = buffer_of(t.O, p.unit_out_bytes);
+  const int rowgap = (p.out_W - p.TW) * p.out_C;
+  const int sr = lane >> 3, sc = lane & 7;  // staging read: pixel 8k + sr, 16-byte chunk sc
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      if (mt0 + 4 * i >= nmt) continue;
+  for (int i = 0; i < MT; ++i) {
+    unsigned pix[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int pix = (mt0 + 4 * i) * 16 + (lane >> 4) * 4 + v;
-        if (pix >= M) continue;
-        const int ph = pix / p.TW, pw = pix - (pix / p.TW) * p.TW;
-        float* orow = t.O + ((long long)ph * p.out_W + pw) * p.out_C;
+    for (int k = 0; k < 4; ++k) {
+      const int q = (mt0 + 4 * i) * 32 + 8 * k + sr;
+      pix[k] = q < M ? unsigned(q * p.out_C + (int)udiv(q, p.m_tw) * rowgap) * 4u : kOutOfRange;
+    }
 #pragma unroll
-        for (int j = 0; j < NT; ++j) __builtin_nontemporal_store(acc[i][j][v], &orow[j * 16 + lrow]);
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4v val = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        *reinterpret_cast<float4v*>(Os + lr * kOutPitch + (8 * g + 4 * hi) * 4) = val;
+      }
+      const int co = j * 32 + 4 * sc;
+      const bool cok = co < p.CO;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint4v val = *reinterpret_cast<const uint4v*>(Os + (8 * k + sr) * kOutPitch + sc * 16);
+        __builtin_amdgcn_raw_buffer_store_b128(val, ob, cok && pix[k] != kOutOfRange ? pix[k] + co * 4u : kOutOfRange,
+                                               0, 2);
       }
     }
   }
 }
 
 template <int NT, bool BF16>
-__global__ __launch_bounds__(256, 1) void conv2d_kernel(ConvArgs p) {
-  extern __shared__ __attribute__((aligned(16))) unsigned short lds[];
-  unsigned short* Fs = lds;
-  const int halo_elems = p.rf_h * p.rf_w * p.cpad;
-  unsigned short* Is0 = lds + p.CO * p.kpad;
-  unsigned short* Is1 = Is0 + halo_elems;
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void compute_unit(const ConvArgs& p, const Unit& t, const unsigned char* Fs,
+                                             const unsigned char* Is, unsigned char* Os, int tid) {
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Wave w owns M tiles w, w+4, w+8, ...  Up to CAP of them go through one
+  // call, so the epilogue stores sit in no loop: a loop holding stores makes
+  // the compiler wait for every outstanding load (the next unit's halo) before
+  // entering it.  Larger units loop CAP tiles at a time (tiles past the end
+  // are computed on clamped pixels and not stored).
+  constexpr int CAP = NT >= 4 ? 1 : 2;  // accumulators: CAP * NT * 16 per lane
+  const int cnt = (p.nmt - wave + 3) >> 2;
+  if (cnt == 1) {
+    conv_tiles<1, NT, BF16>(p, t, Fs, Is, Os + wave * 32 * kOutPitch, wave, lane);
+  } else if (CAP >= 2 && cnt == 2) {
+    conv_tiles<CAP, NT, BF16>(p, t, Fs, Is, Os + wave * 32 * kOutPitch, wave, lane);
+  } else if (cnt > CAP) {
+    for (int mt0 = wave; mt0 < p.nmt; mt0 += 4 * CAP) conv_tiles<CAP, NT, BF16>(p, t, Fs, Is, Os + wave * 32 * kOutPitch, mt0, lane);
+  }
+}
 
-  int u = blockIdx.x;  // the host launches at most total_units workgroups
+// Waves 0-3 compute (MFMAs and output stores only); waves 4-7 fetch the next
+// unit's halo into registers and write it to LDS between the unit's two
+// barriers.  Keeping the global loads out of the compute waves keeps their
+// instruction stream free of waits on memory: each wave waits only on its own
+// counters, and a compute wave has no load outstanding while it runs MFMAs.
+template <int NT, bool BF16>
+__global__ __launch_bounds__(WG, 1) void conv2d_kernel(ConvArgs p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  unsigned char* Fs = lds;
+  unsigned char* Is = lds + NT * 32 * p.kpitch;
+  unsigned char* Os = Is + p.halo_bytes;  // 4 compute waves x 32 pixel rows of output staging
+  const int tid = threadIdx.x;
+  const bool loader = __builtin_amdgcn_readfirstlane(tid >> 6) >= 4;
+  const int ltid = tid - (WG - HT);
+
   uint4v hv[HV];
+  int dst[HV];
+  int u = blockIdx.x;  // the host launches at most total_units workgroups
   Unit cur = unit_of(p, u);
-  load_halo(p, cur, tid, hv);  // in flight while the filter is staged
-  {
+  if (loader) {
+    load_halo(p, cur, ltid, hv, dst);
+    store_halo(Is, hv, dst);
+  } else {
     // The filter tile is the whole filter array (checked by the planner), so
     // every Block - and every unit of this workgroup - uses the same origin.
+    // The compute waves stage it while the loaders fetch the first halo.
     int x, y, z;
     decode_block(u / p.units_per_block, p.gx, p.gy, x, y, z);
-    stage_filter(p, p.filt + p.tf.at(x, y, z), Fs, tid);
+    stage_filter(p, p.filt + p.tf.at(x, y, z), Fs, NT * 32, tid);
   }
-  store_halo(p, Is0, tid, hv);
   __syncthreads();
-  int buf = 0;
   for (; u < p.total_units; u += gridDim.x) {
     const int un = u + gridDim.x;
-    Unit next = cur;
-    if (un < p.total_units) {
-      next = unit_of(p, un);
-      load_halo(p, next, tid, hv);
+    const bool more = un < p.total_units;  // uniform across the workgroup
+    if (loader) {
+      if (more) load_halo(p, unit_of(p, un), ltid, hv, dst);
+    } else {
+      compute_unit<NT, BF16>(p, cur, Fs, Is, Os, tid);
     }
-    compute_unit<NT, BF16>(p, cur, Fs, buf ? Is1 : Is0, tid);
-    if (un < p.total_units) store_halo(p, buf ? Is0 : Is1, tid, hv);
-    __syncthreads();
-    buf ^= 1;
-    cur = next;
+    if (more) {
+      __syncthreads();  // every compute wave is done with this halo
+      if (loader) store_halo(Is, hv, dst);
+      __syncthreads();
+      cur = unit_of(p, un);
+    }
   }
 }
 
@@ -276,7 +453,7 @@ hipError_t launch_conv_t(const ConvArgs& a, dim3 grid, size_t lds, hipStream_t s
     if (e != hipSuccess) return e;
     configured.store(static_cast<int>(lds));
   }
-  hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, a);
+  hipLaunchKernelGGL(fn, grid, dim3(WG), lds, s, a);
   return hipGetLastError();
 }
 
@@ -315,12 +492,13 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   a.out_C = (int)c.out_C;
   a.gx = p.grid[0];
   a.gy = p.grid[1];
-  a.cpad = a.C + 8;
+  a.pitch = 2 * a.C + 16;
   const int K = a.KH * a.KW * a.C;
-  a.kpad = K + 8;
-  const int nt = a.CO / 16;
-  if (a.C % 32 || a.CO % 16 || !(nt == 1 || nt == 2 || nt == 4 || nt == 8)) {
-    why = "conv2d kernel needs Cin % 32 == 0 and Cout in {16, 32, 64, 128}";
+  a.kpitch = 2 * K + 16;
+  a.steps = K / 16;
+  const int nt = (a.CO + 31) / 32;
+  if (a.C % 32 || a.CO % 16 || a.CO > 128) {
+    why = "conv2d kernel needs Cin % 32 == 0, Cout % 16 == 0 and Cout <= 128";
     return hipErrorInvalidValue;
   }
   for (const void* ptr : {(const void*)a.src, (const void*)a.filt, (const void*)a.out})
@@ -340,21 +518,23 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   if (e != hipSuccess) return e;
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
-  // Largest work unit (rows dividing TH) whose double-buffered halo fits.
-  const size_t filt_bytes = size_t(a.CO) * a.kpad * 2;
+  // Largest work unit (rows dividing TH) whose halo fits beside the filter.
+  const int ntp = nt == 3 ? 4 : nt;  // N tiles compiled: 1, 2 or 4
+  const size_t filt_bytes = size_t(ntp) * 32 * a.kpitch;
   size_t lds = 0;
   a.UR = 0;
   for (int ur = a.TH; ur >= 1; --ur) {
     if (a.TH % ur) continue;
     const int rf_h = (ur - 1) * a.sh + a.dh * (a.KH - 1) + 1;
     const int rf_w = (a.TW - 1) * a.sw + a.dw * (a.KW - 1) + 1;
-    const int halo_vecs = rf_h * rf_w * (a.C / 8);
-    const size_t need = filt_bytes + 2 * size_t(rf_h) * rf_w * a.cpad * 2;
-    if (halo_vecs <= 256 * HV && need <= size_t(max_lds)) {
+    const long long halo_vecs = (long long)rf_h * rf_w * (a.C / 8);
+    const size_t need = filt_bytes + size_t(rf_h) * rf_w * a.pitch + 4 * 32 * kOutPitch;
+    if (halo_vecs <= HT * HV && need <= size_t(max_lds) && rf_w < 65536 && rf_h < 32767) {
       a.UR = ur;
       a.rf_h = rf_h;
       a.rf_w = rf_w;
-      a.halo_vecs = halo_vecs;
+      a.halo_vecs = static_cast<int>(halo_vecs);
+      a.halo_bytes = rf_h * rf_w * a.pitch;
       lds = need;
       break;
     }
@@ -365,6 +545,19 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
           " filter does not fit the LDS budget; use a narrower tile";
     return hipErrorInvalidValue;
   }
+  a.nmt = (a.UR * a.TW + 31) / 32;
+  a.m_cv = udiv_magic(a.C / 8);
+  a.m_rfw = udiv_magic(a.rf_w);
+  a.m_tw = udiv_magic(a.TW);
+  a.m_cg = udiv_magic(a.CO / 8);
+  const long long image_bytes = (long long)a.H * a.W * a.C * 2;
+  const long long unit_out_bytes = (long long)a.UR * a.out_W * a.out_C * 4;
+  if (image_bytes >= (1LL << 31) || unit_out_bytes >= (1LL << 31)) {
+    why = "conv2d kernel needs one batch entry of the source and one row band of the output below 2 GiB";
+    return hipErrorInvalidValue;
+  }
+  a.image_bytes = static_cast<unsigned>(image_bytes);
+  a.unit_out_bytes = static_cast<unsigned>(unit_out_bytes);
   a.units_per_block = a.TH / a.UR;
   const long long units = (long long)p.grid[0] * p.grid[1] * p.grid[2] * a.units_per_block;
   if (units > 0x7fffffff) {
@@ -376,11 +569,10 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   dim3 grid(nwg);
   const bool bf16 = c.elem == xt::Elem::BF16;
 #define XT_CONV(NTV, BFV) e = launch_conv_t<NTV, BFV>(a, grid, lds, s)
-  switch (nt) {
+  switch (ntp) {
     case 1: if (bf16) XT_CONV(1, true); else XT_CONV(1, false); break;
     case 2: if (bf16) XT_CONV(2, true); else XT_CONV(2, false); break;
-    case 4: if (bf16) XT_CONV(4, true); else XT_CONV(4, false); break;
-    default: if (bf16) XT_CONV(8, true); else XT_CONV(8, false); break;
+    default: if (bf16) XT_CONV(4, true); else XT_CONV(4, false); break;
   }
 #undef XT_CONV
   return e;

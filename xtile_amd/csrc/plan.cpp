@@ -396,8 +396,8 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
     err = "the HIP conv2d kernel needs a batch tile of 1";
     return false;
   }
-  if (c.C % 32 || c.CO % 16 || c.CO > 256) {
-    err = "the HIP conv2d kernel needs Cin % 32 == 0 and Cout % 16 == 0 (Cout <= 256)";
+  if (c.C % 32 || c.CO % 16 || c.CO > 128) {
+    err = "the HIP conv2d kernel needs Cin % 32 == 0 and Cout % 16 == 0 (Cout <= 128)";
     return false;
   }
   const Attr* pad = find_attr(cv->attrs, "pad");

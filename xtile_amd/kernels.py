@@ -146,7 +146,7 @@ def matmul_bf16(m: int, n: int, k: int, tm: int = 256, tn: int = 128):
 
 
 @kernel
-def conv2d_kernel(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw):
+def conv2d_kernel(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw, pt, pl, pb, pr, sh, sw, dh, dw):
     bid_n = bid(0)
     bid_h = bid(1)
     bid_w = bid(2)
@@ -158,23 +158,30 @@ def conv2d_kernel(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw):
         index=(bid_n, bid_h, bid_w, zero),
         shape=(1, tile_h, tile_w, cout),
         group=1,
-        pad=(kh // 2, kw // 2, kh // 2, kw // 2),
-        stride=(1, 1),
-        dilation=(1, 1),
+        pad=(pt, pl, pb, pr),
+        stride=(sh, sw),
+        dilation=(dh, dw),
     )
     store(out, index=(bid_n, bid_h, bid_w, zero), tile=t)
 
 
-def conv2d(n, h, w, cin, cout, kh=3, kw=3, tile_h=4, tile_w=56, dtype=float16):
-    if h % tile_h or w % tile_w:
-        raise ValueError("tile_h / tile_w must divide h / w")
+def conv2d(n, h, w, cin, cout, kh=3, kw=3, tile_h=4, tile_w=56, dtype=float16, pad=None, stride=(1, 1),
+           dilation=(1, 1)):
+    """NHWC conv; `pad` is (top, left, bottom, right), by default "same" for odd
+    filters as in kernels/conv2d.py:29.  The output is (n, oh, ow, cout)."""
+    if pad is None:
+        pad = (kh // 2, kw // 2, kh // 2, kw // 2)
+    oh = (h + pad[0] + pad[2] - dilation[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dilation[1] * (kw - 1) - 1) // stride[1] + 1
+    if oh <= 0 or ow <= 0 or oh % tile_h or ow % tile_w:
+        raise ValueError("tile_h / tile_w must divide the output height / width")
     inp = Array(shape=(n, h, w, cin), dtype=dtype)
     filt = Array(shape=(kh, kw, cin, cout), dtype=dtype)
-    out = Array(shape=(n, h, w, cout), dtype=float32)
+    out = Array(shape=(n, oh, ow, cout), dtype=float32)
     return convert(
         conv2d_kernel,
-        args=(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw),
-        grid=(n, h // tile_h, w // tile_w),
+        args=(inp, filt, out, tile_h, tile_w, cin, cout, kh, kw, *pad, *stride, *dilation),
+        grid=(n, oh // tile_h, ow // tile_w),
         double_buffering=True,
     )
 
