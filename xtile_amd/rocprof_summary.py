@@ -15,6 +15,7 @@ exactly that many bytes).  The scaled bytes are printed as `fetch_bytes` /
 from __future__ import annotations
 
 import argparse
+import json
 import re
 import sqlite3
 import statistics
@@ -50,6 +51,7 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-mib", type=float, default=256.0)
     ap.add_argument("--kernel", default=None, help="regex selecting the kernel of interest")
     ap.add_argument("--command", action="append", default=[], help="command lines to record")
+    ap.add_argument("--bench-log", default=None, help="stdout of the traced bench.py run")
     args = ap.parse_args(argv)
 
     out = []
@@ -73,6 +75,15 @@ def main(argv=None) -> int:
         if sel:
             out.append(f"selected_kernel: {args.kernel}")
             out.append(f"selected_avg_us: {statistics.mean(sel):.3f}")
+            out.append(f"selected_median_us: {statistics.median(sel):.3f}")
+    if args.bench_log:
+        lines = [ln for ln in open(args.bench_log).read().splitlines() if ln.startswith('{"metric"')]
+        if lines:
+            rec = json.loads(lines[-1])
+            out.append(
+                f"bench_us_per_launch_same_run: {rec['ms_per_step'] * 1000.0:.3f}  "
+                f"(bench.py's own HIP-event timing of its {rec['steps']} timed launches)"
+            )
     if args.fetch and args.write:
         fetch = _counter(args.fetch, "FETCH_SIZE", args.kernel)
         write = _counter(args.write, "WRITE_SIZE", args.kernel)
