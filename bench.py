@@ -1,6 +1,6 @@
 """Benchmark of the xtile_amd HIP path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c6]
 
 One step = one launch of the tile program over one batch of synthetic input
 (numpy PCG64, seed = config index, shapes of BASELINE.json's configs).  The
@@ -42,7 +42,7 @@ if str(ROOT) not in sys.path:
 
 METRIC = "GB/s (add, softmax) & TFLOP/s (matmul, conv2d) on 1 MI355X, % of roofline"
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0}
+MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "i8": 5000.0}  # dense; i8 in TOP/s
 ROTATE_BYTES = 1 << 30
 
 
@@ -120,6 +120,23 @@ def make_config(name: str):
             "bound": "mfma",
             "dtype": "bf16",
             "data": "synthetic: numpy PCG64 seed=5, normal(0,0.02) -> bf16 (RNE)",
+        }
+    if name == "c6":
+        rng = np.random.default_rng(6)
+        m = n = k = 4096
+        a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+        b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        s = _f32(rng.uniform(0.5, 2.0, (1, n)) / (np.sqrt(k) * 64))
+        bias = _f32(rng.uniform(-20, 20, (1, n)))
+        return K.CONFIGS["c6_matmul_i8"](), [a, b, np.zeros((m, n), np.int8), s, bias], [
+            "i8", "i8", "i8", "f32", "f32"
+        ], {
+            "workload": "c6_matmul_i8: kernels/matmul.py, C = int8(A @ B * scale + bias), M=N=K=4096, "
+            "i8 in, i32 acc, f32 epilogue, i8 out, 64x64 Block tiles, B/scale/bias shared=1, grid (64,64,1)",
+            "unit": "TOP/s",
+            "bound": "mfma",
+            "dtype": "i8",
+            "data": "synthetic: numpy PCG64 seed=6, A,B uniform int8, scale ~U[0.5,2]/(64 sqrt(K)), bias ~U[-20,20]",
         }
     raise ValueError(f"unknown config {name}")
 
@@ -225,7 +242,8 @@ def measure(name: str, steps: int, warmup: int, cpu_seconds: float, use_graph: b
     else:
         achieved = plan["flops"] / sec / 1e12
         peak = MFMA_PEAK_TFLOPS[meta["dtype"]]
-        roof = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+        roof = {"bound": "mfma", "achieved": achieved, "peak": peak,
+                "unit": "TOP/s" if meta["dtype"] == "i8" else "TFLOP/s",
                 "frac": achieved / peak, "traffic": _traffic(name)}
     if name == "c4":  # report against the MFMA peak as well
         tf = plan["flops"] / sec / 1e12
@@ -265,7 +283,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="all", help="all, or one of c1..c5")
+    ap.add_argument("--config", default="all", help="all, or one of c1..c6")
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument(
@@ -295,7 +313,7 @@ def main(argv=None) -> int:
             file=sys.stderr,
         )
         return 2
-    names = ["c1", "c2", "c3", "c4", "c5"] if args.config == "all" else [args.config]
+    names = ["c1", "c2", "c3", "c4", "c5", "c6"] if args.config == "all" else [args.config]
     headline = "c2" if "c2" in names else names[0]
     results = {n: measure(n, args.steps, args.warmup, args.cpu_seconds, not args.no_graph) for n in names}
     h = results[headline]

@@ -187,3 +187,111 @@ def test_conv2d_filter_too_large_is_refused(cuda):
     o = torch.zeros((1, 10, 14, 80), dtype=torch.float32, device=cuda)
     with pytest.raises(ValueError, match="does not fit the LDS budget"):
         xt.launch(mod, x, f, o)
+
+
+# -- matmul epilogue and i8 (kernels/matmul.py) ---------------------------------
+
+
+def _i8_inputs(rng, m, n, k):
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    # scale so that roughly a fifth of the outputs saturate and the rest spread over i8
+    s = (rng.uniform(0.5, 2.0, (1, n)) / (np.sqrt(k) * 64)).astype(np.float32)
+    bias = rng.uniform(-20, 20, (1, n)).astype(np.float32)
+    return a, b, s, bias
+
+
+@pytest.mark.parametrize(
+    "m_,n_,k_,tm,tn",
+    [(128, 128, 256, 64, 64), (512, 512, 1024, 64, 64), (256, 384, 512, 64, 64), (256, 256, 4096, 64, 64),
+     (192, 128, 128, 64, 64)],
+)
+def test_matmul_i8_epilogue_bit_exact(cuda, m_, n_, k_, tm, tn):
+    """The reference program kernels/matmul.py: i8 x i8 -> f32, * scale + bias,
+    astype(int8).  Exact i32 accumulation, f32 conversion, two f32 roundings and
+    ftoi (half to even, saturating) make the result bit-exact.  K = 4096 pushes
+    |acc| past 2^24, so the int -> f32 rounding is exercised."""
+    rng = np.random.default_rng(6)
+    mod = K.matmul_i8(m_, n_, k_, tm, tn)
+    a, b, s, bias = _i8_inputs(rng, m_, n_, k_)
+    c = np.zeros((m_, n_), np.int8)
+    got = run_gpu(mod, [a, b, c, s, bias], ["i8", "i8", "i8", "f32", "f32"], cuda,
+                  case=f"mm i8 {m_}x{n_}x{k_} tile {tm}x{tn}")[2]
+    want = run_oracle(mod, [a, b, c, s, bias], oracle_threads())[2]
+    assert np.array_equal(got, want)
+    assert 0.05 < np.mean((want == 127) | (want == -128)) < 0.5
+
+
+def _matmul_epilogue_program(m, n, k, dt_in, scale, bias, ftoi):
+    """store([ftoi]((matmul [* s]) [+ b])) with full-K 64x64 Blocks."""
+    from xtile_amd import Array, bid, cdiv, convert, float32, int8, kernel, load, matmul, store, astype
+
+    @kernel
+    def prog(lhs, rhs, res, sc, bi, tm, tn, tk):
+        x = bid(0)
+        y = bid(1)
+        t = matmul(load(lhs, index=(x, 0), shape=(tm, tk)), load(rhs, index=(0, y), shape=(tk, tn), shared=1))
+        if scale:
+            t = t * load(sc, index=(0, y), shape=(1, tn), shared=1)
+        if bias:
+            t = t + load(bi, index=(0, y), shape=(1, tn), shared=1)
+        if ftoi:
+            t = astype(t, dtype=int8)
+        store(res, index=(x, y), tile=t)
+
+    args = (Array(shape=(m, k), dtype=dt_in), Array(shape=(k, n), dtype=dt_in),
+            Array(shape=(m, n), dtype=int8 if ftoi else float32), Array(shape=(1, n), dtype=float32),
+            Array(shape=(1, n), dtype=float32), 64, 64, k)
+    return convert(prog, args=args, grid=(cdiv(m, 64), cdiv(n, 64), 1))
+
+
+@pytest.mark.parametrize(
+    "dt,scale,bias,ftoi",
+    [("i8", False, False, False), ("i8", True, False, False), ("i8", False, True, True),
+     ("f16", True, True, False), ("bf16", True, True, False), ("f16", False, True, True)],
+)
+def test_matmul_epilogue_variants(cuda, dt, scale, bias, ftoi):
+    """Every part of the epilogue is optional; f16/bf16 tiles take it too."""
+    rng = np.random.default_rng(7)
+    m_, n_, k_ = 256, 256, 512
+    dt_in = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}[dt]
+    mod = _matmul_epilogue_program(m_, n_, k_, dt_in, scale, bias, ftoi)
+    if dt == "i8":
+        a, b, s, bi = _i8_inputs(rng, m_, n_, k_)
+    else:
+        a = rng.normal(0, 1, (m_, k_)).astype(np.float32)
+        b = rng.normal(0, 1, (k_, n_)).astype(np.float32)
+        a, b = (f32_to_bf16_bits(a), f32_to_bf16_bits(b)) if dt == "bf16" else (a.astype(np.float16), b.astype(np.float16))
+        s = rng.uniform(0.05, 0.2, (1, n_)).astype(np.float32)
+        bi = rng.uniform(-3, 3, (1, n_)).astype(np.float32)
+    c = np.zeros((m_, n_), np.int8 if ftoi else np.float32)
+    dts = [dt, dt, "i8" if ftoi else "f32", "f32", "f32"]
+    got = run_gpu(mod, [a, b, c, s, bi], dts, cuda, case=f"mm epilogue {dt} s={scale} b={bias} ftoi={ftoi}")[2]
+    want = run_oracle(mod, [a, b, c, s, bi], oracle_threads())[2]
+    if dt == "i8":
+        assert np.array_equal(got, want)  # exact accumulation: bit-exact in every variant
+    elif ftoi:
+        # f32 accumulation order differs from the oracle's double sums: allow
+        # the rare flip at a rounding boundary
+        assert np.mean(got != want) < 1e-3 and np.max(np.abs(got.astype(int) - want.astype(int))) <= 1
+    else:
+        assert frob_rel(got, want) <= MM_FROB
+
+
+def test_reference_traced_matmul_program(cuda):
+    """tests/golden/dsl/matmul_int8_epilogue.mlir is the text the reference's own
+    tracer (xtile/dsl.py) wrote for the kernels/matmul.py program: parsed as-is
+    and run on the GPU, bit-exact against the oracle."""
+    from pathlib import Path
+
+    text = (Path(__file__).parent / "golden" / "dsl" / "matmul_int8_epilogue.mlir").read_text()
+    mod = xt.parse(text)
+    sig = xt.signature(mod)
+    shapes = [tuple(a["shape"]) for a in sig["args"]]
+    assert shapes == [(1024, 256), (256, 512), (1024, 512), (1, 512), (1, 512)]
+    rng = np.random.default_rng(8)
+    a, b, s, bias = _i8_inputs(rng, 1024, 512, 256)
+    c = np.zeros((1024, 512), np.int8)
+    got = run_gpu(mod, [a, b, c, s, bias], ["i8", "i8", "i8", "f32", "f32"], cuda, case="reference-traced matmul")[2]
+    want = run_oracle(mod, [a, b, c, s, bias], oracle_threads())[2]
+    assert np.array_equal(got, want)

@@ -348,3 +348,35 @@ def test_bf16_conversions():
     assert all(lib.xo_f32_to_bf16(float(v)) == b for v, b in zip(x[:500], numpy_bits[:500]))
     back = oracle.bf16_bits_to_f32(numpy_bits)
     assert np.all(np.abs(back - x) <= np.abs(x) * 2.0**-8)
+
+
+def test_oracle_i8_matmul_epilogue_matches_numpy():
+    """kernels/matmul.py: exact integer products, nearest-f32 conversion, f32
+    multiply then f32 add (no fused multiply-add), ftoi half-to-even with
+    saturation; a planted round-half-away rule is caught."""
+    rng = np.random.default_rng(6)
+    m, n, k = 64, 192, 256
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+    s = (rng.uniform(0.5, 2.0, (1, n)) / (np.sqrt(k) * 64)).astype(np.float32)
+    bias = rng.uniform(-20, 20, (1, n)).astype(np.float32)
+    out = run_c(str(K.matmul_i8(m, n, k)), [a, b, np.zeros((m, n), np.int8), s, bias])[2]
+    f = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    y = ((f * s).astype(np.float32) + bias).astype(np.float32)
+    np.testing.assert_array_equal(out, np.clip(np.rint(y), -128, 127).astype(np.int8))
+    half_away = np.clip(np.sign(y) * np.floor(np.abs(y) + 0.5), -128, 127).astype(np.int8)
+    ties = np.abs(y - np.trunc(y)) == 0.5
+    if ties.any():
+        assert not np.array_equal(out, half_away)
+    # ftoi special cases through a single-element program
+    vals = np.array([[0.5, 1.5, 2.5, -0.5, -1.5, 127.4, 127.6, -128.6, 1e9, -1e9, np.nan, -0.0]], np.float32)
+    text = """
+func.func @f(%x: memref<1x12xf32>, %y: memref<1x12xi8>) attributes {xt.grid = array<i32: 1, 1, 1>} {
+  %z = arith.constant 0 : i32
+  %0 = xt.load(%x, %z, %z) : (memref<1x12xf32>, i32, i32) -> tensor<1x12xf32>
+  %1 = xt.ftoi(%0) : tensor<1x12xf32> -> tensor<1x12xi8>
+  xt.store(%1, %y, %z, %z) : (tensor<1x12xi8>, memref<1x12xi8>, i32, i32) -> ()
+  func.return
+}"""
+    got = run_c(text, [vals, np.zeros((1, 12), np.int8)])[1]
+    np.testing.assert_array_equal(got[0], np.array([0, 2, 2, 0, -2, 127, 127, -128, 127, -128, 0, 0], np.int8))

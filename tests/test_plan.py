@@ -55,14 +55,30 @@ def test_unsupported_program_names_its_ops():
         xt.plan(m)
 
 
-def test_epilogue_matmul_is_reported():
+def test_epilogue_matmul_plans():
+    """The reference's own matmul program (traced by the reference DSL):
+    i8 x i8 -> * scale + bias -> astype(int8) maps onto the epilogue GEMM."""
     from tests.golden.dsl_programs import programs
     from xtile_amd import dsl
 
     kernel, args, grid, db = programs(dsl)["matmul_int8_epilogue"]
     m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
-    with pytest.raises(NotImplementedError, match="epilogues are not supported"):
-        xt.plan(m)
+    assert xt.plan(m)["kernel"] == "gemm i8->f32 tile=64x64 k=256 epilogue=scale,bias,ftoi->i8 grid=(16,8,1)"
+
+
+def test_unsupported_matmul_epilogue_is_reported():
+    text = """
+func.func @k(%a: memref<64x64xf16>, %b: memref<64x64xf16>, %c: memref<64x64xf32>) attributes {xt.grid = array<i32: 1, 1, 1>} {
+  %z = arith.constant 0 : i32
+  %0 = xt.load(%a, %z, %z) : (memref<64x64xf16>, i32, i32) -> tensor<64x64xf16>
+  %1 = xt.load(%b, %z, %z) : (memref<64x64xf16>, i32, i32) -> tensor<64x64xf16>
+  %2 = xt.matmul(%0, %1) : tensor<64x64xf16>, tensor<64x64xf16> -> tensor<64x64xf32>
+  %3 = xt.exp(%2) : tensor<64x64xf32> -> tensor<64x64xf32>
+  xt.store(%3, %c, %z, %z) : (tensor<64x64xf32>, memref<64x64xf32>, i32, i32) -> ()
+  func.return
+}"""
+    with pytest.raises(NotImplementedError, match=r"matmul programs must be store\(\[ftoi\]"):
+        xt.plan(xt.parse(text))
 
 
 def test_nova_stages_raise():

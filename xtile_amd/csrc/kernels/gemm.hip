@@ -1,36 +1,43 @@
-// Tile matmul C = A @ B with f16 or bf16 inputs and f32 accumulation on the
-// gfx950 matrix cores.
+// Tile matmul C = epilogue(A @ B) on the gfx950 matrix cores.
 //
-// Semantics: xt.matmul over one Block's tiles, the whole K extent of the
-// tile (kernels/matmul.py:11-16,35; lib/xt/XTOps.cpp:218-253 with the
-// narrow-float extension).
+// Semantics: xt.matmul over one Block's tiles, the whole K extent of the tile
+// (kernels/matmul.py:11-16,35; lib/xt/XTOps.cpp:218-253): f16 x f16 and
+// bf16 x bf16 accumulate in f32 (the narrow-float extension); i8 x i8
+// accumulates exactly in i32 and the result is f32.  The optional epilogue is
+// the one of kernels/matmul.py:15-17: t * scale + bias with (1, TN) row tiles
+// broadcast over the rows (two separately rounded f32 operations, never fused),
+// then astype(int8) = xt.ftoi (round half to even, saturate to [-128, 127],
+// NaN -> 0; the reference fixes no rule, this is the oracle's).
 //
 // Workgroup tiles are decoupled from xt Block tiles.  A Block's TM x TN output
 // tile is split into (TM/BM) x (TN/BN) workgroup tiles when it is larger, and
 // neighbouring Blocks are fused into one workgroup tile when it is smaller and
 // the planner's affine addresses show them to be contiguous (the next Block
-// along one grid axis continues the same A rows / B columns / C tile).  Blocks
-// are independent (README.md:85-89), so both are pure scheduling choices.
+// along one grid axis continues the same A rows / B columns / C tile / scale
+// and bias columns).  Blocks are independent (README.md:85-89), so both are
+// pure scheduling choices.
 //
-// Two kernel families:
-//   gemm256_kernel  BM x BN x BK = 256 x 256 x 64, 4 waves of 128 x 128 using
-//                   v_mfma_f32_32x32x16_{f16,bf16}; one workgroup per CU
-//                   (128 KB of LDS), 256 accumulators per lane in AGPRs.
-//                   Per 16-wide K step a wave reads 8 LDS fragments for 16
-//                   MFMAs, half the LDS bytes per FLOP of a 64 x 64 wave tile.
-//   gemm_kernel     BM, BN in {64, 128} x BK = 64, 4 waves of (BM/2) x (BN/2)
-//                   using v_mfma_f32_16x16x32; for tiles the 256 family cannot
-//                   cover.
-// Common data path:
-//   * A slices (K-contiguous rows) go global -> VGPR -> LDS with 16-byte
-//     accesses.
-//   * B slices are N-contiguous in memory but MFMA wants K-contiguous lanes, so
-//     each thread loads a 4(k) x 8(n) sub-block, transposes it in registers and
-//     writes eight 8-byte K-runs into an N-major LDS tile.
-//   * Both LDS tiles are double buffered: the next slice's global loads are in
-//     flight while the current slice feeds the MFMAs; one barrier per slice.
-//   * LDS rows are padded by 8 elements (16 bytes): every ds_read_b128 of a
-//     fragment and every LDS store above runs at the bank-conflict-free rate.
+// One kernel template for BM x BN in {256 x 256, 128 x 128, 64 x 64}:
+//   * 4 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_{f16,bf16} or
+//     v_mfma_i32_32x32x32_i8.  Every fragment is 16 bytes per lane, so one
+//     K slice is 128 bytes of every row whatever the element type (64 f16/bf16
+//     or 128 i8 values) and the staging below moves bytes.
+//   * A rows (K-contiguous) go global -> VGPR -> LDS as 16-byte vectors.  B is
+//     N-contiguous in memory but the matrix cores want K-contiguous lanes, so
+//     each thread loads an 8(k) x 8(n) block of 16-bit values or a
+//     16(k) x 8(n) block of bytes and transposes it in registers (16-bit
+//     halves, or 4x4 byte transposes with v_perm_b32) into eight N rows.
+//   * LDS tiles are unpadded [rows][128 B] arrays whose 16-byte chunks are
+//     XOR-swizzled (chunk c of row r at c ^ swz(r)): fragment reads and the
+//     transposed B stores both run at the bank-conflict-free rate.
+//   * Two register staging sets keep two K slices in flight; sched_group_barrier
+//     interleaves every MFMA with at most one fragment read, one global load,
+//     one LDS store and two VALU ops.
+//   * For an f32 result a half-wave stores one whole 128-byte line per
+//     accumulator register.  For an i8 result the MFMAs compute
+//     D = B^T-fragment x A-fragment instead, so each lane holds runs of four
+//     consecutive output columns of one row and writes them as one 4-byte
+//     store.
 //   * Workgroups are dispatched round-robin over the 8 XCDs; the linear id is
 //     remapped so that each XCD receives a contiguous run of tiles, and tiles
 //     are ordered in groups of GROUP tile columns so that concurrently resident
@@ -41,56 +48,66 @@
 namespace xtk {
 namespace {
 
-constexpr int BK = 64;
-constexpr int PAD = 8;
-constexpr int LDK = BK + PAD;  // LDS row pitch in 16-bit elements
+constexpr int SLICE = 128;  // bytes of K per LDS row and K slice
+
+enum { kF16 = 0, kBF16 = 1, kI8 = 2 };
 
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef int int16v __attribute__((ext_vector_type(16)));
 
 struct GemmArgs {
-  const unsigned short* a;
-  const unsigned short* b;
-  float* c;
-  TileOff ta, tb, tc;
-  long long lda, ldb, ldc;
-  int K;
-  int vgx, vgy;       // virtual grid (fused axes divided by their factor)
-  int mul[3];         // block id = virtual id * mul (fused axes)
-  int sub_m, sub_n;   // workgroup tiles per (fused) Block along M and N
+  const unsigned char* a;
+  const unsigned char* b;
+  void* c;
+  const float* scale;
+  const float* bias;
+  TileOff ta, tb, tc, ts, tbias;  // element offsets
+  long long lda, ldb, ldc;        // row pitches in elements
+  int nk;                         // K slices
+  int vgx, vgy;                   // virtual grid (fused axes divided by their factor)
+  int mul[3];                     // block id = virtual id * mul (fused axes)
+  int sub_m, sub_n;               // workgroup tiles per (fused) Block along M and N
   int nwg;
   int group;
+  int has_scale, has_bias;
 };
 
-template <bool BF16>
-__device__ __forceinline__ float4v mfma16(short8 a, short8 b, float4v c) {
-  if constexpr (BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+template <int ELEM>
+struct Acc {
+  typedef float16v type;
+};
+template <>
+struct Acc<kI8> {
+  typedef int16v type;
+};
+
+template <int ELEM>
+__device__ __forceinline__ typename Acc<ELEM>::type mfma(uint4v a, uint4v b, typename Acc<ELEM>::type c) {
+  if constexpr (ELEM == kI8)
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(int4v, a), __builtin_bit_cast(int4v, b), c,
+                                                 0, 0, 0);
+  else if constexpr (ELEM == kBF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
-                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c,
+                                                  0, 0, 0);
 }
 
-template <bool BF16>
-__device__ __forceinline__ float16v mfma32(short8 a, short8 b, float16v c) {
-  if constexpr (BF16)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
-                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
-}
-
-// Workgroup -> (tile origin pointers).  Contiguous runs per XCD, then
-// GROUP-wide column groups over the virtual grid.
+// Workgroup -> tile origins.  Contiguous runs per XCD, then GROUP-wide column
+// groups over the virtual grid.
 struct TilePtrs {
-  const unsigned short* A;
-  const unsigned short* B;
-  float* C;
+  const unsigned char* A;
+  const unsigned char* B;
+  long long c_off;  // element offset of the C tile
+  const float* S;
+  const float* Bias;
 };
 
-template <int BM, int BN>
+template <int ELEM, int BM, int BN>
 __device__ __forceinline__ TilePtrs gemm_tile_of(const GemmArgs& p) {
+  constexpr int ES = ELEM == kI8 ? 1 : 2;
   int L = blockIdx.x;
   if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
   const int subs = p.sub_m * p.sub_n;
@@ -110,202 +127,199 @@ __device__ __forceinline__ TilePtrs gemm_tile_of(const GemmArgs& p) {
   const int y = (r / gsize) * p.mul[1];
   const int z = vz * p.mul[2];
   TilePtrs t;
-  t.A = p.a + p.ta.at(x, y, z) + (long long)sm * BM * p.lda;
-  t.B = p.b + p.tb.at(x, y, z) + (long long)sn * BN;
-  t.C = p.c + p.tc.at(x, y, z) + (long long)sm * BM * p.ldc + (long long)sn * BN;
+  t.A = p.a + (p.ta.at(x, y, z) + (long long)sm * BM * p.lda) * ES;
+  t.B = p.b + p.tb.at(x, y, z) * ES + (long long)sn * BN * ES;
+  t.c_off = p.tc.at(x, y, z) + (long long)sm * BM * p.ldc + (long long)sn * BN;
+  t.S = p.scale + p.ts.at(x, y, z) + sn * BN;
+  t.Bias = p.bias + p.tbias.at(x, y, z) + sn * BN;
   return t;
 }
 
-// Global -> VGPR staging of one BK slice (A rows, B 4x8 sub-blocks) and the
-// VGPR -> LDS stores with the B transpose.
-template <int BM, int BN>
-struct Stager {
-  static constexpr int A_VECS = BM * BK / 8 / 256;  // 16-byte vectors per thread
-  static constexpr int B_SUBS = (BK / 4) * (BN / 8);
-  static constexpr int B_ITERS = (B_SUBS + 255) / 256;
-  uint4v ra[A_VECS];
-  uint4v rb[B_ITERS][4];
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
-  __device__ __forceinline__ void load(const unsigned short* A, const unsigned short* B,
-                                       long long lda, long long ldb, int kt, int tid) {
+// 4x4 byte transpose: rows a..d (byte i = column i) -> o[i] = column i
+// (byte j = row j).  v_perm_b32 takes bytes 0-3 from its second and 4-7 from
+// its first source.
+__device__ __forceinline__ void transpose4x4(unsigned a, unsigned b, unsigned c, unsigned d, unsigned (&o)[4]) {
+  const unsigned ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const unsigned ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const unsigned cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);
+  const unsigned cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);
+  o[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);  // a0 b0 c0 d0
+  o[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+}
+
+// Global -> VGPR staging of one K slice and the VGPR -> LDS stores.  B
+// sub-blocks: nb = sb % (BN/8) selects 8 output columns, kb = sb / (BN/8) the
+// 16-byte chunk of K (8 values of 16 bits or 16 bytes).
+template <int ELEM, int BM, int BN>
+struct Stager {
+  static constexpr int AV = BM * 8 / 256;      // 16-byte A vectors per thread
+  static constexpr int NB = BN / 8;            // B column blocks
+  static constexpr int BSUB = 8 * NB;          // B sub-blocks per slice
+  static constexpr int BROWS = ELEM == kI8 ? 16 : 8;
+  static constexpr int KPS = ELEM == kI8 ? SLICE : SLICE / 2;  // K values per slice
+  uint4v ra[AV];
+  uint4v rb[ELEM == kI8 ? 1 : 8];  // 16-bit: 8 rows of 8 values
+  uint2v rb8[ELEM == kI8 ? 16 : 1];  // bytes: 16 rows of 8 values
+
+  // Buffer loads: the descriptors cover the workgroup's A and B panels, each
+  // lane keeps one 32-bit offset, and the per-slice / per-row parts travel as
+  // the uniform scalar offset, so the staging needs no per-row pointers.
+  // lda, ldb in bytes.
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t A, __amdgpu_buffer_rsrc_t B, unsigned lda,
+                                       unsigned ldb, int kt, int tid) {
+    const unsigned va = (unsigned)(tid >> 3) * lda + (tid & 7) * 16;
 #pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
-      const int v = tid + i * 256;
-      const int row = v >> 3, cv = v & 7;
-      ra[i] = *reinterpret_cast<const uint4v*>(A + (long long)row * lda + kt * BK + cv * 8);
-    }
+    for (int i = 0; i < AV; ++i)
+      ra[i] = __builtin_amdgcn_raw_buffer_load_b128(A, va, kt * SLICE + i * 32 * lda, 0);
+    if (BSUB >= 256 || tid < BSUB) {
+      const int nb = (unsigned)tid % NB, kb = (unsigned)tid / NB;
+      if constexpr (ELEM == kI8) {
+        const unsigned vb = (unsigned)(kb * 16) * ldb + nb * 8;
 #pragma unroll
-    for (int it = 0; it < B_ITERS; ++it) {
-      const int sb = tid + it * 256;
-      if (B_SUBS % 256 == 0 || sb < B_SUBS) {
-        const int kb = sb & 15, nb = sb >> 4;
+        for (int i = 0; i < 16; ++i)
+          rb8[i] = __builtin_bit_cast(uint2v, __builtin_amdgcn_raw_buffer_load_b64(B, vb, (kt * KPS + i) * ldb, 0));
+      } else {
+        const unsigned vb = (unsigned)(kb * 8) * ldb + nb * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          rb[it][i] = *reinterpret_cast<const uint4v*>(B + (long long)(kt * BK + kb * 4 + i) * ldb + nb * 8);
+        for (int i = 0; i < 8; ++i) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(B, vb, (kt * KPS + i) * ldb, 0);
       }
     }
   }
 
-  __device__ __forceinline__ void store(unsigned short (*As)[LDK], unsigned short (*Bs)[LDK],
-                                        int tid) const {
+  __device__ __forceinline__ void store(unsigned char (*As)[SLICE], unsigned char (*Bs)[SLICE], int tid) const {
 #pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
+    for (int i = 0; i < AV; ++i) {
       const int v = tid + i * 256;
       const int row = v >> 3, cv = v & 7;
-      *reinterpret_cast<uint4v*>(&As[row][cv * 8]) = ra[i];
+      *reinterpret_cast<uint4v*>(&As[row][(cv ^ swz(row)) * 16]) = ra[i];
     }
+    if (BSUB >= 256 || tid < BSUB) {
+      const int nb = (unsigned)tid % NB, kb = (unsigned)tid / NB;
+      if constexpr (ELEM == kI8) {
+        // rows k = 0..15 of columns n = 0..7 -> column n holds 16 K bytes
+        uint4v col[8];
 #pragma unroll
-    for (int it = 0; it < B_ITERS; ++it) {
-      const int sb = tid + it * 256;
-      if (B_SUBS % 256 == 0 || sb < B_SUBS) {
-        const int kb = sb & 15, nb = sb >> 4;
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            unsigned o[4];
+            transpose4x4(rb8[4 * q][h], rb8[4 * q + 1][h], rb8[4 * q + 2][h], rb8[4 * q + 3][h], o);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) col[4 * h + i][q] = o[i];
+          }
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          const int r = nb * 8 + n;
+          *reinterpret_cast<uint4v*>(&Bs[r][(kb ^ swz(r)) * 16]) = col[n];
+        }
+      } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          // columns n = 2j and 2j+1 of the 4 loaded rows
-          const unsigned int d0 = rb[it][0][j], d1 = rb[it][1][j];
-          const unsigned int d2 = rb[it][2][j], d3 = rb[it][3][j];
-          uint2v even, odd;
-          even.x = (d0 & 0xFFFFu) | (d1 << 16);
-          even.y = (d2 & 0xFFFFu) | (d3 << 16);
-          odd.x = (d0 >> 16) | (d1 & 0xFFFF0000u);
-          odd.y = (d2 >> 16) | (d3 & 0xFFFF0000u);
-          *reinterpret_cast<uint2v*>(&Bs[nb * 8 + 2 * j][kb * 4]) = even;
-          *reinterpret_cast<uint2v*>(&Bs[nb * 8 + 2 * j + 1][kb * 4]) = odd;
+          // columns n = 2j (low halves) and 2j+1 (high halves) of the 8 loaded rows
+          uint4v even, odd;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const unsigned lo = rb[2 * q][j], hi = rb[2 * q + 1][j];
+            even[q] = (lo & 0xFFFFu) | (hi << 16);
+            odd[q] = (lo >> 16) | (hi & 0xFFFF0000u);
+          }
+          const int r0 = nb * 8 + 2 * j, r1 = r0 + 1;
+          *reinterpret_cast<uint4v*>(&Bs[r0][(kb ^ swz(r0)) * 16]) = even;
+          *reinterpret_cast<uint4v*>(&Bs[r1][(kb ^ swz(r1)) * 16]) = odd;
         }
       }
     }
   }
 };
 
-// Stager of the 256 family.  LDS tiles are unpadded [rows][64] arrays whose
-// 16-byte chunks are XOR-swizzled: chunk c of row r lives at c ^ swz(r) with
-// swz(r) = (r ^ r >> 3) & 7.  Eight consecutive rows then spread one chunk
-// index over all eight chunk positions (fragment reads), and rows 8 apart get
-// different positions too (transposed B stores): every access below runs at
-// the bank-conflict-free rate.  B is staged as 8(k) x 8(n) sub-blocks: a
-// half-wave reads 512 contiguous bytes of one B row per instruction.
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// x * s + b as two separately rounded f32 operations.
+__device__ __forceinline__ float scale_bias(float x, float s, float b, bool hs, bool hb) {
+#pragma clang fp contract(off)
+  float t = hs ? x * s : x;
+  return hb ? t + b : t;
+}
 
-struct Stager256 {
-  static constexpr int BM = 256, BN = 256;
-  uint4v ra[BM * BK / 8 / 256];  // 8 row chunks of A
-  uint4v rb[8];                  // one 8(k) x 8(n) sub-block of B
+__device__ __forceinline__ int ftoi_i8(float v) {
+  if (v != v) return 0;
+  const float r = __builtin_rintf(v);  // round half to even
+  return (int)fminf(fmaxf(r, -128.f), 127.f);
+}
 
-  __device__ __forceinline__ void load(const unsigned short* A, const unsigned short* B,
-                                       long long lda, long long ldb, int kt, int tid) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int v = tid + i * 256;
-      const int row = v >> 3, cv = v & 7;
-      ra[i] = *reinterpret_cast<const uint4v*>(A + (long long)row * lda + kt * BK + cv * 8);
-    }
-    const int nb = tid & 31, kb = tid >> 5;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      rb[i] = *reinterpret_cast<const uint4v*>(B + (long long)(kt * BK + kb * 8 + i) * ldb + nb * 8);
-  }
-
-  __device__ __forceinline__ void store(unsigned short (*As)[BK], unsigned short (*Bs)[BK],
-                                        int tid) const {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int v = tid + i * 256;
-      const int row = v >> 3, cv = v & 7;
-      *reinterpret_cast<uint4v*>(&As[row][(cv ^ swz(row)) * 8]) = ra[i];
-    }
-    const int nb = tid & 31, kb = tid >> 5;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // columns n = 2j (low halves) and 2j+1 (high halves) of the 8 loaded rows
-      uint4v even, odd;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const unsigned int lo = rb[2 * q][j], hi = rb[2 * q + 1][j];
-        even[q] = (lo & 0xFFFFu) | (hi << 16);
-        odd[q] = (lo >> 16) | (hi & 0xFFFF0000u);
-      }
-      const int r0 = nb * 8 + 2 * j, r1 = r0 + 1;
-      *reinterpret_cast<uint4v*>(&Bs[r0][(kb ^ swz(r0)) * 8]) = even;
-      *reinterpret_cast<uint4v*>(&Bs[r1][(kb ^ swz(r1)) * 8]) = odd;
-    }
-  }
-};
-
-// --- 256 x 256 family ---------------------------------------------------------
-
-template <bool BF16>
-__global__ __launch_bounds__(256, 1) void gemm256_kernel(GemmArgs p) {
-  constexpr int BM = 256, BN = 256;
-  constexpr int WM = 128, WN = 128;  // 2 x 2 waves
+template <int ELEM, int BM, int BN, bool OUT_I8>
+__global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(GemmArgs p) {
+  constexpr int WM = BM / 2, WN = BN / 2;  // 2 x 2 waves
   constexpr int MI = WM / 32, NI = WN / 32;
-  __shared__ __attribute__((aligned(16))) unsigned short As[2][BM][BK];
-  __shared__ __attribute__((aligned(16))) unsigned short Bs[2][BN][BK];
+  constexpr int KS = SLICE / 32;  // MFMA K steps per slice (32 bytes each: 16 f16 or 32 i8)
+  typedef typename Acc<ELEM>::type acc_t;
+  __shared__ __attribute__((aligned(16))) unsigned char As[2][BM][SLICE];
+  __shared__ __attribute__((aligned(16))) unsigned char Bs[2][BN][SLICE];
 
-  const TilePtrs t = gemm_tile_of<BM, BN>(p);
+  const TilePtrs t = gemm_tile_of<ELEM, BM, BN>(p);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Two register staging sets keep two K slices in flight: slice kt+2 is
-  // requested while slice kt feeds the MFMAs and slice kt+1 (requested one
-  // iteration earlier) is moved to LDS.
-  Stager256 st0, st1;
-  float16v acc[MI][NI];
+  Stager<ELEM, BM, BN> st0, st1;
+  acc_t acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-  const int nk = p.K / BK;  // >= 1
-  st0.load(t.A, t.B, p.lda, p.ldb, 0, tid);
-  st1.load(t.A, t.B, p.lda, p.ldb, min(1, nk - 1), tid);
+  const int nk = p.nk;  // >= 1
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(t.A), (short)0,
+                                                                       (int)0xFFFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(t.B), (short)0,
+                                                                       (int)0xFFFFFFFF, 0x00020000);
+  const unsigned lda = (unsigned)(p.lda * (ELEM == kI8 ? 1 : 2)), ldb = (unsigned)(p.ldb * (ELEM == kI8 ? 1 : 2));
+  st0.load(ra, rb, lda, ldb, 0, tid);
+  st1.load(ra, rb, lda, ldb, min(1, nk - 1), tid);
   st0.store(As[0], Bs[0], tid);
   __syncthreads();
   const int lrow = lane & 31;
-  // Fragments of K step ks+1 are read from LDS while the 16 MFMAs of step ks
-  // run (two register sets), so only the first read of each slice is exposed.
-  short8 af[2][MI], bfr[2][NI];
-  // chunk index of this lane's 8 K values in step ks: 2*ks + lane/32
+  uint4v af[2][MI], bfr[2][NI];
+  // 16-byte chunk of this lane's K values in step ks: 2*ks + lane/32
   auto read_frags = [&](int buf, int ks, int set) {
     const int c = ks * 2 + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const int r = wm * WM + i * 32 + lrow;
-      af[set][i] = *reinterpret_cast<const short8*>(&As[buf][r][(c ^ swz(r)) * 8]);
+      af[set][i] = *reinterpret_cast<const uint4v*>(&As[buf][r][(c ^ swz(r)) * 16]);
     }
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       const int r = wn * WN + j * 32 + lrow;
-      bfr[set][j] = *reinterpret_cast<const short8*>(&Bs[buf][r][(c ^ swz(r)) * 8]);
+      bfr[set][j] = *reinterpret_cast<const uint4v*>(&Bs[buf][r][(c ^ swz(r)) * 16]);
     }
   };
   // One K slice: compute from LDS[cur], request slice kt+2 into `next2`, move
   // slice kt+1 from `next1` into LDS[cur^1].  Branch-free: slice indices are
   // clamped to the last slice, whose repeated copies land in the idle buffer.
-  auto slice = [&](int kt, Stager256& next2, const Stager256& next1) {
+  auto slice = [&](int kt, Stager<ELEM, BM, BN>& next2, const Stager<ELEM, BM, BN>& next1) {
     const int cur = kt & 1;
     read_frags(cur, 0, 0);
-    next2.load(t.A, t.B, p.lda, p.ldb, min(kt + 2, nk - 1), tid);
+    next2.load(ra, rb, lda, ldb, min(kt + 2, nk - 1), tid);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      if (ks + 1 < BK / 16) read_frags(cur, ks + 1, (ks + 1) & 1);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read_frags(cur, ks + 1, (ks + 1) & 1);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          acc[i][j] = mfma32<BF16>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
+          acc[i][j] = OUT_I8 ? mfma<ELEM>(bfr[ks & 1][j], af[ks & 1][i], acc[i][j])
+                             : mfma<ELEM>(af[ks & 1][i], bfr[ks & 1][j], acc[i][j]);
     }
     next1.store(As[cur ^ 1], Bs[cur ^ 1], tid);
-    // Issue order for the slice: the first 8 fragment reads, then every MFMA
-    // followed by at most one fragment read, one global load, one LDS store
-    // and two VALU ops, so the global loads, the B transposes and the LDS
-    // stores of the next slices issue while the MFMA pipe stays busy.
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, MI + NI, 0);
 #pragma unroll
-    for (int g = 0; g < MI * NI * (BK / 16); ++g) {
+    for (int g = 0; g < MI * NI * KS; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
@@ -321,77 +335,49 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(GemmArgs p) {
   }
   if (kt < nk) slice(kt, st0, st1);
 
-  // D layout of a 32x32 f32 MFMA tile: lane l, register v holds
-  // row 8*(v/4) + 4*(l/32) + v%4, column l%32.
-  const int orow = (lane >> 5) * 4;
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
+  const bool hs = p.has_scale, hb = p.has_bias;
+  if constexpr (OUT_I8) {
+    // D = B^T x A per 32x32 tile: lane l holds output row m = l%32 of tile i
+    // and register v output column 8*(v/4) + 4*(l/32) + v%4 of tile j, so four
+    // consecutive columns pack into one 4-byte store.
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v)
-        t.C[(long long)(wm * WM + i * 32 + (v >> 2) * 8 + orow + (v & 3)) * p.ldc + wn * WN + j * 32 +
-            lrow] = acc[i][j][v];
-}
-
-// --- 64/128 family --------------------------------------------------------------
-
-template <int BM, int BN, bool BF16>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
-  constexpr int WM = BM / 2, WN = BN / 2;   // 2 x 2 waves
-  constexpr int MI = WM / 16, NI = WN / 16; // 16x16 MFMA tiles per wave
-  __shared__ __attribute__((aligned(16))) unsigned short As[2][BM][LDK];
-  __shared__ __attribute__((aligned(16))) unsigned short Bs[2][BN][LDK];
-
-  const TilePtrs t = gemm_tile_of<BM, BN>(p);
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  Stager<BM, BN> st;
-  float4v acc[MI][NI];
+      for (int g = 0; g < 4; ++g) {
+        const int n0 = wn * WN + j * 32 + 8 * g + 4 * (lane >> 5);
+        float4v sv = {1.f, 1.f, 1.f, 1.f}, bv = {0.f, 0.f, 0.f, 0.f};
+        if (hs) sv = *reinterpret_cast<const float4v*>(t.S + n0);
+        if (hb) bv = *reinterpret_cast<const float4v*>(t.Bias + n0);
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MI; ++i) {
+          const long long off = t.c_off + (long long)(wm * WM + i * 32 + lrow) * p.ldc + n0;
+          unsigned packed = 0;
 #pragma unroll
-    for (int j = 0; j < NI; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
-
-  const int nk = p.K / BK;
-  st.load(t.A, t.B, p.lda, p.ldb, 0, tid);
-  st.store(As[0], Bs[0], tid);
-  __syncthreads();
-  const int lrow = lane & 15;
-  const int lk = (lane >> 4) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) st.load(t.A, t.B, p.lda, p.ldb, kt + 1, tid);
+          for (int e = 0; e < 4; ++e) {
+            const float y = scale_bias((float)acc[i][j][4 * g + e], sv[e], bv[e], hs, hb);
+            packed |= (unsigned)(ftoi_i8(y) & 0xff) << (8 * e);
+          }
+          *reinterpret_cast<unsigned*>(static_cast<signed char*>(p.c) + off) = packed;
+        }
+      }
+  } else {
+    // D = A x B per 32x32 tile: lane l holds output column l%32 of tile j and
+    // register v row 8*(v/4) + 4*(l/32) + v%4 of tile i; a half-wave writes one
+    // whole 128-byte line per register.
+    const int orow = (lane >> 5) * 4;
 #pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      short8 af[MI], bfr[NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-        af[i] = *reinterpret_cast<const short8*>(&As[cur][wm * WM + i * 16 + lrow][ks * 32 + lk]);
-#pragma unroll
-      for (int j = 0; j < NI; ++j)
-        bfr[j] = *reinterpret_cast<const short8*>(&Bs[cur][wn * WN + j * 16 + lrow][ks * 32 + lk]);
+    for (int j = 0; j < NI; ++j) {
+      const int n = wn * WN + j * 32 + lrow;
+      const float sv = hs ? t.S[n] : 1.f, bv = hb ? t.Bias[n] : 0.f;
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = mfma16<BF16>(af[i], bfr[j], acc[i][j]);
+        for (int v = 0; v < 16; ++v) {
+          const long long off = t.c_off + (long long)(wm * WM + i * 32 + (v >> 2) * 8 + orow + (v & 3)) * p.ldc + n;
+          static_cast<float*>(p.c)[off] = scale_bias((float)acc[i][j][v], sv, bv, hs, hb);
+        }
     }
-    if (kt + 1 < nk) st.store(As[cur ^ 1], Bs[cur ^ 1], tid);
-    __syncthreads();
   }
-
-  // D layout of a 16x16 f32 MFMA tile: lane l holds rows 4*(l/16)+v, column l%16.
-  const int orow = (lane >> 4) * 4;
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        t.C[(long long)(wm * WM + i * 16 + orow + v) * p.ldc + wn * WN + j * 16 + lrow] = acc[i][j][v];
 }
 
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
@@ -426,13 +412,18 @@ Cover cover_dim(const xt::Plan& p, long long w, bool is_m) {
   const int f = static_cast<int>(w / t);
   for (int ax = 0; ax < 3; ++ax) {
     if (p.grid[ax] % f) continue;
+    // the epilogue rows follow B's columns
+    const bool rows_fixed = (!p.gemm_scale || axis_step(p.scale.addr, ax) == 0) &&
+                            (!p.gemm_bias || axis_step(p.bias.addr, ax) == 0);
+    const bool rows_follow = (!p.gemm_scale || axis_step(p.scale.addr, ax) == t) &&
+                             (!p.gemm_bias || axis_step(p.bias.addr, ax) == t);
     bool contiguous;
     if (is_m)
       contiguous = axis_step(p.c.addr, ax) == t * p.c.ld && axis_step(p.a.addr, ax) == t * p.a.ld &&
-                   axis_step(p.b.addr, ax) == 0;
+                   axis_step(p.b.addr, ax) == 0 && rows_fixed;
     else
       contiguous = axis_step(p.c.addr, ax) == t && axis_step(p.b.addr, ax) == t &&
-                   axis_step(p.a.addr, ax) == 0;
+                   axis_step(p.a.addr, ax) == 0 && rows_follow;
     if (contiguous) {
       c.ok = true;
       c.axis = ax;
@@ -443,42 +434,84 @@ Cover cover_dim(const xt::Plan& p, long long w, bool is_m) {
   return c;
 }
 
+template <int ELEM, bool OUT_I8>
+void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
+  const dim3 grid(a.nwg), block(256);
+  if (bm == 256) hipLaunchKernelGGL((gemm_kernel<ELEM, 256, 256, OUT_I8>), grid, block, 0, s, a);
+  else if (bm == 128) hipLaunchKernelGGL((gemm_kernel<ELEM, 128, 128, OUT_I8>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((gemm_kernel<ELEM, 64, 64, OUT_I8>), grid, block, 0, s, a);
+}
+
 }  // namespace
 
 hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why) {
+  const bool i8 = p.a.elem == xt::Elem::I8;
+  const long long es = i8 ? 1 : 2;
   GemmArgs a;
-  a.a = static_cast<const unsigned short*>(bufs[p.a.arg]);
-  a.b = static_cast<const unsigned short*>(bufs[p.b.arg]);
-  a.c = static_cast<float*>(bufs[p.c.arg]);
+  a.a = static_cast<const unsigned char*>(bufs[p.a.arg]);
+  a.b = static_cast<const unsigned char*>(bufs[p.b.arg]);
+  a.c = bufs[p.c.arg];
+  a.scale = p.gemm_scale ? static_cast<const float*>(bufs[p.scale.arg]) : nullptr;
+  a.bias = p.gemm_bias ? static_cast<const float*>(bufs[p.bias.arg]) : nullptr;
+  a.has_scale = p.gemm_scale;
+  a.has_bias = p.gemm_bias;
   a.ta = to_off(p.a.addr);
   a.tb = to_off(p.b.addr);
   a.tc = to_off(p.c.addr);
+  a.ts = p.gemm_scale ? to_off(p.scale.addr) : TileOff{0, 0, 0, 0};
+  a.tbias = p.gemm_bias ? to_off(p.bias.addr) : TileOff{0, 0, 0, 0};
   a.lda = p.a.ld;
   a.ldb = p.b.ld;
   a.ldc = p.c.ld;
-  a.K = static_cast<int>(p.gemm_k);
+  const long long kbytes = p.gemm_k * es;
   const long long TM = p.a.rows, TN = p.b.cols;
-  if (a.K % BK || TM % 64 || TN % 64) {
-    why = "matmul tile must have M, N, K multiples of 64";
+  if (kbytes % SLICE || TM % 64 || TN % 64) {
+    why = i8 ? "i8 matmul tile must have M, N multiples of 64 and K a multiple of 128"
+             : "matmul tile must have M, N, K multiples of 64";
     return hipErrorInvalidValue;
   }
+  a.nk = static_cast<int>(kbytes / SLICE);
   for (const void* ptr : {bufs[p.a.arg], bufs[p.b.arg], bufs[p.c.arg]})
     if (reinterpret_cast<uintptr_t>(ptr) % 16) {
       why = "matmul buffers must be 16-byte aligned";
       return hipErrorInvalidValue;
     }
-  if (a.lda % 8 || a.ldb % 8 || !offs_multiple(p.a.addr, 8) || !offs_multiple(p.b.addr, 8)) {
+  if ((a.lda * es) % 16 || (a.ldb * es) % 16 || !offs_multiple(p.a.addr, 16 / es) ||
+      !offs_multiple(p.b.addr, 16 / es)) {
     why = "matmul input tiles must start on 16-byte boundaries";
     return hipErrorInvalidValue;
   }
-  // Prefer 256 x 256 workgroup tiles when the Blocks can be split or fused into them.
-  int bm = 256, bn = 256;
-  Cover cm = cover_dim(p, 256, true), cn = cover_dim(p, 256, false);
-  if (!cm.ok || !cn.ok || (cm.axis >= 0 && cm.axis == cn.axis)) {
-    bm = TM % 128 == 0 ? 128 : 64;
-    bn = TN % 128 == 0 ? 128 : 64;
-    cm = cover_dim(p, bm, true);
-    cn = cover_dim(p, bn, false);
+  // the staging addresses each workgroup's A and B panels with 32-bit offsets
+  if (TM * a.lda * es >= (1LL << 32) || p.gemm_k * a.ldb * es >= (1LL << 32)) {
+    why = "matmul A and B tile panels must each span less than 4 GiB";
+    return hipErrorInvalidValue;
+  }
+  if (p.c.ld % 4 || !offs_multiple(p.c.addr, 4)) {
+    why = "matmul output tiles must start on 4-element boundaries";
+    return hipErrorInvalidValue;
+  }
+  for (int e = 0; e < 2; ++e) {
+    const bool on = e == 0 ? p.gemm_scale : p.gemm_bias;
+    const xt::Access2D& v = e == 0 ? p.scale : p.bias;
+    if (on && (reinterpret_cast<uintptr_t>(bufs[v.arg]) % 16 || !offs_multiple(v.addr, 4))) {
+      why = "matmul scale / bias tiles must start on 16-byte boundaries";
+      return hipErrorInvalidValue;
+    }
+  }
+  // Largest square workgroup tile the Blocks can be split or fused into.
+  int bm = 0;
+  Cover cm, cn;
+  for (int w : {256, 128, 64}) {
+    cm = cover_dim(p, w, true);
+    cn = cover_dim(p, w, false);
+    if (cm.ok && cn.ok && !(cm.axis >= 0 && cm.axis == cn.axis)) {
+      bm = w;
+      break;
+    }
+  }
+  if (bm == 0) {
+    why = "matmul Blocks cannot be mapped onto 64x64 workgroup tiles";
+    return hipErrorInvalidValue;
   }
   a.mul[0] = a.mul[1] = a.mul[2] = 1;
   int vg[3] = {p.grid[0], p.grid[1], p.grid[2]};
@@ -501,22 +534,12 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   }
   a.nwg = static_cast<int>(nwg);
   a.group = 8;
-  const bool bf16 = p.a.elem == xt::Elem::BF16;
-  dim3 grid(a.nwg), block(256);
-#define XT_GEMM(BMV, BNV, BFV) hipLaunchKernelGGL((gemm_kernel<BMV, BNV, BFV>), grid, block, 0, s, a)
-  if (bm == 256) {
-    if (bf16) hipLaunchKernelGGL((gemm256_kernel<true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((gemm256_kernel<false>), grid, block, 0, s, a);
-  } else if (bm == 128 && bn == 128) {
-    if (bf16) XT_GEMM(128, 128, true); else XT_GEMM(128, 128, false);
-  } else if (bm == 128) {
-    if (bf16) XT_GEMM(128, 64, true); else XT_GEMM(128, 64, false);
-  } else if (bn == 128) {
-    if (bf16) XT_GEMM(64, 128, true); else XT_GEMM(64, 128, false);
-  } else {
-    if (bf16) XT_GEMM(64, 64, true); else XT_GEMM(64, 64, false);
+  const bool out_i8 = p.c.elem == xt::Elem::I8;
+  switch (p.a.elem) {
+    case xt::Elem::I8: out_i8 ? launch_t<kI8, true>(bm, a, s) : launch_t<kI8, false>(bm, a, s); break;
+    case xt::Elem::BF16: out_i8 ? launch_t<kBF16, true>(bm, a, s) : launch_t<kBF16, false>(bm, a, s); break;
+    default: out_i8 ? launch_t<kF16, true>(bm, a, s) : launch_t<kF16, false>(bm, a, s); break;
   }
-#undef XT_GEMM
   return hipGetLastError();
 }
 

@@ -6,8 +6,8 @@
 //   RowSoftmax load -> reduce_max -> sub -> exp -> reduce_sum -> reciprocal
 //              -> mul -> store, reductions over axis 1
 //              (kernels/softmax.py:10-19; test/python/dsl_convert.py:25-40)
-//   Gemm       store(matmul(load A, load B))         f16/bf16 in, f32 out
-//              (kernels/matmul.py:6-16 without its epilogue)
+//   Gemm       store([ftoi]((matmul(load A, load B) [* load S]) [+ load Bias]))
+//              f16/bf16/i8 in, f32 or i8 out (kernels/matmul.py:6-19)
 //   Conv2d     store(load_conv2d(S, load F))         f16/bf16 in, f32 out
 //              (kernels/conv2d.py:10-37; conv slice math lib/xt/XTToNova.cpp:110-142)
 #include "plan.h"
@@ -282,17 +282,54 @@ bool match_softmax(const Analysis& an, Plan& p, std::string& err) {
 
 // -- Gemm ----------------------------------------------------------------------
 
+// store([ftoi](([matmul * load S] | matmul) [+ load Bias])): the epilogue of
+// kernels/matmul.py:15-17, every part optional.  Scale and bias are (1, TN)
+// f32 row tiles broadcast over the rows (xtile/dsl.py:658-679,754-759).
+bool epilogue_row(const Analysis& an, const Op* bin, const Type& tile, Access2D& acc, std::string& err) {
+  const Op* ld = def_of(an, bin->operands[1]);
+  if (!ld || ld->name != "xt.load") {
+    err = "matmul epilogue operands must be loaded (1, N) f32 tiles";
+    return false;
+  }
+  const Type& t = an.f.type_of(ld->results[0]);
+  if (t.elem != Elem::F32 || t.rank() != 2 || t.shape[0] != 1 || t.shape[1] != tile.shape[1]) {
+    err = "matmul epilogue operands must be (1, N) f32 tiles matching the result columns";
+    return false;
+  }
+  return access_of(an, *ld, acc, err);
+}
+
 bool match_gemm(const Analysis& an, Plan& p, std::string& err) {
   int nmm, nst;
   const Op* mm = only(an, "xt.matmul", nmm);
   const Op* st = only(an, "xt.store", nst);
-  if (nmm != 1 || nst != 1 || count_ops(an) != 4) {
-    if (nmm >= 1)
-      err = "matmul programs must be store(matmul(load, load)); epilogues are not supported yet";
+  if (nmm != 1 || nst != 1) {
+    if (nmm >= 1) err = "matmul programs must hold one matmul and one store";
     return false;
   }
-  if (st->operands[0] != mm->results[0]) {
-    err = "matmul programs must store the matmul result";
+  const Type& tc = an.f.type_of(mm->results[0]);
+  p.gemm_scale = p.gemm_bias = p.gemm_ftoi = false;
+  int expected = 4;
+  const Op* o = def_of(an, st->operands[0]);
+  if (o && o->name == "xt.ftoi") {
+    p.gemm_ftoi = true;
+    ++expected;
+    o = def_of(an, o->operands[0]);
+  }
+  if (o && o->name == "xt.add" && o != mm) {
+    if (!epilogue_row(an, o, tc, p.bias, err)) return false;
+    p.gemm_bias = true;
+    expected += 2;
+    o = def_of(an, o->operands[0]);
+  }
+  if (o && o->name == "xt.mul" && o != mm) {
+    if (!epilogue_row(an, o, tc, p.scale, err)) return false;
+    p.gemm_scale = true;
+    expected += 2;
+    o = def_of(an, o->operands[0]);
+  }
+  if (o != mm || count_ops(an) != expected) {
+    err = "matmul programs must be store([ftoi]((matmul [* scale]) [+ bias])) with loaded operands";
     return false;
   }
   const Op* la = def_of(an, mm->operands[0]);
@@ -303,21 +340,26 @@ bool match_gemm(const Analysis& an, Plan& p, std::string& err) {
   }
   const Type& ta = an.f.type_of(la->results[0]);
   const Type& tb = an.f.type_of(lb->results[0]);
-  const Type& tc = an.f.type_of(mm->results[0]);
-  if (!((ta.elem == Elem::F16 || ta.elem == Elem::BF16) && tb.elem == ta.elem &&
+  if (!((ta.elem == Elem::F16 || ta.elem == Elem::BF16 || ta.elem == Elem::I8) && tb.elem == ta.elem &&
         tc.elem == Elem::F32)) {
-    err = "the HIP matmul kernel takes f16 x f16 or bf16 x bf16 tiles with an f32 result";
+    err = "the HIP matmul kernel takes f16 x f16, bf16 x bf16 or i8 x i8 tiles with an f32 result";
     return false;
   }
   if (!access_of(an, *la, p.a, err) || !access_of(an, *lb, p.b, err) ||
       !access_of(an, *st, p.c, err))
     return false;
-  int64_t M = ta.shape[0], K = ta.shape[1], N = tb.shape[1];
-  if (M % 64 || N % 64 || K % 64) {
-    err = "the HIP matmul kernel needs tile M, N and K to be multiples of 64";
+  if (p.c.elem != (p.gemm_ftoi ? Elem::I8 : Elem::F32)) {
+    err = "matmul result must be stored as f32, or as i8 after astype(int8)";
     return false;
   }
-  if (p.a.ld % 8 || p.b.ld % 8 || p.c.ld % 4) {
+  const bool i8 = ta.elem == Elem::I8;
+  int64_t M = ta.shape[0], K = ta.shape[1], N = tb.shape[1];
+  if (M % 64 || N % 64 || K % (i8 ? 128 : 64)) {
+    err = i8 ? "the HIP i8 matmul kernel needs tile M, N multiples of 64 and K a multiple of 128"
+             : "the HIP matmul kernel needs tile M, N and K to be multiples of 64";
+    return false;
+  }
+  if (p.a.ld % (i8 ? 16 : 8) || p.b.ld % (i8 ? 16 : 8) || p.c.ld % 4) {
     err = "the HIP matmul kernel needs 16-byte aligned rows";
     return false;
   }
@@ -327,7 +369,10 @@ bool match_gemm(const Analysis& an, Plan& p, std::string& err) {
   p.algo_flops = blocks * 2.0 * double(M) * double(N) * double(K);
   // minimum HBM traffic: each argument once
   double bytes = 0;
-  for (int arg : {p.a.arg, p.b.arg, p.c.arg}) {
+  std::vector<int> args = {p.a.arg, p.b.arg, p.c.arg};
+  if (p.gemm_scale) args.push_back(p.scale.arg);
+  if (p.gemm_bias) args.push_back(p.bias.arg);
+  for (int arg : args) {
     const Type& t = an.f.type_of(an.f.args[arg]);
     bytes += double(t.numel()) * elem_bytes(t.elem);
   }
@@ -477,6 +522,13 @@ std::string Plan::describe() const {
     case PlanKind::Gemm:
       os << "gemm " << elem_name(a.elem) << "->f32 tile=" << a.rows << "x" << b.cols
          << " k=" << gemm_k;
+      if (gemm_scale || gemm_bias || gemm_ftoi) {
+        os << " epilogue=";
+        const char* sep = "";
+        if (gemm_scale) os << sep << "scale", sep = ",";
+        if (gemm_bias) os << sep << "bias", sep = ",";
+        if (gemm_ftoi) os << sep << "ftoi->i8";
+      }
       break;
     case PlanKind::Conv2d:
       os << "conv2d_nhwc " << elem_name(conv.elem) << "->f32 tile=" << conv.TB << "x" << conv.TH

@@ -65,6 +65,10 @@ struct Plan {
   Access2D a, b, c;
   EwOp ew_op = EwOp::Add;
   int64_t gemm_k = 0;
+  // Gemm epilogue (kernels/matmul.py:15-17): t * scale + bias with (1, TN)
+  // row tiles, then an optional ftoi (the store's element type is then i8).
+  bool gemm_scale = false, gemm_bias = false, gemm_ftoi = false;
+  Access2D scale, bias;
   ConvPlan conv;
   double algo_bytes = 0;  // algorithmic HBM bytes per launch
   double algo_flops = 0;  // algorithmic FLOPs per launch

@@ -2,7 +2,7 @@
 
 Each builder returns a parsed Module for one configuration.  They reproduce
 the reference programs (kernels/add.py:6-30, kernels/softmax.py:10-36,
-kernels/matmul.py:6-38 without the int8 epilogue, kernels/conv2d.py:10-59) with
+kernels/matmul.py:6-38, kernels/conv2d.py:10-59) with
 the tile sizes of the five benchmark configurations:
 
   C1 add      fp32 1024x1024, 32x64 tiles, grid (32, 16, 1)
@@ -17,6 +17,7 @@ from __future__ import annotations
 
 from . import (
     Array,
+    astype,
     bfloat16,
     bid,
     cdiv,
@@ -24,6 +25,7 @@ from . import (
     exp,
     float16,
     float32,
+    int8,
     kernel,
     load,
     load_conv2d,
@@ -142,6 +144,37 @@ def matmul_bf16(m: int, n: int, k: int, tm: int = 256, tn: int = 128):
     )
 
 
+@kernel
+def matmul_i8_kernel(lhs, rhs, res, scale, bias, tm, tn, tk):
+    """kernels/matmul.py:6-19: i8 x i8 -> f32, then * scale + bias per column
+    and astype(int8); B, scale and bias are shared along axis 0."""
+    bid_x = bid(0)
+    bid_y = bid(1)
+    lhs_tile = load(lhs, index=(bid_x, 0), shape=(tm, tk))
+    rhs_tile = load(rhs, index=(0, bid_y), shape=(tk, tn), shared=1)
+    s_tile = load(scale, index=(0, bid_y), shape=(1, tn), shared=1)
+    b_tile = load(bias, index=(0, bid_y), shape=(1, tn), shared=1)
+    t = matmul(lhs_tile, rhs_tile)
+    t = t * s_tile + b_tile
+    t = astype(t, dtype=int8)
+    store(res, index=(bid_x, bid_y), tile=t)
+
+
+def matmul_i8(m: int, n: int, k: int, tm: int = 64, tn: int = 64):
+    """The reference's matmul program (kernels/matmul.py:22-38, 64 x 64 tiles)."""
+    a = Array(shape=(m, k), dtype=int8)
+    b = Array(shape=(k, n), dtype=int8)
+    c = Array(shape=(m, n), dtype=int8)
+    s = Array(shape=(1, n), dtype=float32)
+    bias = Array(shape=(1, n), dtype=float32)
+    return convert(
+        matmul_i8_kernel,
+        args=(a, b, c, s, bias, tm, tn, k),
+        grid=(cdiv(m, tm), cdiv(n, tn), 1),
+        double_buffering=True,
+    )
+
+
 # -- conv2d ------------------------------------------------------------------
 
 
@@ -192,4 +225,5 @@ CONFIGS = {
     "c3_matmul_f16": lambda: matmul_f16(4096, 4096, 4096, 128, 128),
     "c4_conv2d_f16": lambda: conv2d(32, 56, 56, 64, 64, 3, 3, 4, 56),
     "c5_matmul_bf16": lambda: matmul_bf16(4096, 11008, 4096, 256, 128),
+    "c6_matmul_i8": lambda: matmul_i8(4096, 4096, 4096, 64, 64),
 }
