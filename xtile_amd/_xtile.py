@@ -82,7 +82,7 @@ def _load() -> ctypes.CDLL:
     path = os.environ.get("XTILE_AMD_LIB", str(_LIB_PATH))
     if not os.path.exists(path):
         raise ImportError(
-            f"{path} is not built; run `python -m xtile_amd.build` (or __graft_entry__.build())"
+            f"{path} is not built; run `python xtile_amd/build.py` (or __graft_entry__.build())"
         )
     # One HIP runtime per process.  PyTorch-ROCm ships its own libamdhip64 /
     # libhsa-runtime64 (loaded under file names without the .7 / .1 suffix but

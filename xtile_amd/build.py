@@ -5,7 +5,8 @@ Produces, under ``xtile_amd/lib/``:
     verifier, passes, launch planner and the gfx950 HIP kernels;
   * ``xt-opt``          - the command-line driver (host code only).
 
-Usage: ``python -m xtile_amd.build`` (or ``__graft_entry__.build()``).
+Usage: ``python xtile_amd/build.py`` (or ``__graft_entry__.build()``); it runs
+without importing the package, whose __init__ needs the library it builds.
 Every call recompiles everything.
 """
 
