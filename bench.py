@@ -165,7 +165,7 @@ def gpu_time(module, host, dtypes, steps: int, warmup: int, use_graph: bool):
 
     dev = torch.device("cuda:0")
     set_bytes = sum(h.nbytes for h in host)
-    nsets = max(1, min(16, math.ceil(ROTATE_BYTES / set_bytes)))
+    nsets = max(1, min(128, math.ceil(ROTATE_BYTES / set_bytes)))
     first = [to_device(h, d, dev) for h, d in zip(host, dtypes)]
     sets = [first] + [[t.clone() for t in first] for _ in range(nsets - 1)]
     torch.cuda.synchronize()

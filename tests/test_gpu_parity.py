@@ -27,7 +27,8 @@ MM_FROB = 1e-3
 
 @pytest.mark.parametrize(
     "rows,cols,th,tw",
-    [(1024, 1024, 32, 64), (64, 128, 32, 64), (96, 40, 32, 8), (33, 7, 11, 7), (1, 4, 1, 4)],
+    [(1024, 1024, 32, 64), (64, 128, 32, 64), (96, 40, 32, 8), (33, 7, 11, 7), (1, 4, 1, 4),
+     (128, 96, 64, 96), (256, 384, 64, 24), (64, 2048, 64, 2048)],
 )
 def test_add_bit_exact(cuda, rows, cols, th, tw):
     rng = np.random.default_rng(1)
@@ -76,7 +77,8 @@ func.func @k(%a: memref<64x96xf32>, %b: memref<64x96xf32>, %c: memref<64x96xf32>
 
 @pytest.mark.parametrize(
     "rows,cols,trow",
-    [(8192, 4096, 1), (128, 64, 64), (64, 4096, 2), (16, 1000, 4), (24, 8192, 1), (5, 3, 5)],
+    [(8192, 4096, 1), (128, 64, 64), (64, 4096, 2), (16, 1000, 4), (24, 8192, 1), (5, 3, 5),
+     (9, 6144, 3), (16, 2048, 4), (6, 8192, 2)],
 )
 def test_softmax(cuda, rows, cols, trow):
     rng = np.random.default_rng(2)

@@ -33,6 +33,12 @@ __device__ __forceinline__ void decode_block(int b, int gx, int gy, int& x, int&
   z = t / gy;
 }
 
+// Scheduling fence: no instruction moves across it.  Placed after a batch of
+// independent global loads, it keeps the compiler from hoisting arithmetic on
+// the first load (and so a wait for it) above the remaining loads of the
+// batch; every load of the batch is then in flight before the first wait.
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 __device__ __forceinline__ float wave_max(float v, int width) {
   for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;

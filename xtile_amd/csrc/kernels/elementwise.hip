@@ -23,6 +23,8 @@ struct EwArgs {
   long long lda, ldb, ldc;
   int rows, cols;
   int gx, gy;
+  int y_fastest;  // linearise blocks y-fastest (consecutive groups are adjacent in memory)
+  int cv_shift;   // log2(cols / VW) when that is a power of two, else -1
 };
 
 template <int OP>
@@ -39,14 +41,30 @@ __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_lo
 template <typename T>
 __device__ __forceinline__ void st_nt(T v, T* p) { __builtin_nontemporal_store(v, p); }
 
-// Each thread handles U vectors per step.  All U loads are issued before any
-// is consumed (indices past the end are clamped to element 0 and their results
-// discarded), so a step costs one memory round trip, not U.
-template <int OP, int VW>
+// Blocks are independent (any execution order gives the same result), so the
+// launcher may pick the linearisation whose neighbouring workgroups touch
+// neighbouring memory.
+__device__ __forceinline__ void ew_block(const EwArgs& p, int& x, int& y, int& z) {
+  if (p.y_fastest) {
+    y = blockIdx.x % p.gy;
+    const int t = blockIdx.x / p.gy;
+    x = t % p.gx;
+    z = t / p.gx;
+  } else {
+    decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  }
+}
+
+// Each thread handles U vectors per step; U is the smallest of 1, 2, 4 that
+// covers the tile in one step (4 when it takes several).  All U loads are
+// issued before any is consumed; indices past the end of the tile (only in a
+// tile's last step) are clamped to element 0 and their results discarded, so a
+// step costs one memory round trip, not U.  POW2: the row length in vectors is
+// a power of two and row/column come from a shift and a mask.
+template <int OP, int VW, int U, bool POW2>
 __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
-  constexpr int U = 4;
   int x, y, z;
-  decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  ew_block(p, x, y, z);
   const float* A = p.a + p.ta.at(x, y, z);
   const float* B = p.b + p.tb.at(x, y, z);
   float* C = p.c + p.tc.at(x, y, z);
@@ -60,8 +78,8 @@ __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
       const int i = base + u * 256;
       ok[u] = i < n;
       const int ic = ok[u] ? i : 0;
-      const int r = ic / cv;
-      const int col = (ic - r * cv) * VW;
+      const int r = POW2 ? (ic >> p.cv_shift) : ic / cv;
+      const int col = (POW2 ? (ic & (cv - 1)) : ic - r * cv) * VW;
       offa[u] = r * p.lda + col;
       offb[u] = r * p.ldb + col;
       offc[u] = r * p.ldc + col;
@@ -73,6 +91,7 @@ __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
         va[u] = ld_nt(reinterpret_cast<const float4v*>(A + offa[u]));
         vb[u] = ld_nt(reinterpret_cast<const float4v*>(B + offb[u]));
       }
+      issue_fence();
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         float4v vc;
@@ -89,6 +108,7 @@ __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
         va[u] = ld_nt(A + offa[u]);
         vb[u] = ld_nt(B + offb[u]);
       }
+      issue_fence();
 #pragma unroll
       for (int u = 0; u < U; ++u)
         if (ok[u]) st_nt(ew_apply<OP>(va[u], vb[u]), C + offc[u]);
@@ -174,6 +194,7 @@ __global__ __launch_bounds__(256) void row_softmax_kernel(SoftmaxArgs p) {
         v[j][0] = ld_nt(xr + cc);
       }
     }
+    issue_fence();
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -208,6 +229,63 @@ __global__ __launch_bounds__(256) void row_softmax_kernel(SoftmaxArgs p) {
   }
 }
 
+// Full-row softmax: a TPB-thread workgroup owns one row of the tile at a time,
+// each thread NV float4 of it (cols == TPB * NV * 4 exactly, row starts
+// 16-byte aligned).  The row's loads are one instruction per float4 with
+// compile-time offsets, max/sum are trees within the thread, then a wave
+// butterfly, then one LDS exchange across the TPB/64 waves.  On gfx950 a
+// 512-thread group with two float4 per thread keeps the HBM read/write
+// stream at the rate of a plain device copy for 4096-wide rows.
+template <int TPB, int NV>
+__global__ __launch_bounds__(TPB) void row_softmax_wide_kernel(SoftmaxArgs p) {
+  constexpr int NW = TPB / 64;
+  __shared__ float lds[2][NW];
+  int x, y, z;
+  decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  const float* X = p.x + p.tx.at(x, y, z);
+  float* Y = p.y + p.ty.at(x, y, z);
+  const int w = threadIdx.x >> 6;
+  for (int r = 0; r < p.rows; ++r) {
+    const float4v* xr = reinterpret_cast<const float4v*>(X + r * p.ldx) + threadIdx.x;
+    float4v* yr = reinterpret_cast<float4v*>(Y + r * p.ldy) + threadIdx.x;
+    float4v v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = ld_nt(xr + j * TPB);
+    issue_fence();
+    float m = fmaxf(fmaxf(v[0].x, v[0].y), fmaxf(v[0].z, v[0].w));
+#pragma unroll
+    for (int j = 1; j < NV; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) lds[0][w] = m;
+    __syncthreads();
+    m = lds[0][0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) m = fmaxf(m, lds[0][k]);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      v[j].x = expf(v[j].x - m);
+      v[j].y = expf(v[j].y - m);
+      v[j].z = expf(v[j].z - m);
+      v[j].w = expf(v[j].w - m);
+      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    // the max slot and the sum slot are distinct, so this barrier also orders
+    // every read of lds[0] above before the next row's writes to it
+    if ((threadIdx.x & 63) == 0) lds[1][w] = s;
+    __syncthreads();
+    s = lds[1][0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) s += lds[1][k];
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) st_nt(v[j] * inv, yr + j * TPB);
+  }
+}
+
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
 
 bool aligned4(const xt::Access2D& a, const void* base) {
@@ -239,19 +317,45 @@ hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s,
     why = "elementwise operand tiles differ in shape";
     return hipErrorInvalidValue;
   }
-  bool vec = aligned4(p.a, a.a) && aligned4(p.b, a.b) && aligned4(p.c, a.c);
-  dim3 grid(num_blocks(p)), block(256);
-  int op = static_cast<int>(p.ew_op);
-#define XT_EW(OPV, VWV) hipLaunchKernelGGL((ew_binary_kernel<OPV, VWV>), grid, block, 0, s, a)
-  if (vec) {
-    if (op == 0) XT_EW(0, 4);
-    else if (op == 1) XT_EW(1, 4);
-    else XT_EW(2, 4);
-  } else {
-    if (op == 0) XT_EW(0, 1);
-    else if (op == 1) XT_EW(1, 1);
-    else XT_EW(2, 1);
+  const bool vec = aligned4(p.a, a.a) && aligned4(p.b, a.b) && aligned4(p.c, a.c);
+  const int vw = vec ? 4 : 1;
+  const long long cv = a.cols / vw;
+  const long long nvec = static_cast<long long>(a.rows) * cv;
+  if (nvec >= (1LL << 30)) {
+    why = "elementwise tile too large";
+    return hipErrorInvalidValue;
   }
+  a.cv_shift = -1;
+  if (cv > 0 && (cv & (cv - 1)) == 0) a.cv_shift = __builtin_ctzll(static_cast<unsigned long long>(cv));
+  const int u = nvec <= 256 ? 1 : nvec <= 512 ? 2 : 4;
+  const long long sx = p.c.addr.sx < 0 ? -p.c.addr.sx : p.c.addr.sx;
+  const long long sy = p.c.addr.sy < 0 ? -p.c.addr.sy : p.c.addr.sy;
+  a.y_fastest = (p.grid[1] > 1 && (sx == 0 || (sy != 0 && sy < sx))) ? 1 : 0;
+  dim3 grid(num_blocks(p)), block(256);
+  const int op = static_cast<int>(p.ew_op);
+  const bool pow2 = a.cv_shift >= 0;
+  // kernel variant index: op (3) x vector width (2) x U (3) x pow2 (2)
+#define XT_EW(OPV, VWV, UV, P2) \
+  hipLaunchKernelGGL((ew_binary_kernel<OPV, VWV, UV, P2>), grid, block, 0, s, a)
+#define XT_EW_P2(OPV, VWV, UV) \
+  do { if (pow2) XT_EW(OPV, VWV, UV, true); else XT_EW(OPV, VWV, UV, false); } while (0)
+#define XT_EW_U(OPV, VWV)                \
+  do {                                   \
+    if (u == 1) XT_EW_P2(OPV, VWV, 1);   \
+    else if (u == 2) XT_EW_P2(OPV, VWV, 2); \
+    else XT_EW_P2(OPV, VWV, 4);          \
+  } while (0)
+#define XT_EW_OP(VWV)                  \
+  do {                                 \
+    if (op == 0) XT_EW_U(0, VWV);      \
+    else if (op == 1) XT_EW_U(1, VWV); \
+    else XT_EW_U(2, VWV);              \
+  } while (0)
+  if (vw == 4) XT_EW_OP(4);
+  else XT_EW_OP(1);
+#undef XT_EW_OP
+#undef XT_EW_U
+#undef XT_EW_P2
 #undef XT_EW
   return hipGetLastError();
 }
@@ -274,6 +378,17 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
     return hipErrorInvalidValue;
   }
   const int vw = (aligned4(p.a, a.x) && aligned4(p.c, a.y)) ? 4 : 1;
+  dim3 grid(num_blocks(p));
+  if (vw == 4 && a.cols % 2048 == 0 && a.cols <= 8 * 2048) {
+    a.tpr = 512;
+    switch (a.cols / 2048) {
+#define XT_SMW(NVV) \
+  case NVV: hipLaunchKernelGGL((row_softmax_wide_kernel<512, NVV>), grid, dim3(512), 0, s, a); break
+      XT_SMW(1); XT_SMW(2); XT_SMW(3); XT_SMW(4); XT_SMW(5); XT_SMW(6); XT_SMW(7); XT_SMW(8);
+#undef XT_SMW
+    }
+    return hipGetLastError();
+  }
   // smallest NV in {1,2,4,8} with NV * VW * 256 >= cols, then the narrowest
   // power-of-two thread group that covers the row
   int nv = 1;
@@ -287,7 +402,7 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
   while (tpr < need) tpr *= 2;
   a.tpr = tpr;
   const bool exact = a.cols == nv * vw * tpr && a.rows % (256 / tpr) == 0;
-  dim3 grid(num_blocks(p)), block(256);
+  dim3 block(256);
 #define XT_SM(NVV, VWV, TPRV)                                                               \
   do {                                                                                      \
     if (VWV == 4 && TPRV >= 64 && exact)                                                    \
