@@ -155,11 +155,16 @@ def test_conv2d_f16(cuda, n, h, w, cin, cout, th, tw):
         (2, 11, 13, 32, 64, 3, 3, 3, 7, (0, 1, 2, 1), (2, 2), (1, 1), "f16"),
         (2, 14, 14, 64, 64, 3, 3, 7, 14, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),
         (1, 8, 8, 32, 128, 3, 3, 4, 8, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),
+        (2, 12, 12, 32, 64, 3, 3, 4, 12, (2, 2, 2, 2), (1, 1), (2, 2), "f16"),
+        (5, 61, 16, 32, 32, 3, 3, 61, 16, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),
     ],
 )
 def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
     """Strides, dilations, asymmetric padding, 1x1 / 5x5 filters, Cout with a
-    partial 32-channel N tile (48, 80) and bf16 operands."""
+    partial 32-channel N tile (48, 80) and bf16 operands.  Cout a multiple of
+    32 takes the band kernel (the 5 x 61-row case has 305 rows over the CUs:
+    two-row bands with a one-row band at the end of each image); the others
+    take the per-unit kernel."""
     rng = np.random.default_rng(5)
     mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
                    pad=pad, stride=stride, dilation=dil)

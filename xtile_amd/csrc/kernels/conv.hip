@@ -439,6 +439,253 @@ __global__ __launch_bounds__(WG, 1) void conv2d_kernel(ConvArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Band kernel: one workgroup per band of R consecutive output rows of one
+// image, used when the Blocks tile the whole output (TW = output width) and
+// the band's receptive field fits in LDS beside the whole filter.  Blocks are
+// independent (README.md:85-89) and every output pixel is computed with the
+// same K order as in the per-Block kernel, so regrouping pixels into bands is
+// a scheduling choice; R is picked so that the bands spread evenly over the
+// CUs (C4: 32 images x 56 rows = 256 bands of 7 rows).
+//   * The filter [KH*KW*Cin][Cout] (HWIO, Cout contiguous) and the band's halo
+//     [rows][cols][Cin] go global -> LDS by buffer DMA (16 bytes per lane, one
+//     1 KB run per wave instruction); halo pixels outside the image come from
+//     out-of-range buffer offsets, which the DMA writes as zeros.
+//   * MFMA view: D[pixel][cout] += P[pixel][k] F[k][cout] with
+//     v_mfma_f32_32x32x16_{f16,bf16}.  Pixel fragments are ds_read_b128 of the
+//     halo (channels contiguous); filter fragments come from ds_read_b64_tr_b16,
+//     which returns K-contiguous lanes from the Cout-contiguous rows.
+//   * Both LDS tiles are XOR-swizzled in 16-byte chunks (applied on the global
+//     side of the DMA), so 16 consecutive pixels or the transposed 4x16 blocks
+//     of four filter rows hit 16 distinct bank groups.
+//   * Work: the band's 32-pixel M tiles x 32-channel N tiles, dealt
+//     round-robin over the 8 waves (two waves per SIMD); a wave runs two of its
+//     M tiles at a time against one N tile and stores them straight from the
+//     accumulators (each store instruction writes two 128-byte pixel runs).
+constexpr int BWG = 512;
+
+struct BandArgs {
+  const unsigned char* src;
+  const unsigned char* filt;
+  float* out;
+  int H, W, C;           // source image
+  int KH, KW, CO;
+  int OH, OW;            // output rows / columns per image
+  int pad_t, pad_l, sh, sw, dh, dw;
+  int R;                 // output rows per band
+  int bands_per_image;
+  int rf_w;              // halo columns
+  int K, steps;          // K = KH*KW*C, steps = K / 16
+  int rb_shift;          // log2(2 * Cout): bytes per filter row
+  int fsw_shift, fsw_mask;  // filter chunk swizzle: 4 * ((k >> shift) & mask)
+  int pitch;             // LDS bytes per halo pixel: 2*Cin (+16 to make the chunk count odd)
+  int nchp;              // pitch / 16
+  int ppi;               // halo pixels per DMA instruction: 64 / nchp
+  Magic m_nchp, m_rfw, m_ow;
+  int filt_instr;        // 1 KB DMA runs of the filter
+  unsigned filt_bytes;   // K*CO*2 (LDS offset of the halo)
+  unsigned image_bytes;  // H*W*C*2
+};
+
+template <bool BF16>
+__device__ __forceinline__ float16v band_mfma(short8 a, short8 b, float16v c) {
+  return mfma32<BF16>(a, b, c);
+}
+
+typedef __attribute__((address_space(3))) unsigned char band_lds_t;
+
+// MI M tiles of the band (first pixel q0, then every tstride pixels) against
+// N tile j, all in one pass so that each filter fragment feeds MI MFMAs.  K
+// runs in steps of 16: tap s / (Cin/16), channels 16 * (s % (Cin/16)).  The
+// fragments of step s+1 are read while the MFMAs of step s run.  Pixels at or
+// past qend are computed on clamped addresses and not stored.
+template <int MI, bool BF16>
+__device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* Fs, const band_lds_t* Hs,
+                                           __amdgpu_buffer_rsrc_t orc, int q0, int tstride, int qend, int j,
+                                           int lane) {
+  const int lr = lane & 31, hi = lane >> 5;
+  const int g = lane >> 4, li = lane & 15;
+  const int RB = p.CO * 2;
+  const int cs_per_tap = p.C / 16;
+  // Filter fragment: two transposed 4x16 reads (K rows fk, fk + 4 of the
+  // step).  A step moves 16 rows, which leaves the row swizzle unchanged, so
+  // each read is a per-lane constant plus 16 * RB * s.
+  int boff[2];
+  {
+    const int ncol = 32 * j + 16 * (g & 1) + 4 * (li & 3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
+      boff[h] = k * RB + (((ncol >> 3) ^ (4 * ((k >> p.fsw_shift) & p.fsw_mask))) << 4) + (ncol & 7) * 2;
+    }
+  }
+  const int bstep = 16 * RB;
+  // Pixel fragment of tile t at tap offset `tapoff` (halo pixels) and channel
+  // step cs: Hs + (hp0 + tapoff) * pitch + 16 * (2 * cs + hi).
+  int hbase[MI];
+#pragma unroll
+  for (int t = 0; t < MI; ++t) {
+    const int q = min(q0 + t * tstride + lr, qend - 1);
+    const int r = (int)udiv((unsigned)q, p.m_ow), c = q - r * p.OW;
+    hbase[t] = (r * p.sh * p.rf_w + c * p.sw) * p.pitch + hi * 16;
+  }
+  int base[MI];
+  auto set_tap = [&](int tapoff) {
+    const int tb = tapoff * p.pitch;
+#pragma unroll
+    for (int t = 0; t < MI; ++t) base[t] = hbase[t] + tb;
+  };
+  auto read = [&](int s, int cs, short8 (&a)[MI], short8& b) {
+#pragma unroll
+    for (int t = 0; t < MI; ++t)
+      a[t] = *reinterpret_cast<const short8 __attribute__((address_space(3)))*>(Hs + base[t] + cs * 32);
+    const band_lds_t* f = Fs + s * bstep;
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<short4v __attribute__((address_space(3)))*>(const_cast<band_lds_t*>(f) + boff[0]));
+    const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<short4v __attribute__((address_space(3)))*>(const_cast<band_lds_t*>(f) + boff[1]));
+    b = short8{lo[0], lo[1], lo[2], lo[3], h4[0], h4[1], h4[2], h4[3]};
+  };
+  float16v acc[MI];
+#pragma unroll
+  for (int t = 0; t < MI; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[t][v] = 0.f;
+
+  // Cin / 16 is even, so steps s and s+1 share a tap.  The loop body has no
+  // branch: the tap advance is a pair of selects and the read-ahead of step
+  // s+2 always runs (on the last iteration it rereads the last tap and step,
+  // in bounds, and the result is unused), so the compiler can issue it ahead
+  // of the MFMAs of step s+1.
+  short8 a0[MI], a1[MI], b0, b1;
+  int kh = 0, kw = 0, cs = 0;
+  set_tap(0);
+  read(0, 0, a0, b0);
+  // Scheduling fences keep each read batch ahead of the MFMAs that do not
+  // need it (left alone, the scheduler sinks the reads next to their MFMAs to
+  // save registers and the LDS latency shows on every step).
+  for (int s = 0; s < p.steps; s += 2) {
+    read(s + 1, cs + 1, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<BF16>(a0[t], b0, acc[t]);
+    __builtin_amdgcn_sched_barrier(0);
+    cs += 2;
+    const bool tap_end = cs == cs_per_tap;
+    cs = tap_end ? 0 : cs;
+    kw += tap_end ? 1 : 0;
+    const bool row_end = kw == p.KW;
+    kw = row_end ? 0 : kw;
+    kh += row_end ? 1 : 0;
+    const bool last = s + 2 >= p.steps;
+    set_tap(last ? (p.KH - 1) * p.dh * p.rf_w + (p.KW - 1) * p.dw : kh * p.dh * p.rf_w + kw * p.dw);
+    read(last ? p.steps - 1 : s + 2, last ? cs_per_tap - 1 : cs, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<BF16>(a1[t], b1, acc[t]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // D = P x F: lane l holds channel 32j + l%32; register v holds pixel
+  // 8*(v/4) + 4*(l/32) + v%4 of the tile.  Pixels at or past qend get an
+  // out-of-range offset (the store is dropped).
+#pragma unroll
+  for (int t = 0; t < MI; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int q = q0 + t * tstride + 8 * (v >> 2) + 4 * hi + (v & 3);
+      const unsigned off = q < qend ? (unsigned)((q * p.CO + 32 * j + lr) * 4) : kOutOfRange;
+      // the element goes through a scalar: __builtin_bit_cast of an
+      // ext_vector element lvalue reads element 0 whatever the index
+      const float val = acc[t][v];
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), orc, off, 0, 2);
+    }
+}
+
+// Tiles m0, m0 + mstep, ... (< nmt) of pixels [qbeg, qend) against N tile j,
+// up to four per pass.
+template <bool BF16>
+__device__ __forceinline__ void band_wave(const BandArgs& p, const band_lds_t* Fs, const band_lds_t* Hs,
+                                          __amdgpu_buffer_rsrc_t orc, int qbeg, int qend, int m0, int mstep,
+                                          int j, int lane) {
+  const int nmt = (qend - qbeg + 31) >> 5;
+  int n = m0 < nmt ? (nmt - m0 + mstep - 1) / mstep : 0;
+  int q0 = qbeg + m0 * 32;
+  const int tstride = mstep * 32;
+  while (n > 0) {
+    const int c = min(n, 4);
+    switch (c) {
+      case 1: band_tiles<1, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 2: band_tiles<2, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 3: band_tiles<3, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      default: band_tiles<4, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+    }
+    q0 += c * tstride;
+    n -= c;
+  }
+}
+
+template <int NT, bool BF16>
+__global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char blds[];
+  typedef __attribute__((address_space(3))) unsigned char lds_t;
+  lds_t* Fs = (lds_t*)blds;  // filter [K][Cout]
+  lds_t* Hs = Fs + p.filt_bytes;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int band = blockIdx.x;
+  const int n = band / p.bands_per_image;
+  const int r0 = (band - n * p.bands_per_image) * p.R;
+  const int rows = min(p.R, p.OH - r0);
+  const int hrows = (rows - 1) * p.sh + (p.KH - 1) * p.dh + 1;
+  const int hpix = hrows * p.rf_w;
+  // -- DMA: filter, then halo --------------------------------------------
+  {
+    const __amdgpu_buffer_rsrc_t fr = buffer_of(p.filt, p.filt_bytes);
+    for (int i = wave; i < p.filt_instr; i += BWG / 64) {
+      const unsigned b = (unsigned)i * 1024u + lane * 16u;
+      const int k = b >> p.rb_shift;
+      const int pos = (b - (k << p.rb_shift)) >> 4;
+      const int chunk = pos ^ (4 * ((k >> p.fsw_shift) & p.fsw_mask));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(fr, (void __attribute__((address_space(3)))*)(Fs + i * 1024),
+                                               16, (unsigned)((k << p.rb_shift) + chunk * 16), 0, 0, 0);
+    }
+    // Halo pixels are `pitch` bytes apart in LDS (an odd number of 16-byte
+    // chunks, so sixteen consecutive pixels fall in sixteen distinct bank
+    // groups).  One DMA instruction writes ppi whole pixels: lane l carries
+    // chunk l % nchp of pixel l / nchp; the pad chunk reads zero and lanes past
+    // ppi * nchp are masked off.
+    const __amdgpu_buffer_rsrc_t ir = buffer_of(p.src + (size_t)n * p.image_bytes, p.image_bytes);
+    const int ih0 = r0 * p.sh - p.pad_t, iw0 = -p.pad_l;
+    const int lp = (int)udiv((unsigned)lane, p.m_nchp);
+    const int lc = lane - lp * p.nchp;
+    const bool lane_on = lp < p.ppi;
+    const int nch = p.C / 8;
+    const int hinstr = (hpix + p.ppi - 1) / p.ppi;
+    for (int i = wave; i < hinstr; i += BWG / 64) {
+      const int q = i * p.ppi + lp;
+      const int hr = (int)udiv((unsigned)q, p.m_rfw), hc = q - hr * p.rf_w;
+      const int ih = ih0 + hr, iw = iw0 + hc;
+      const bool inside = lc < nch && q < hpix && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+      const unsigned off = inside ? (unsigned)((ih * p.W + iw) * nch + lc) * 16u : kOutOfRange;
+      if (lane_on)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ir, (void __attribute__((address_space(3)))*)(Hs + i * p.ppi * p.pitch), 16, off, 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed
+  __syncthreads();                // and every other wave's
+
+  // -- compute ------------------------------------------------------------
+  const int M = rows * p.OW;
+  const int j = wave % NT;              // this wave's N tile
+  constexpr int MSTEP = (BWG / 64) / NT; // M-tile stride between a wave's tiles
+  const __amdgpu_buffer_rsrc_t orc =
+      buffer_of(p.out + ((size_t)n * p.OH + r0) * p.OW * p.CO, (unsigned)(M * p.CO * 4));
+
+  band_wave<BF16>(p, Fs, Hs, orc, 0, M, wave / NT, MSTEP, j, lane);
+}
+
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
 
 // Raises the kernel's dynamic-LDS limit once (a host-side attribute, so later
@@ -455,6 +702,130 @@ hipError_t launch_conv_t(const ConvArgs& a, dim3 grid, size_t lds, hipStream_t s
   }
   hipLaunchKernelGGL(fn, grid, dim3(WG), lds, s, a);
   return hipGetLastError();
+}
+
+template <int NT, bool BF16>
+hipError_t launch_band_t(const BandArgs& a, int bands, size_t lds, hipStream_t s) {
+  static std::atomic<int> configured{0};
+  auto fn = conv2d_band_kernel<NT, BF16>;
+  if (static_cast<int>(lds) > configured.load()) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    configured.store(static_cast<int>(lds));
+  }
+  hipLaunchKernelGGL(fn, dim3(bands), dim3(BWG), lds, s, a);
+  return hipGetLastError();
+}
+
+int ilog2(unsigned v) {
+  int r = 0;
+  while ((1u << (r + 1)) <= v) ++r;
+  return r;
+}
+
+// The band kernel applies when the Blocks tile images [0, gB) x all output
+// rows and columns exactly once, in the output's natural NHWC addressing, and
+// the filter tile is the whole filter.  Returns false (nothing launched) when
+// it does not apply; `e` carries a launch error otherwise.
+bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, int cus, hipError_t& e) {
+  const xt::ConvPlan& c = p.conv;
+  if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
+      c.ch.axis == c.cw.axis)
+    return false;
+  const long long gB = p.grid[c.cb.axis], gH = p.grid[c.ch.axis], gW = p.grid[c.cw.axis];
+  if (gH * c.TH != c.out_H || gW * c.TW != c.out_W || c.out_C != c.CO) return false;
+  auto step = [&](const xt::TileAddr& t, int axis) { return axis == 0 ? t.sx : axis == 1 ? t.sy : t.sz; };
+  const long long plane = c.out_H * c.out_W * c.out_C;
+  if (c.out_addr.c0 != 0 || (gB > 1 && step(c.out_addr, c.cb.axis) != plane) ||
+      (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
+      (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
+    return false;
+  if (c.filt_addr.c0 || c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz) return false;
+  if (c.C % 16 || c.CO % 32 || c.CO > 128 || c.CO == 96) return false;
+  const long long K = c.KH * c.KW * c.C;
+  const long long filt_bytes = K * c.CO * 2;
+  if (filt_bytes % 1024) return false;
+  const long long PB = c.C * 2;
+  // LDS pitch of a halo pixel: an odd number of 16-byte chunks
+  const long long pitch = (PB / 16) % 2 ? PB : PB + 16;
+  const long long nchp = pitch / 16;
+  if (nchp > 64) return false;
+  const long long ppi = 64 / nchp;
+  const long long rf_w = (c.out_W - 1) * c.stride_w + (c.KW - 1) * c.dil_w + 1;
+  const long long image_bytes = c.H * c.W * PB;
+  if (image_bytes >= (1LL << 31) || filt_bytes >= (1LL << 31)) return false;
+  // rows per band: spread gB * OH rows over the CUs, shrink until LDS fits
+  const long long total_rows = gB * c.out_H;
+  long long R = std::min<long long>(c.out_H, (total_rows + cus - 1) / std::max(cus, 1));
+  size_t lds = 0;
+  long long hpix_max = 0;
+  for (; R >= 1; --R) {
+    const long long hrows = (R - 1) * c.stride_h + (c.KH - 1) * c.dil_h + 1;
+    hpix_max = hrows * rf_w;
+    const long long halo = ((hpix_max + ppi - 1) / ppi) * ppi * pitch;
+    if (filt_bytes + halo <= max_lds) {
+      lds = static_cast<size_t>(filt_bytes + halo);
+      break;
+    }
+  }
+  if (R < 1) return false;
+  // the kernel divides pixel indices below 2^16 by multiply-high reciprocals
+  if (hpix_max + ppi >= 65536 || R * c.out_W >= 65536 || rf_w >= 65536 || c.out_W >= 65536) return false;
+  if (R * c.out_W * c.CO * 4 >= (1LL << 31)) return false;
+  BandArgs a;
+  a.src = static_cast<const unsigned char*>(bufs[c.src_arg]);
+  a.filt = static_cast<const unsigned char*>(bufs[c.filt_arg]);
+  a.out = static_cast<float*>(bufs[c.out_arg]);
+  for (const void* ptr : {(const void*)a.src, (const void*)a.filt, (const void*)a.out})
+    if (reinterpret_cast<uintptr_t>(ptr) % 16) return false;
+  a.H = (int)c.H;
+  a.W = (int)c.W;
+  a.C = (int)c.C;
+  a.KH = (int)c.KH;
+  a.KW = (int)c.KW;
+  a.CO = (int)c.CO;
+  a.OH = (int)c.out_H;
+  a.OW = (int)c.out_W;
+  a.pad_t = (int)c.pad_top;
+  a.pad_l = (int)c.pad_left;
+  a.sh = (int)c.stride_h;
+  a.sw = (int)c.stride_w;
+  a.dh = (int)c.dil_h;
+  a.dw = (int)c.dil_w;
+  a.R = (int)R;
+  a.bands_per_image = (int)((c.out_H + R - 1) / R);
+  a.rf_w = (int)rf_w;
+  a.K = (int)K;
+  a.steps = (int)(K / 16);
+  // filter rows of RB = 2*Cout bytes: the transposed reads of one half-wave
+  // cover 64 bytes of four consecutive rows; XOR the 64-byte block index
+  // with the row's position inside a 256-byte bank window
+  const int RB = a.CO * 2;
+  a.rb_shift = ilog2((unsigned)RB);
+  a.fsw_shift = ilog2(256 / RB);
+  a.fsw_mask = RB / 64 - 1;
+  a.pitch = (int)pitch;
+  a.nchp = (int)nchp;
+  a.ppi = (int)ppi;
+  a.m_nchp = udiv_magic((unsigned)nchp);
+  a.m_rfw = udiv_magic((unsigned)rf_w);
+  a.m_ow = udiv_magic((unsigned)c.out_W);
+  a.filt_instr = (int)(filt_bytes / 1024);
+  a.filt_bytes = (unsigned)filt_bytes;
+  a.image_bytes = (unsigned)image_bytes;
+  const long long bands = gB * a.bands_per_image;
+  if (bands > 0x7fffffff) return false;
+  const bool bf16 = c.elem == xt::Elem::BF16;
+  const int nt = a.CO / 32;
+#define XT_BAND(NTV, BFV) e = launch_band_t<NTV, BFV>(a, (int)bands, lds, s)
+  switch (nt) {
+    case 1: if (bf16) XT_BAND(1, true); else XT_BAND(1, false); break;
+    case 2: if (bf16) XT_BAND(2, true); else XT_BAND(2, false); break;
+    default: if (bf16) XT_BAND(4, true); else XT_BAND(4, false); break;
+  }
+#undef XT_BAND
+  return true;
 }
 
 }  // namespace
@@ -518,6 +889,7 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   if (e != hipSuccess) return e;
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
+  if (try_band(p, bufs, s, max_lds, cus, e)) return e;
   // Largest work unit (rows dividing TH) whose halo fits beside the filter.
   const int ntp = nt == 3 ? 4 : nt;  // N tiles compiled: 1, 2 or 4
   const size_t filt_bytes = size_t(ntp) * 32 * a.kpitch;
