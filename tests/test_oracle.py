@@ -380,3 +380,64 @@ func.func @f(%x: memref<1x12xf32>, %y: memref<1x12xi8>) attributes {xt.grid = ar
 }"""
     got = run_c(text, [vals, np.zeros((1, 12), np.int8)])[1]
     np.testing.assert_array_equal(got[0], np.array([0, 2, 2, 0, -2, 127, 127, -128, 127, -128, 0, 0], np.int8))
+
+
+# -- general tile programs (the GPU tile interpreter's op set) ---------------------
+
+
+def test_oracle_layernorm_matches_float64_closed_form():
+    """Row layernorm (reduce, broadcast subtract, square, reduce, rsqrt, gamma,
+    beta): the oracle's broadcasts and reductions against numpy float64."""
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 1.5, (128, 64)).astype(np.float32)
+    g = rng.normal(1, 0.2, (1, 64)).astype(np.float32)
+    b = rng.normal(0, 0.2, (1, 64)).astype(np.float32)
+    inv_n = np.full((1, 1), 1.0 / 64, np.float32)
+    eps = np.full((1, 1), 1e-5, np.float32)
+    y = run_c(str(K.layernorm(128, 64, 64)), [x, g, b, inv_n, eps, np.zeros_like(x)])[5]
+    xd = x.astype(np.float64)
+    mu = xd.mean(axis=1, keepdims=True)
+    var = ((xd - mu) ** 2).mean(axis=1, keepdims=True)
+    ref = (xd - mu) / np.sqrt(var + 1e-5) * g + b
+    np.testing.assert_allclose(y, ref, rtol=0, atol=2e-5)
+    # a planted error in the checker (gamma and beta swapped) is caught
+    bad = (xd - mu) / np.sqrt(var + 1e-5) * b + g
+    assert np.max(np.abs(y - bad)) > 0.1
+
+
+def test_oracle_column_softmax_and_bias_add():
+    rng = np.random.default_rng(12)
+    x = rng.normal(0, 2, (64, 128)).astype(np.float32)
+    y = run_c(str(K.column_softmax(64, 128, 32)), [x, np.zeros_like(x)])[1]
+    ref = cf.softmax_rows(x.T).T
+    assert np.max(np.abs(y - ref) / np.maximum(ref, 1e-30)) < 2e-6
+    np.testing.assert_allclose(y.sum(axis=0), 1.0, atol=1e-6)
+    v = rng.normal(0, 1, (1, 256)).astype(np.float32)
+    a = rng.normal(0, 1, (128, 256)).astype(np.float32)
+    out = run_c(str(K.bias_add(128, 256)), [a, v, np.zeros_like(a)])[2]
+    assert np.array_equal(out, a + v)  # IEEE f32 add, broadcast along rows
+
+
+def test_oracle_unary_chain_transpose_and_reshape():
+    """cos -> sin -> rsqrt -> sigmoid -> tanh -> silu, reshape, transpose of a
+    rank-3 tile (the last two dims swap), against numpy."""
+    from tests.golden.dsl_programs import programs
+    from xtile_amd import dsl
+    import xtile_amd as xt
+
+    kernel, args, grid, db = programs(dsl)["unary_and_shape"]
+    m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
+    rng = np.random.default_rng(13)
+    x = rng.uniform(-1, 1, (8, 8)).astype(np.float32)
+    t = rng.normal(0, 1, (2, 3, 4)).astype(np.float32)
+    bufs = run_c(str(m), [x, np.zeros((8, 8), np.float32), np.zeros((4, 16), np.float32), t,
+                          np.zeros((2, 4, 3), np.float32)])
+    v = x.astype(np.float64)
+    v = np.sin(np.cos(v))
+    v = 1 / np.sqrt(v)
+    v = 1 / (1 + np.exp(-v))
+    v = np.tanh(v)
+    v = v / (1 + np.exp(-v))
+    np.testing.assert_allclose(bufs[1], v, rtol=2e-6, atol=0)
+    assert np.array_equal(bufs[2], bufs[1].reshape(4, 16))
+    assert np.array_equal(bufs[4], t.transpose(0, 2, 1))

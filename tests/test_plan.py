@@ -46,13 +46,40 @@ def test_out_of_bounds_tiles_are_rejected():
 
 
 def test_unsupported_program_names_its_ops():
+    """i8 xt.mma (test/python/dsl_convert.py:142-166) has no HIP kernel."""
     from tests.golden.dsl_programs import programs
     from xtile_amd import dsl
 
-    kernel, args, grid, db = programs(dsl)["unary_and_shape"]
+    kernel, args, grid, db = programs(dsl)["compute_ops"]
     m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
-    with pytest.raises(NotImplementedError, match="unsupported tile program.*xt.cos"):
+    with pytest.raises(NotImplementedError, match="unsupported tile program.*xt.mma"):
         xt.plan(m)
+
+
+@pytest.mark.parametrize(
+    "name,kernel",
+    [
+        ("unary_and_shape", "tile_vm f32 insts=12 loads=2 stores=3 lds="),
+        ("column_reduce", "tile_vm f32 insts=3 loads=1 stores=1 lds="),
+        ("divide_kernel", "tile_vm f32 insts=5 loads=2 stores=1 lds="),
+    ],
+)
+def test_general_programs_plan_onto_the_tile_interpreter(name, kernel):
+    from tests.golden.dsl_programs import programs
+    from xtile_amd import dsl
+
+    k, args, grid, db = programs(dsl)[name]
+    m = xt.convert(k, args=args, grid=grid, double_buffering=db)
+    assert xt.plan(m)["kernel"].startswith(kernel)
+
+
+def test_interpreter_programs_and_lds_budget():
+    assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith("tile_vm f32 insts=17 loads=5 stores=1")
+    assert xt.plan(K.column_softmax(64, 128, 32))["kernel"].startswith("tile_vm")
+    assert xt.plan(K.bias_add(128, 256))["kernel"].startswith("tile_vm")
+    # live tiles beyond 160 KB of LDS are refused on the host
+    with pytest.raises(NotImplementedError, match="KB of LDS"):
+        xt.plan(K.layernorm(512, 256, 256))
 
 
 def test_epilogue_matmul_plans():

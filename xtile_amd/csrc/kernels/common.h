@@ -24,6 +24,26 @@ struct TileOff {
   }
 };
 
+struct Magic {
+  unsigned m, k;
+};
+
+// n / d for n, d < 2^16 as umulhi(n, ceil(2^32 / d)) + (n & k), where k is
+// all ones for d == 1 (m = 0) and zero otherwise, so there is no branch.
+// Exact: with m*d = 2^32 + r (0 <= r < d) and n = q*d + s, n*m / 2^32 =
+// q + (s + n*r / 2^32) / d and n*r < 2^32, so the fraction stays below 1.
+__host__ __device__ __forceinline__ unsigned udiv(unsigned n, Magic m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __umulhi(n, m.m) + (n & m.k);
+#else
+  return unsigned((unsigned long long)n * m.m >> 32) + (n & m.k);
+#endif
+}
+
+inline Magic udiv_magic(unsigned d) {
+  return d == 1 ? Magic{0u, ~0u} : Magic{unsigned(((1ull << 32) + d - 1) / d), 0u};
+}
+
 // Block id (x, y, z) of the grid point handled by linear index `b`, in the
 // reference's z -> y -> x order (x fastest).
 __device__ __forceinline__ void decode_block(int b, int gx, int gy, int& x, int& y, int& z) {

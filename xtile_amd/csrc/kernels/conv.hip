@@ -49,9 +49,7 @@ constexpr int kOutPitch = 144;  // LDS bytes per staged output pixel (32 floats 
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-struct Magic {
-  unsigned m, k;
-};
+
 
 struct ConvArgs {
   const unsigned short* src;
@@ -82,21 +80,6 @@ struct ConvArgs {
   unsigned unit_out_bytes;           // UR*out_W*out_C*4: the output rows of one unit
 };
 
-// n / d for n, d < 2^16 as umulhi(n, ceil(2^32 / d)) + (n & k), where k is
-// all ones for d == 1 (m = 0) and zero otherwise, so there is no branch.
-// Exact: with m*d = 2^32 + r (0 <= r < d) and n = q*d + s, n*m / 2^32 =
-// q + (s + n*r / 2^32) / d and n*r < 2^32, so the fraction stays below 1.
-__host__ __device__ __forceinline__ unsigned udiv(unsigned n, Magic m) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  return __umulhi(n, m.m) + (n & m.k);
-#else
-  return unsigned((unsigned long long)n * m.m >> 32) + (n & m.k);
-#endif
-}
-
-inline Magic udiv_magic(unsigned d) {
-  return d == 1 ? Magic{0u, ~0u} : Magic{unsigned(((1ull << 32) + d - 1) / d), 0u};
-}
 
 template <bool BF16>
 __device__ __forceinline__ float16v mfma32(short8 a, short8 b, float16v c) {

@@ -202,14 +202,7 @@ bool match_ew(const Analysis& an, Plan& p, std::string& err) {
   if (count_ops(an) != expected) return false;
   const Type& ta = an.f.type_of(la->results[0]);
   const Type& tb = an.f.type_of(lb->results[0]);
-  if (ta != tb) {
-    err = "elementwise programs with broadcast operands are not supported by the HIP backend yet";
-    return false;
-  }
-  if (ta.elem != Elem::F32) {
-    err = "elementwise programs currently require f32 tiles";
-    return false;
-  }
+  if (ta != tb || ta.elem != Elem::F32) return false;  // broadcast or non-f32: the interpreter
   if (!access_of(an, *la, p.a, err, true) || !access_of(an, *lb, p.b, err, true) ||
       !access_of(an, *st, p.c, err, true))
     return false;
@@ -265,15 +258,9 @@ bool match_softmax(const Analysis& an, Plan& p, std::string& err) {
       rmax->operands[0] != ld->results[0] || !axis_is(rmax, 1))
     return false;
   const Type& t = an.f.type_of(ld->results[0]);
-  if (t.elem != Elem::F32 || t.rank() != 2) {
-    err = "row softmax requires a rank-2 f32 tile";
-    return false;
-  }
+  // other shapes and types run on the tile interpreter
+  if (t.elem != Elem::F32 || t.rank() != 2 || t.shape[1] > 8192) return false;
   if (!access_of(an, *ld, p.a, err) || !access_of(an, *st, p.c, err)) return false;
-  if (t.shape[1] > 8192) {
-    err = "row softmax supports rows of at most 8192 elements";
-    return false;
-  }
   p.kind = PlanKind::RowSoftmax;
   double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
   p.algo_bytes = blocks * double(t.numel()) * 8;
@@ -502,6 +489,232 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
   return true;
 }
 
+// -- TileVM ----------------------------------------------------------------------
+//
+// Every other f32 program without matmul / conv: the Block's ops, in program
+// order, become tile instructions over LDS slots (one workgroup per Block).
+// Slots are assigned by liveness, first fit; reshape renames a slot (the data
+// is row-major either way, xtile/dsl.py reshape); transpose swaps the last two
+// dims and permute reorders dims (include/xt/XTOps.td), both as a Permute.
+
+bool vm_unary(const std::string& n, VmUnary& k) {
+  static const std::pair<const char*, VmUnary> table[] = {
+      {"xt.exp", VmUnary::Exp},       {"xt.cos", VmUnary::Cos},         {"xt.sin", VmUnary::Sin},
+      {"xt.reciprocal", VmUnary::Recip}, {"xt.rsqrt", VmUnary::Rsqrt}, {"xt.sigmoid", VmUnary::Sigmoid},
+      {"xt.tanh", VmUnary::Tanh},     {"xt.silu", VmUnary::Silu}};
+  for (auto& e : table)
+    if (n == e.first) {
+      k = e.second;
+      return true;
+    }
+  return false;
+}
+
+// shape padded to rank 3 with leading 1s
+bool pad3(const std::vector<int64_t>& s, int dims[3], std::string& err) {
+  if (s.empty() || s.size() > 3) {
+    err = "tile programs on the HIP backend take tensors of rank 1 to 3";
+    return false;
+  }
+  const int off = 3 - static_cast<int>(s.size());
+  for (int d = 0; d < 3; ++d) dims[d] = d < off ? 1 : static_cast<int>(s[d - off]);
+  return true;
+}
+
+bool match_vm(const Analysis& an, Plan& p, std::string& err) {
+  const int nops = static_cast<int>(an.compute.size());
+  // every op must be one the interpreter runs, on f32 tensors
+  for (const Op* o : an.compute) {
+    VmUnary u;
+    const std::string& n = o->name;
+    const bool ok = n == "xt.load" || n == "xt.store" || n == "xt.add" || n == "xt.sub" || n == "xt.mul" ||
+                    n == "xt.reduce_sum" || n == "xt.reduce_max" || n == "xt.reshape" ||
+                    n == "xt.transpose" || n == "xt.permute" || vm_unary(n, u);
+    if (!ok) return false;
+  }
+  for (const Op* o : an.compute) {
+    const std::string& n = o->name;
+    for (int r : o->results)
+      if (an.f.type_of(r).elem != Elem::F32) {
+        err = "tile programs on the HIP backend compute in f32 (" + n + " yields " +
+              elem_name(an.f.type_of(r).elem) + ")";
+        return false;
+      }
+    if (n == "xt.store" && an.f.type_of(o->operands[1]).elem != Elem::F32) {
+      err = "tile programs on the HIP backend store f32 tiles";
+      return false;
+    }
+  }
+  // storage roots (reshape results share their operand's slot) and last uses
+  std::map<int, int> root;
+  auto root_of = [&](int v) {
+    auto it = root.find(v);
+    return it == root.end() ? v : it->second;
+  };
+  std::map<int, int> last_use;
+  for (int i = 0; i < nops; ++i) {
+    const Op* o = an.compute[i];
+    if (o->name == "xt.reshape") root[o->results[0]] = root_of(o->operands[0]);
+    for (int v : o->operands) {
+      if (!an.f.type_of(v).is_tensor()) continue;
+      last_use[root_of(v)] = i;
+    }
+  }
+  // first-fit allocation over [0, inf) in floats, 4-float granules
+  std::vector<std::pair<int, int>> used;  // (offset, size) of live slots
+  std::map<int, std::pair<int, int>> slot; // root -> (offset, size)
+  int high = 0;
+  auto alloc = [&](int floats) {
+    floats = (floats + 3) & ~3;
+    int at = 0;
+    for (;;) {
+      bool clash = false;
+      for (auto& u : used)
+        if (at < u.first + u.second && u.first < at + floats) {
+          at = u.first + u.second;
+          clash = true;
+        }
+      if (!clash) break;
+    }
+    used.push_back({at, floats});
+    high = std::max(high, at + floats);
+    return std::make_pair(at, floats);
+  };
+  auto release = [&](int r) {
+    auto it = slot.find(r);
+    if (it == slot.end()) return;
+    for (size_t k = 0; k < used.size(); ++k)
+      if (used[k].first == it->second.first) {
+        used.erase(used.begin() + k);
+        break;
+      }
+  };
+  VmPlan vm;
+  double bytes = 0;
+  for (int i = 0; i < nops; ++i) {
+    const Op* o = an.compute[i];
+    const std::string& n = o->name;
+    VmInst in;
+    if (n == "xt.load" || n == "xt.store") {
+      const bool is_load = n == "xt.load";
+      const int mem_v = is_load ? o->operands[0] : o->operands[1];
+      const Type& mem = an.f.type_of(mem_v);
+      const Type& ten = is_load ? an.f.type_of(o->results[0]) : an.f.type_of(o->operands[0]);
+      VmAccess acc;
+      acc.arg = an.arg_index(mem_v);
+      if (acc.arg < 0) {
+        err = n + " must access a function argument";
+        return false;
+      }
+      int shared = 0;
+      if (is_load)
+        if (const Attr* sh = find_attr(o->attrs, "shared")) shared = static_cast<int>(sh->i);
+      std::vector<int> cv(o->operands.begin() + (is_load ? 1 : 2), o->operands.end());
+      const std::string what = n + " of argument #" + std::to_string(acc.arg);
+      if (!tile_origin(an, cv, shared, ten.shape, mem.shape, what, acc.addr, nullptr, err)) return false;
+      if (!pad3(ten.shape, in.dims, err)) return false;
+      std::vector<int64_t> st = strides_of(mem.shape);
+      const int off = 3 - static_cast<int>(st.size());
+      for (int d = 0; d < 3; ++d) acc.stride[d] = d < off ? 0 : st[d - off];
+      in.op = is_load ? VmOp::Load : VmOp::Store;
+      in.kind = static_cast<int16_t>(vm.access.size());
+      vm.access.push_back(acc);
+      bytes += double(ten.numel()) * 4;
+      if (is_load) {
+        auto sl = alloc(static_cast<int>(ten.numel()));
+        slot[o->results[0]] = sl;
+        in.dst = sl.first;
+      } else {
+        in.a = slot.at(root_of(o->operands[0])).first;
+      }
+    } else if (n == "xt.reshape") {
+      continue;  // same slot, new shape
+    } else {
+      const Type& res = an.f.type_of(o->results[0]);
+      const Type& ta = an.f.type_of(o->operands[0]);
+      in.a = slot.at(root_of(o->operands[0])).first;
+      VmUnary u;
+      if (vm_unary(n, u)) {
+        in.op = VmOp::Unary;
+        in.kind = static_cast<int16_t>(u);
+        if (!pad3(res.shape, in.dims, err)) return false;
+      } else if (n == "xt.add" || n == "xt.sub" || n == "xt.mul") {
+        const Type& tb = an.f.type_of(o->operands[1]);
+        in.op = VmOp::Binary;
+        in.kind = static_cast<int16_t>(n == "xt.add" ? VmBinary::Add : n == "xt.sub" ? VmBinary::Sub : VmBinary::Mul);
+        in.b = slot.at(root_of(o->operands[1])).first;
+        if (ta.shape != res.shape || tb.rank() != res.rank()) {
+          err = "tile programs on the HIP backend broadcast the right operand only, at equal rank "
+                "(xtile/dsl.py:754-759)";
+          return false;
+        }
+        if (!pad3(res.shape, in.dims, err) || !pad3(tb.shape, in.aux, err)) return false;
+        for (int d = 0; d < 3; ++d)
+          if (in.aux[d] != in.dims[d] && in.aux[d] != 1) {
+            err = "broadcast operand dims must equal the result's or be 1";
+            return false;
+          }
+      } else if (n == "xt.reduce_sum" || n == "xt.reduce_max") {
+        if (ta.rank() != 2) {
+          err = "reductions take rank-2 tiles (lib/xt/XTOps.cpp:274-307)";
+          return false;
+        }
+        int64_t axis = find_attr(o->attrs, "axis")->i;
+        if (axis < 0) axis += 2;
+        in.op = VmOp::Reduce;
+        in.kind = static_cast<int16_t>(n == "xt.reduce_sum" ? VmReduce::Sum : VmReduce::Max);
+        if (!pad3(ta.shape, in.dims, err)) return false;
+        in.aux[0] = static_cast<int>(axis);
+      } else {  // transpose / permute
+        in.op = VmOp::Permute;
+        if (!pad3(ta.shape, in.dims, err)) return false;
+        const int r = ta.rank(), off = 3 - r;
+        int perm[3] = {0, 1, 2};
+        if (n == "xt.transpose") {
+          if (r < 2) {
+            err = "transpose needs a tile of rank >= 2";
+            return false;
+          }
+          std::swap(perm[1], perm[2]);
+        } else {
+          const Attr* pa = find_attr(o->attrs, "permutation");
+          if (!pa || static_cast<int>(pa->ints.size()) != r) {
+            err = "permute needs a permutation attribute of the tile's rank";
+            return false;
+          }
+          for (int d = 0; d < r; ++d) perm[off + d] = static_cast<int>(pa->ints[d]) + off;
+        }
+        for (int d = 0; d < 3; ++d) in.aux[d] = perm[d];
+      }
+      auto sl = alloc(static_cast<int>(res.numel()));
+      slot[o->results[0]] = sl;
+      in.dst = sl.first;
+    }
+    vm.inst.push_back(in);
+    // free the slots whose last use was this op
+    for (int v : o->operands) {
+      if (!an.f.type_of(v).is_tensor()) continue;
+      const int r = root_of(v);
+      if (last_use[r] == i) release(r);
+    }
+  }
+  vm.lds_floats = high;
+  if (int64_t(high) * 4 > 160 * 1024) {
+    err = "tile program needs " + std::to_string((int64_t(high) * 4 + 1023) / 1024) +
+          " KB of LDS for its live tiles (at most 160 KB per workgroup)";
+    return false;
+  }
+  if (vm.inst.size() > 40 || vm.access.size() > 8) {
+    err = "tile program too long for the HIP interpreter (at most 40 instructions and 8 loads/stores)";
+    return false;
+  }
+  p.kind = PlanKind::TileVM;
+  p.vm = std::move(vm);
+  const double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
+  p.algo_bytes = blocks * bytes;
+  return true;
+}
+
 }  // namespace
 
 std::string Plan::describe() const {
@@ -530,6 +743,16 @@ std::string Plan::describe() const {
         if (gemm_ftoi) os << sep << "ftoi->i8";
       }
       break;
+    case PlanKind::TileVM: {
+      int loads = 0, stores = 0;
+      for (const VmInst& in : vm.inst) {
+        loads += in.op == VmOp::Load;
+        stores += in.op == VmOp::Store;
+      }
+      os << "tile_vm f32 insts=" << vm.inst.size() << " loads=" << loads << " stores=" << stores
+         << " lds=" << vm.lds_floats * 4 << "B";
+      break;
+    }
     case PlanKind::Conv2d:
       os << "conv2d_nhwc " << elem_name(conv.elem) << "->f32 tile=" << conv.TB << "x" << conv.TH
          << "x" << conv.TW << "x" << conv.CO << " filter=" << conv.KH << "x" << conv.KW << "x"
@@ -583,6 +806,7 @@ bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& 
   if (match_softmax(an, p, err) || !err.empty()) return err.empty();
   if (match_gemm(an, p, err) || !err.empty()) return err.empty();
   if (match_conv(an, p, err) || !err.empty()) return err.empty();
+  if (match_vm(an, p, err) || !err.empty()) return err.empty();
   std::ostringstream os;
   os << "unsupported tile program for the HIP backend: @" << f->name << " uses";
   for (const Op* o : an.compute) os << " " << o->name;

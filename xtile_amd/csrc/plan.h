@@ -40,7 +40,7 @@ struct Coord {
   int64_t value = 0;
 };
 
-enum class PlanKind { EwBinary, RowSoftmax, Gemm, Conv2d };
+enum class PlanKind { EwBinary, RowSoftmax, Gemm, Conv2d, TileVM };
 enum class EwOp { Add = 0, Sub = 1, Mul = 2 };
 
 struct ConvPlan {
@@ -54,6 +54,35 @@ struct ConvPlan {
   TileAddr filt_addr;                     // filter tile origin
   TileAddr out_addr;                      // stored tile origin in the output
   int64_t out_H = 0, out_W = 0, out_C = 0;  // output memref dims 1..3
+};
+
+// General f32 tile programs (anything without matmul / conv): the Block's
+// ops become a straight-line list of tile instructions over LDS slots, run by
+// one workgroup per Block (kernels/tilevm.hip).  Shapes are padded to rank 3
+// with leading 1s.
+enum class VmOp : int16_t { Load, Store, Unary, Binary, Reduce, Permute };
+enum class VmUnary : int16_t { Exp, Cos, Sin, Recip, Rsqrt, Sigmoid, Tanh, Silu };
+enum class VmBinary : int16_t { Add, Sub, Mul };
+enum class VmReduce : int16_t { Sum, Max };
+
+struct VmAccess {                 // a load or store tile against a memref argument
+  int arg = -1;
+  TileAddr addr;                  // tile origin (element offset), affine in the block id
+  int64_t stride[3] = {0, 0, 0};  // memref element strides of the tile's dims
+};
+
+struct VmInst {
+  VmOp op = VmOp::Load;
+  int16_t kind = 0;               // VmUnary / VmBinary / VmReduce, or the access index
+  int dst = 0, a = 0, b = 0;      // LDS float offsets of the operands' slots
+  int dims[3] = {1, 1, 1};        // result dims (Reduce, Permute: source dims)
+  int aux[3] = {1, 1, 1};         // Binary: rhs dims; Reduce: axis in aux[0]; Permute: perm
+};
+
+struct VmPlan {
+  std::vector<VmAccess> access;
+  std::vector<VmInst> inst;
+  int lds_floats = 0;             // LDS slots, in floats
 };
 
 struct Plan {
@@ -70,6 +99,7 @@ struct Plan {
   bool gemm_scale = false, gemm_bias = false, gemm_ftoi = false;
   Access2D scale, bias;
   ConvPlan conv;
+  VmPlan vm;
   double algo_bytes = 0;  // algorithmic HBM bytes per launch
   double algo_flops = 0;  // algorithmic FLOPs per launch
   std::string describe() const;

@@ -195,6 +195,7 @@ int xt_gpu_run(xt_module* m, const char* func, void* const* bufs, const size_t* 
     case xt::PlanKind::RowSoftmax: e = xtk::launch_row_softmax(p, bufs, s, why); break;
     case xt::PlanKind::Gemm: e = xtk::launch_gemm(p, bufs, s, why); break;
     case xt::PlanKind::Conv2d: e = xtk::launch_conv2d(p, bufs, s, why); break;
+    case xt::PlanKind::TileVM: e = xtk::launch_tilevm(p, bufs, s, why); break;
   }
   if (!why.empty()) return fail(err, XT_ERR_ARGUMENT, why);
   if (e != hipSuccess)

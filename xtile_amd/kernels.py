@@ -17,6 +17,7 @@ from __future__ import annotations
 
 from . import (
     Array,
+    add as tile_add,
     astype,
     bfloat16,
     bid,
@@ -31,7 +32,11 @@ from . import (
     load_conv2d,
     matmul,
     max as tile_max,
+    mul as tile_mul,
+    reciprocal,
+    rsqrt,
     store,
+    sub as tile_sub,
     sum as tile_sum,
 )
 
@@ -217,6 +222,73 @@ def conv2d(n, h, w, cin, cout, kh=3, kw=3, tile_h=4, tile_w=56, dtype=float16, p
         grid=(n, oh // tile_h, ow // tile_w),
         double_buffering=True,
     )
+
+
+# -- programs for the tile interpreter ----------------------------------------
+
+
+@kernel
+def layernorm_kernel(inp, gamma, beta, inv_n, eps, out, trow, col):
+    """Row layernorm, the xt form of the reference's layernorm program
+    (test/nova/to_x1.mlir:82-128: reduce, broadcast subtract, square, reduce,
+    scale by 1/C plus epsilon, rsqrt, scale by gamma, add beta).  The DSL has
+    no scalar operands, so 1/C and epsilon are (1, 1) tiles."""
+    row = bid(0)
+    x = load(inp, index=(row, 0), shape=(trow, col))
+    g = load(gamma, index=(0, 0), shape=(1, col), shared=1)
+    b = load(beta, index=(0, 0), shape=(1, col), shared=1)
+    n = load(inv_n, index=(0, 0), shape=(1, 1), shared=1)
+    e = load(eps, index=(0, 0), shape=(1, 1), shared=1)
+    mean = tile_mul(tile_sum(x, axis=1), n)
+    xc = tile_sub(x, mean)
+    var = tile_mul(tile_sum(tile_mul(xc, xc), axis=1), n)
+    r = rsqrt(tile_add(var, e))
+    y = tile_add(tile_mul(tile_mul(xc, r), g), b)
+    store(out, index=(row, 0), tile=y)
+
+
+def layernorm(rows: int, cols: int, trow: int = 64):
+    if rows % trow:
+        raise ValueError("trow must divide rows")
+    a = Array(shape=(rows, cols), dtype=float32)
+    v = Array(shape=(1, cols), dtype=float32)
+    s = Array(shape=(1, 1), dtype=float32)
+    return convert(layernorm_kernel, args=(a, v, v, s, s, a, trow, cols), grid=(rows // trow, 1, 1),
+                   double_buffering=True)
+
+
+@kernel
+def column_softmax_kernel(inp, out, row, tcol):
+    """Softmax down the columns of a (row, tcol) tile: reductions over axis 0."""
+    c = bid(0)
+    x = load(inp, index=(0, c), shape=(row, tcol))
+    m = tile_max(x, axis=0)
+    ex = exp(tile_sub(x, m))
+    y = tile_mul(ex, reciprocal(tile_sum(ex, axis=0)))
+    store(out, index=(0, c), tile=y)
+
+
+def column_softmax(rows: int, cols: int, tcol: int = 32):
+    if cols % tcol:
+        raise ValueError("tcol must divide cols")
+    a = Array(shape=(rows, cols), dtype=float32)
+    return convert(column_softmax_kernel, args=(a, a, rows, tcol), grid=(cols // tcol, 1, 1))
+
+
+@kernel
+def bias_add_kernel(inp, bias, out, trow, tcol):
+    """x + bias with a (1, tcol) bias row broadcast over the tile's rows."""
+    r = bid(0)
+    c = bid(1)
+    x = load(inp, index=(r, c), shape=(trow, tcol))
+    b = load(bias, index=(0, c), shape=(1, tcol), shared=1)
+    store(out, index=(r, c), tile=tile_add(x, b))
+
+
+def bias_add(rows: int, cols: int, trow: int = 32, tcol: int = 64):
+    a = Array(shape=(rows, cols), dtype=float32)
+    v = Array(shape=(1, cols), dtype=float32)
+    return convert(bias_add_kernel, args=(a, v, a, trow, tcol), grid=(rows // trow, cols // tcol, 1))
 
 
 CONFIGS = {
