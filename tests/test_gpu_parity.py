@@ -183,6 +183,54 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
     assert frob_rel(got, want) <= MM_FROB
 
 
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil",
+    [
+        (1, 32, 64, 128, 64, 3, 3, 32, 64, (1, 1, 1, 1), (1, 1), (1, 1)),  # kernels/conv2d.py defaults
+        (2, 16, 24, 64, 32, 3, 3, 8, 12, (1, 1, 1, 1), (2, 2), (1, 1)),
+        (1, 20, 20, 64, 128, 3, 3, 4, 20, (2, 2, 2, 2), (1, 1), (2, 2)),
+        (3, 9, 12, 64, 64, 1, 1, 3, 12, (0, 0, 0, 0), (1, 1), (1, 1)),
+        (2, 11, 13, 64, 64, 3, 3, 3, 7, (0, 1, 2, 1), (2, 2), (1, 1)),
+    ],
+)
+def test_conv2d_i8_bit_exact(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil):
+    """The reference's own load_conv2d dtype (xtile/dsl.py:284-285): i8 source
+    and filter, f32 result.  The i32 MFMA sum is exact and is rounded to f32
+    once, as the oracle rounds its exact double sum, so the result is
+    bit-exact."""
+    rng = np.random.default_rng(6)
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.int8, pad=pad, stride=stride, dilation=dil)
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
+    x = rng.integers(-128, 128, (n, h, w, cin), dtype=np.int8)
+    f = rng.integers(-128, 128, (kh, kw, cin, cout), dtype=np.int8)
+    planted = kh == 3 and kw == 3 and cin == 128 and stride == (1, 1) and dil == (1, 1)
+    if planted:
+        # an odd sum above 2^24 at output (5, 5), channel 0: the i32 -> f32
+        # conversion must round it (127 * 127 * 1151 + 126 * 127 = 18580481)
+        x[0, 4:7, 4:7, :] = 127
+        x[0, 4, 4, 0] = 126
+        f[:, :, :, 0] = 127
+    o = np.zeros((n, oh, ow, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], ["i8", "i8", "f32"], cuda,
+                  case=f"conv i8 {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert np.array_equal(got, want)
+    if planted:
+        assert want[0, 5, 5, 0] == np.float32(18580481.0) and float(want[0, 5, 5, 0]) != 18580481.0
+
+
+def test_conv2d_i8_outside_the_band_kernel_is_refused(cuda):
+    import torch
+
+    mod = K.conv2d(1, 8, 8, 32, 32, 3, 3, 4, 8, dtype=xt.int8)
+    x = torch.zeros((1, 8, 8, 32), dtype=torch.int8, device=cuda)
+    f = torch.zeros((3, 3, 32, 32), dtype=torch.int8, device=cuda)
+    o = torch.zeros((1, 8, 8, 32), dtype=torch.float32, device=cuda)
+    with pytest.raises(ValueError, match="i8 conv2d runs on the band kernel only"):
+        xt.launch(mod, x, f, o)
+
+
 def test_conv2d_filter_too_large_is_refused(cuda):
     """The whole filter lives in LDS; a 5x5x64x80 filter (411 KB transposed)
     cannot, and the launch is refused on the host before any kernel runs."""

@@ -459,50 +459,83 @@ struct BandArgs {
   int bands_per_image;
   int rf_w;              // halo columns
   int K, steps;          // K = KH*KW*C, steps = K / 16
-  int rb_shift;          // log2(2 * Cout): bytes per filter row
-  int fsw_shift, fsw_mask;  // filter chunk swizzle: 4 * ((k >> shift) & mask)
+  int rb_shift;          // log2(bytes per filter row)
+  int fsw_unit, fsw_shift, fsw_mask;  // filter chunk swizzle: unit * ((k >> shift) & mask)
   int pitch;             // LDS bytes per halo pixel: 2*Cin (+16 to make the chunk count odd)
+  int nch;               // 16-byte data chunks per halo pixel: Cin * esize / 16
   int nchp;              // pitch / 16
   int ppi;               // halo pixels per DMA instruction: 64 / nchp
   Magic m_nchp, m_rfw, m_ow;
   int filt_instr;        // 1 KB DMA runs of the filter
-  unsigned filt_bytes;   // K*CO*2 (LDS offset of the halo)
-  unsigned image_bytes;  // H*W*C*2
+  unsigned filt_bytes;   // K*CO*esize (LDS offset of the halo)
+  unsigned image_bytes;  // H*W*C*esize
 };
 
-template <bool BF16>
-__device__ __forceinline__ float16v band_mfma(short8 a, short8 b, float16v c) {
-  return mfma32<BF16>(a, b, c);
+enum { kBandF16 = 0, kBandBF16 = 1, kBandI8 = 2 };
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef int int16v __attribute__((ext_vector_type(16)));
+typedef int int2v __attribute__((ext_vector_type(2)));
+
+// f16 / bf16 accumulate in f32; i8 in i32 (exact), converted to f32 when stored.
+template <int ELEM>
+struct BandAcc {
+  typedef float16v type;
+};
+template <>
+struct BandAcc<kBandI8> {
+  typedef int16v type;
+};
+
+// One K step of 32 bytes per pixel: 16 f16 / bf16 values or 32 i8 values.
+template <int ELEM>
+__device__ __forceinline__ typename BandAcc<ELEM>::type band_mfma(short8 a, short8 b,
+                                                                 typename BandAcc<ELEM>::type c) {
+  if constexpr (ELEM == kBandI8)
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(int4v, a), __builtin_bit_cast(int4v, b), c, 0,
+                                                 0, 0);
+  else
+    return mfma32<ELEM == kBandBF16>(a, b, c);
 }
 
 typedef __attribute__((address_space(3))) unsigned char band_lds_t;
 
 // MI M tiles of the band (first pixel q0, then every tstride pixels) against
 // N tile j, all in one pass so that each filter fragment feeds MI MFMAs.  K
-// runs in steps of 16: tap s / (Cin/16), channels 16 * (s % (Cin/16)).  The
-// fragments of step s+1 are read while the MFMAs of step s run.  Pixels at or
-// past qend are computed on clamped addresses and not stored.
-template <int MI, bool BF16>
+// runs in steps of 32 bytes per pixel (16 f16 / bf16 or 32 i8 channels): tap
+// s / cs_per_tap, channel step s % cs_per_tap.  The fragments of step s+1 are
+// read while the MFMAs of step s run.  Pixels at or past qend are computed on
+// clamped addresses and not stored.
+template <int MI, int ELEM>
 __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* Fs, const band_lds_t* Hs,
                                            __amdgpu_buffer_rsrc_t orc, int q0, int tstride, int qend, int j,
                                            int lane) {
   const int lr = lane & 31, hi = lane >> 5;
   const int g = lane >> 4, li = lane & 15;
-  const int RB = p.CO * 2;
-  const int cs_per_tap = p.C / 16;
-  // Filter fragment: two transposed 4x16 reads (K rows fk, fk + 4 of the
-  // step).  A step moves 16 rows, which leaves the row swizzle unchanged, so
-  // each read is a per-lane constant plus 16 * RB * s.
+  constexpr int ES = ELEM == kBandI8 ? 1 : 2;  // bytes per element
+  constexpr int RS = 32 / ES;                  // K rows per step
+  const int RB = p.CO * ES;
+  const int cs_per_tap = p.C * ES / 32;
+  // Filter fragment: two transposed reads per step.  16-bit: each 16-lane
+  // group reads a 4 (K) x 16 (Cout) block, lane i at K row i/4 and columns
+  // 4*(i%4)..+3 (ds_read_b64_tr_b16).  8-bit: an 8 x 16 block, lane i at K row
+  // i/2 and columns 8*(i%2)..+7 (ds_read_b64_tr_b8).  A step moves RS rows,
+  // which leaves the row swizzle unchanged, so each read is a per-lane
+  // constant plus RS * RB * s.
   int boff[2];
-  {
-    const int ncol = 32 * j + 16 * (g & 1) + 4 * (li & 3);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
-      boff[h] = k * RB + (((ncol >> 3) ^ (4 * ((k >> p.fsw_shift) & p.fsw_mask))) << 4) + (ncol & 7) * 2;
+  for (int h = 0; h < 2; ++h) {
+    int k, ncol;
+    if constexpr (ELEM == kBandI8) {
+      k = 16 * (g >> 1) + 8 * h + (li >> 1);
+      ncol = 32 * j + 16 * (g & 1) + 8 * (li & 1);
+    } else {
+      k = 8 * (g >> 1) + 4 * h + (li >> 2);
+      ncol = 32 * j + 16 * (g & 1) + 4 * (li & 3);
     }
+    const int cb = ncol * ES;  // byte column
+    boff[h] = k * RB + (((cb >> 4) ^ (p.fsw_unit * ((k >> p.fsw_shift) & p.fsw_mask))) << 4) + (cb & 15);
   }
-  const int bstep = 16 * RB;
+  const int bstep = RS * RB;
   // Pixel fragment of tile t at tap offset `tapoff` (halo pixels) and channel
   // step cs: Hs + (hp0 + tapoff) * pitch + 16 * (2 * cs + hi).
   int hbase[MI];
@@ -522,18 +555,26 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
 #pragma unroll
     for (int t = 0; t < MI; ++t)
       a[t] = *reinterpret_cast<const short8 __attribute__((address_space(3)))*>(Hs + base[t] + cs * 32);
-    const band_lds_t* f = Fs + s * bstep;
-    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<short4v __attribute__((address_space(3)))*>(const_cast<band_lds_t*>(f) + boff[0]));
-    const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        reinterpret_cast<short4v __attribute__((address_space(3)))*>(const_cast<band_lds_t*>(f) + boff[1]));
-    b = short8{lo[0], lo[1], lo[2], lo[3], h4[0], h4[1], h4[2], h4[3]};
+    band_lds_t* f = const_cast<band_lds_t*>(Fs) + s * bstep;
+    if constexpr (ELEM == kBandI8) {
+      const int2v lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[0]));
+      const int2v h4 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[1]));
+      b = __builtin_bit_cast(short8, int4v{lo[0], lo[1], h4[0], h4[1]});
+    } else {
+      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[0]));
+      const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[1]));
+      b = short8{lo[0], lo[1], lo[2], lo[3], h4[0], h4[1], h4[2], h4[3]};
+    }
   };
-  float16v acc[MI];
+  typename BandAcc<ELEM>::type acc[MI];
 #pragma unroll
   for (int t = 0; t < MI; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[t][v] = 0.f;
+    for (int v = 0; v < 16; ++v) acc[t][v] = 0;
 
   // Cin / 16 is even, so steps s and s+1 share a tap.  The loop body has no
   // branch: the tap advance is a pair of selects and the read-ahead of step
@@ -551,7 +592,7 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
     read(s + 1, cs + 1, a1, b1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<BF16>(a0[t], b0, acc[t]);
+    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<ELEM>(a0[t], b0, acc[t]);
     __builtin_amdgcn_sched_barrier(0);
     cs += 2;
     const bool tap_end = cs == cs_per_tap;
@@ -565,7 +606,7 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
     read(last ? p.steps - 1 : s + 2, last ? cs_per_tap - 1 : cs, a0, b0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<BF16>(a1[t], b1, acc[t]);
+    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<ELEM>(a1[t], b1, acc[t]);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -579,15 +620,16 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
       const int q = q0 + t * tstride + 8 * (v >> 2) + 4 * hi + (v & 3);
       const unsigned off = q < qend ? (unsigned)((q * p.CO + 32 * j + lr) * 4) : kOutOfRange;
       // the element goes through a scalar: __builtin_bit_cast of an
-      // ext_vector element lvalue reads element 0 whatever the index
-      const float val = acc[t][v];
+      // ext_vector element lvalue reads element 0 whatever the index.  An
+      // i8 sum is an exact i32; it is rounded to f32 once (nearest even).
+      const float val = static_cast<float>(acc[t][v]);
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), orc, off, 0, 2);
     }
 }
 
 // Tiles m0, m0 + mstep, ... (< nmt) of pixels [qbeg, qend) against N tile j,
 // up to four per pass.
-template <bool BF16>
+template <int ELEM>
 __device__ __forceinline__ void band_wave(const BandArgs& p, const band_lds_t* Fs, const band_lds_t* Hs,
                                           __amdgpu_buffer_rsrc_t orc, int qbeg, int qend, int m0, int mstep,
                                           int j, int lane) {
@@ -598,17 +640,17 @@ __device__ __forceinline__ void band_wave(const BandArgs& p, const band_lds_t* F
   while (n > 0) {
     const int c = min(n, 4);
     switch (c) {
-      case 1: band_tiles<1, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
-      case 2: band_tiles<2, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
-      case 3: band_tiles<3, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
-      default: band_tiles<4, BF16>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 1: band_tiles<1, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 2: band_tiles<2, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 3: band_tiles<3, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      default: band_tiles<4, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
     }
     q0 += c * tstride;
     n -= c;
   }
 }
 
-template <int NT, bool BF16>
+template <int NT, int ELEM>
 __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char blds[];
   typedef __attribute__((address_space(3))) unsigned char lds_t;
@@ -629,7 +671,7 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
       const unsigned b = (unsigned)i * 1024u + lane * 16u;
       const int k = b >> p.rb_shift;
       const int pos = (b - (k << p.rb_shift)) >> 4;
-      const int chunk = pos ^ (4 * ((k >> p.fsw_shift) & p.fsw_mask));
+      const int chunk = pos ^ (p.fsw_unit * ((k >> p.fsw_shift) & p.fsw_mask));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(fr, (void __attribute__((address_space(3)))*)(Fs + i * 1024),
                                                16, (unsigned)((k << p.rb_shift) + chunk * 16), 0, 0, 0);
     }
@@ -643,7 +685,7 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
     const int lp = (int)udiv((unsigned)lane, p.m_nchp);
     const int lc = lane - lp * p.nchp;
     const bool lane_on = lp < p.ppi;
-    const int nch = p.C / 8;
+    const int nch = p.nch;
     const int hinstr = (hpix + p.ppi - 1) / p.ppi;
     for (int i = wave; i < hinstr; i += BWG / 64) {
       const int q = i * p.ppi + lp;
@@ -666,7 +708,7 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
   const __amdgpu_buffer_rsrc_t orc =
       buffer_of(p.out + ((size_t)n * p.OH + r0) * p.OW * p.CO, (unsigned)(M * p.CO * 4));
 
-  band_wave<BF16>(p, Fs, Hs, orc, 0, M, wave / NT, MSTEP, j, lane);
+  band_wave<ELEM>(p, Fs, Hs, orc, 0, M, wave / NT, MSTEP, j, lane);
 }
 
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
@@ -687,10 +729,10 @@ hipError_t launch_conv_t(const ConvArgs& a, dim3 grid, size_t lds, hipStream_t s
   return hipGetLastError();
 }
 
-template <int NT, bool BF16>
+template <int NT, int ELEM>
 hipError_t launch_band_t(const BandArgs& a, int bands, size_t lds, hipStream_t s) {
   static std::atomic<int> configured{0};
-  auto fn = conv2d_band_kernel<NT, BF16>;
+  auto fn = conv2d_band_kernel<NT, ELEM>;
   if (static_cast<int>(lds) > configured.load()) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -725,11 +767,14 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
   if (c.filt_addr.c0 || c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz) return false;
-  if (c.C % 16 || c.CO % 32 || c.CO > 128 || c.CO == 96) return false;
+  const bool i8 = c.elem == xt::Elem::I8;
+  const long long es = i8 ? 1 : 2;
+  // a K step is 32 bytes of a pixel; steps go in pairs within a tap
+  if ((c.C * es) % 64 || c.CO % 32 || c.CO > 128 || c.CO == 96) return false;
   const long long K = c.KH * c.KW * c.C;
-  const long long filt_bytes = K * c.CO * 2;
+  const long long filt_bytes = K * c.CO * es;
   if (filt_bytes % 1024) return false;
-  const long long PB = c.C * 2;
+  const long long PB = c.C * es;
   // LDS pitch of a halo pixel: an odd number of 16-byte chunks
   const long long pitch = (PB / 16) % 2 ? PB : PB + 16;
   const long long nchp = pitch / 16;
@@ -780,14 +825,18 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   a.bands_per_image = (int)((c.out_H + R - 1) / R);
   a.rf_w = (int)rf_w;
   a.K = (int)K;
-  a.steps = (int)(K / 16);
-  // filter rows of RB = 2*Cout bytes: the transposed reads of one half-wave
-  // cover 64 bytes of four consecutive rows; XOR the 64-byte block index
-  // with the row's position inside a 256-byte bank window
-  const int RB = a.CO * 2;
+  a.steps = (int)(K * es / 32);
+  // Filter rows of RB = Cout * esize bytes.  The transposed reads of one
+  // half-wave cover 64 bytes of four consecutive rows (16-bit) or 32 bytes of
+  // eight rows (8-bit); XOR that block index with the row's position inside
+  // a 256-byte bank window so the rows fall in distinct banks.
+  const int RB = (int)(a.CO * es);
+  const int blk = i8 ? 32 : 64;
   a.rb_shift = ilog2((unsigned)RB);
+  a.fsw_unit = blk / 16;
   a.fsw_shift = ilog2(256 / RB);
-  a.fsw_mask = RB / 64 - 1;
+  a.fsw_mask = RB / blk - 1;
+  a.nch = (int)(PB / 16);
   a.pitch = (int)pitch;
   a.nchp = (int)nchp;
   a.ppi = (int)ppi;
@@ -799,13 +848,18 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   a.image_bytes = (unsigned)image_bytes;
   const long long bands = gB * a.bands_per_image;
   if (bands > 0x7fffffff) return false;
-  const bool bf16 = c.elem == xt::Elem::BF16;
+  const int el = i8 ? kBandI8 : c.elem == xt::Elem::BF16 ? kBandBF16 : kBandF16;
   const int nt = a.CO / 32;
-#define XT_BAND(NTV, BFV) e = launch_band_t<NTV, BFV>(a, (int)bands, lds, s)
+#define XT_BAND(NTV)                                                             \
+  do {                                                                          \
+    if (el == kBandI8) e = launch_band_t<NTV, kBandI8>(a, (int)bands, lds, s);   \
+    else if (el == kBandBF16) e = launch_band_t<NTV, kBandBF16>(a, (int)bands, lds, s); \
+    else e = launch_band_t<NTV, kBandF16>(a, (int)bands, lds, s);                \
+  } while (0)
   switch (nt) {
-    case 1: if (bf16) XT_BAND(1, true); else XT_BAND(1, false); break;
-    case 2: if (bf16) XT_BAND(2, true); else XT_BAND(2, false); break;
-    default: if (bf16) XT_BAND(4, true); else XT_BAND(4, false); break;
+    case 1: XT_BAND(1); break;
+    case 2: XT_BAND(2); break;
+    default: XT_BAND(4); break;
   }
 #undef XT_BAND
   return true;
@@ -873,6 +927,11 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   if (try_band(p, bufs, s, max_lds, cus, e)) return e;
+  if (c.elem == xt::Elem::I8) {
+    why = "i8 conv2d runs on the band kernel only, which needs Blocks tiling the whole output, Cin % 64 == 0, "
+          "Cout in {32, 64, 128} and the filter plus one band's halo within LDS";
+    return hipErrorInvalidValue;
+  }
   // Largest work unit (rows dividing TH) whose halo fits beside the filter.
   const int ntp = nt == 3 ? 4 : nt;  // N tiles compiled: 1, 2 or 4
   const size_t filt_bytes = size_t(ntp) * 32 * a.kpitch;

@@ -8,7 +8,7 @@
 //              (kernels/softmax.py:10-19; test/python/dsl_convert.py:25-40)
 //   Gemm       store([ftoi]((matmul(load A, load B) [* load S]) [+ load Bias]))
 //              f16/bf16/i8 in, f32 or i8 out (kernels/matmul.py:6-19)
-//   Conv2d     store(load_conv2d(S, load F))         f16/bf16 in, f32 out
+//   Conv2d     store(load_conv2d(S, load F))         i8/f16/bf16 in, f32 out
 //              (kernels/conv2d.py:10-37; conv slice math lib/xt/XTToNova.cpp:110-142)
 #include "plan.h"
 
@@ -389,8 +389,11 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
   const Type& fm = an.f.type_of(lf->operands[0]);
   const Type& res = an.f.type_of(cv->results[0]);
   const Type& outm = an.f.type_of(st->operands[1]);
-  if (!((src.elem == Elem::F16 || src.elem == Elem::BF16) && res.elem == Elem::F32)) {
-    err = "the HIP conv2d kernel takes f16 or bf16 source/filter with an f32 result";
+  // i8 is the reference's own load_conv2d dtype (xtile/dsl.py:284-285); f16
+  // and bf16 are the narrow-float extension
+  if (!((src.elem == Elem::F16 || src.elem == Elem::BF16 || src.elem == Elem::I8) &&
+        ft.elem == src.elem && res.elem == Elem::F32)) {
+    err = "the HIP conv2d kernels take i8, f16 or bf16 source and filter of one type with an f32 result";
     return false;
   }
   if (ft.shape != fm.shape) {
