@@ -208,7 +208,7 @@ def _run_line(path: Path) -> str:
 
 
 @pytest.mark.skipif(not REF_TESTS.exists(), reason="reference tree not mounted (build container only)")
-@pytest.mark.parametrize("name", ["parse", "serialize", "canonicalize", "invalid", "serialize_invalid"])
+@pytest.mark.parametrize("name", ["parse", "serialize", "canonicalize", "invalid", "serialize_invalid", "to_nova"])
 def test_reference_lit_file(name, tmp_path):
     """Run the reference's own lit test through this xt-opt and FileCheck."""
     path = REF_TESTS / f"{name}.mlir"

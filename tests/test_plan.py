@@ -109,15 +109,33 @@ func.func @k(%a: memref<64x64xf16>, %b: memref<64x64xf16>, %c: memref<64x64xf32>
 
 
 def test_nova_stages_raise():
+    m = xt.xt_to_nova(K.add(64, 64, 32, 32))
     with pytest.raises(NotImplementedError, match="x1 NPU lowering"):
-        xt.xt_to_nova(K.add(64, 64, 32, 32))
+        xt.nova_optimize(m)
+
+
+def test_xt_to_nova_returns_the_same_module():
+    """test/python/to_nova.py: the wrapper is returned, its text lowered."""
+    m = xt.parse(
+        """
+        module {
+          func.func @main(%arg0: tensor<4xf32>) -> tensor<4xf32> {
+            %0 = xt.add(%arg0, %arg0) : tensor<4xf32>, tensor<4xf32> -> tensor<4xf32>
+            func.return %0 : tensor<4xf32>
+          }
+        }
+        """
+    )
+    assert xt.xt_to_nova(m) is m
+    assert "nova.elementwise 1 %arg0, %arg0" in str(m)
 
 
 def test_save_compile_results(tmp_path, capsys):
     m = K.add(64, 128, 32, 64)
     xt.save_compile_results(m, str(tmp_path / "add"))
     files = sorted(p.name for p in (tmp_path / "add").iterdir())
-    assert files == ["0_xt.mlir", "1_hip_plan.txt", "2_xt_serialize.mlir"]
+    assert files == ["0_xt.mlir", "1_hip_plan.txt", "2_xt_serialize.mlir", "3_xt_to_nova.mlir"]
+    assert "nova.elementwise" in (tmp_path / "add" / "3_xt_to_nova.mlir").read_text()
     assert "ew_binary" in (tmp_path / "add" / "1_hip_plan.txt").read_text()
     assert "compiled kernel ->" in capsys.readouterr().out
 

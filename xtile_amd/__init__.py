@@ -2,9 +2,10 @@
 
 The public API mirrors the reference package's facade (xtile/__init__.py):
 the DSL (``kernel, bid, load, load_conv2d, store, add, ... , convert``), the
-module wrapper ``Module``, ``parse``, ``xt_serialize``, ``compile``,
-``save_ir``, ``save_compile_results`` and ``cdiv``.  Where the reference lowers
-a program to command text for its "x1" NPU, this package plans and launches
+module wrapper ``Module``, ``parse``, ``xt_serialize``, ``xt_to_nova``,
+``compile``, ``save_ir``, ``save_compile_results`` and ``cdiv``.  Where the
+reference lowers nova further to command text for its "x1" NPU (the
+``nova_*`` stages, which raise here), this package plans and launches
 hand-written HIP kernels: ``compile`` validates and plans the launch, and
 ``launch`` runs the program on the GPU over caller-owned device tensors.
 
@@ -112,6 +113,14 @@ def canonicalize(module: Any):
     return _after_pass(module, _native.canonicalize(module))
 
 
+def xt_to_nova(module: Any):
+    """Lower xt ops to the nova dialect (lib/xt/XTToNova.cpp): tile offsets
+    resolved to start indices, conv halo slices, unit affines; mutates and
+    returns `module`.  An IR-level stage only: the HIP kernels launch from
+    the xt form."""
+    return _after_pass(module, _native.xt_to_nova(module))
+
+
 def _x1_unavailable(name: str):
     def stage(module: Any):
         raise NotImplementedError(
@@ -123,7 +132,6 @@ def _x1_unavailable(name: str):
     return stage
 
 
-xt_to_nova = _x1_unavailable("xt_to_nova")
 nova_optimize = _x1_unavailable("nova_optimize")
 nova_threading = _x1_unavailable("nova_threading")
 nova_barrier = _x1_unavailable("nova_barrier")
@@ -227,8 +235,8 @@ def save_compile_results(ir: object, save_dir: str) -> None:
 
     Stage files follow the reference's numbering (xtile/__init__.py:186-205)
     for the stages this backend has: 0_xt.mlir, then 1_hip_plan.txt (the
-    kernel that `launch` would run), then 2_xt_serialize.mlir (which mutates
-    `ir`, as in the reference)."""
+    kernel that `launch` would run), then 2_xt_serialize.mlir and
+    3_xt_to_nova.mlir (both mutate `ir`, as in the reference)."""
     os.makedirs(save_dir, exist_ok=True)
     save_ir(ir, os.path.join(save_dir, "0_xt.mlir"))
     lines = []
@@ -242,6 +250,8 @@ def save_compile_results(ir: object, save_dir: str) -> None:
         f.write("\n".join(lines) + "\n")
     ir = xt_serialize(ir)
     save_ir(ir, os.path.join(save_dir, "2_xt_serialize.mlir"))
+    ir = xt_to_nova(ir)
+    save_ir(ir, os.path.join(save_dir, "3_xt_to_nova.mlir"))
     print("compiled kernel ->", save_dir)
 
 

@@ -188,6 +188,10 @@ def canonicalize(module: object) -> object:
     return _run_pass(module, "canonicalize")
 
 
+def xt_to_nova(module: object) -> object:
+    return _run_pass(module, "xt-to-nova")
+
+
 def _module_asm(module: object) -> str:
     handle = _unwrap(module)
     out = ctypes.c_void_p()

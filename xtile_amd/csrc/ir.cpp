@@ -1156,6 +1156,7 @@ struct Printer {
     };
     auto it = op_table().find(o.name);
     Fmt fmt = it == op_table().end() ? Fmt::Functional : it->second.fmt;
+    if (o.name.rfind("nova.", 0) == 0) return out + nova(o);
     if (o.name == "func.return") {
       out += "return";
       if (!o.operands.empty()) out += " " + refs(o.operands) + " : " + types_of(o.operands);
@@ -1199,6 +1200,57 @@ struct Printer {
         break;
     }
     return out;
+  }
+
+  // Assembly forms of the reference's nova ops that xt-to-nova produces
+  // (include/nova/NovaOps.td of the reference; test/xt/to_nova.mlir).
+  std::string nova(const Op& o) const {
+    auto i64 = [&](const char* name) {
+      const Attr* a = find_attr(o.attrs, name);
+      return a ? a->i : 0;
+    };
+    auto flt = [&](const char* name) {
+      const Attr* a = find_attr(o.attrs, name);
+      return format_float(a ? a->f : 0.0);
+    };
+    auto list = [&](const char* name) {
+      const Attr* a = find_attr(o.attrs, name);
+      return a ? a->str() : std::string("[]");
+    };
+    auto res = [&]() { return o.results.empty() ? std::string("()") : f.type_of(o.results[0]).str(); };
+    const std::string& n = o.name;
+    std::string out = n;
+    if (n == "nova.reduce") {
+      out += " " + std::to_string(i64("mode")) + " " + refs(o.operands) + " {axis = " + std::to_string(i64("axis")) +
+             " : i64} : " + types_of(o.operands) + " -> " + res();
+    } else if (n == "nova.broadcast" || n == "nova.elementwise") {
+      out += " " + std::to_string(i64("mode")) + " " + refs(o.operands) + " lhs " + flt("lhs_a") + " " +
+             flt("lhs_b") + " rhs " + flt("rhs_a") + " " + flt("rhs_b") + " : " + types_of(o.operands) + " -> " +
+             res();
+    } else if (n == "nova.scalar") {
+      out += " " + std::to_string(i64("mode")) + " " + refs(o.operands) + ", " + flt("rhs") + " : " +
+             types_of(o.operands) + " -> " + res();
+    } else if (n == "nova.load") {
+      out += " " + refs(o.operands) + " " + list("start") + attr_dict_text_pad(o.attrs, {"start"}) + " : " +
+             types_of(o.operands) + " -> " + res();
+    } else if (n == "nova.store") {
+      out += " " + refs(o.operands) + " " + list("start") + attr_dict_text_pad(o.attrs, {"start"}) + " : (" +
+             types_of(o.operands) + ") -> ()";
+    } else if (n == "nova.conv2d") {
+      out += " " + refs(o.operands) + " group " + std::to_string(i64("group")) + " pad " + list("pad") +
+             " stride " + list("stride") + " dilation " + list("dilation") + " : " + types_of(o.operands) + " -> " +
+             res();
+    } else if (n == "nova.permute") {
+      out += " " + refs(o.operands) + " " + list("permutation") + " : " + types_of(o.operands) + " -> " + res();
+    } else {  // nova.matmul and the unary forms
+      out += " " + refs(o.operands) + " : " + types_of(o.operands) + " -> " + res();
+    }
+    return out;
+  }
+
+  static std::string attr_dict_text_pad(const AttrDict& d, const std::vector<std::string>& skip) {
+    std::string a = attr_dict_text(d, skip);
+    return a.empty() ? a : " " + a;
   }
 
   std::string func(const std::string& indent) const {

@@ -144,6 +144,8 @@ std::string print_module(const Module& m);
 // Passes.  Each mutates the module in place and returns false on failure.
 bool pass_xt_serialize(Module& m, Diag& diag);
 bool pass_canonicalize(Module& m, Diag& diag);
+// lib/xt/XTToNova.cpp restated: xt ops -> the reference's nova ops (printing only)
+bool pass_xt_to_nova(Module& m, Diag& diag);
 
 // Helpers shared by passes and the launch planner.
 const Func* find_func(const Module& m, const std::string& name);

@@ -94,6 +94,7 @@ int xt_pass_run(xt_module* m, const char* pass, char** err) {
   bool ok;
   if (name == "xt-serialize") ok = xt::pass_xt_serialize(*m->ir, diag);
   else if (name == "canonicalize") ok = xt::pass_canonicalize(*m->ir, diag);
+  else if (name == "xt-to-nova") ok = xt::pass_xt_to_nova(*m->ir, diag);
   else return fail(err, XT_ERR_TYPE, "unknown pass '" + name + "'");
   if (ok) ok = xt::verify_module(*m->ir, diag);
   if (!ok) {

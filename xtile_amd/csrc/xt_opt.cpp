@@ -1,7 +1,7 @@
 // xt-opt: MLIR-free driver for the `xt` subset.  Mirrors the command line the
 // reference's lit tests use (xt-opt/xt-opt.cpp:18-33, test/lit.cfg.py:22):
 //
-//   xt-opt [--xt-serialize] [--canonicalize] [--split-input-file] [-o out] [file|-]
+//   xt-opt [--xt-serialize] [--canonicalize] [--xt-to-nova] [--split-input-file] [-o out] [file|-]
 //
 // Each input chunk is parsed and verified, the requested passes run in the
 // order given, and the result is printed.  Diagnostics go to stderr as
@@ -19,7 +19,7 @@
 
 static void usage() {
   std::fprintf(stderr,
-               "usage: xt-opt [--xt-serialize] [--canonicalize] [--split-input-file] "
+               "usage: xt-opt [--xt-serialize] [--canonicalize] [--xt-to-nova] [--split-input-file] "
                "[-o <file>] [<file>|-]\n");
 }
 
@@ -31,6 +31,7 @@ int main(int argc, char** argv) {
     std::string a = argv[k];
     if (a == "--xt-serialize" || a == "-xt-serialize") passes.push_back("xt-serialize");
     else if (a == "--canonicalize" || a == "-canonicalize") passes.push_back("canonicalize");
+    else if (a == "--xt-to-nova" || a == "-xt-to-nova") passes.push_back("xt-to-nova");
     else if (a == "--split-input-file" || a == "-split-input-file") split = true;
     else if (a == "-o" && k + 1 < argc) output = argv[++k];
     else if (a == "-h" || a == "--help") {
@@ -78,6 +79,7 @@ int main(int argc, char** argv) {
       if (!ok) break;
       if (p == "xt-serialize") ok = xt::pass_xt_serialize(*m, diag);
       else if (p == "canonicalize") ok = xt::pass_canonicalize(*m, diag);
+      else if (p == "xt-to-nova") ok = xt::pass_xt_to_nova(*m, diag);
       if (ok) ok = xt::verify_module(*m, diag);
     }
     if (!ok) {
