@@ -220,28 +220,98 @@ def test_conv2d_i8_bit_exact(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stri
         assert want[0, 5, 5, 0] == np.float32(18580481.0) and float(want[0, 5, 5, 0]) != 18580481.0
 
 
-def test_conv2d_i8_outside_the_band_kernel_is_refused(cuda):
-    import torch
+def _conv_inputs(rng, dt, n, h, w, cin, cout, kh, kw):
+    if dt == "i8":
+        return (rng.integers(-128, 128, (n, h, w, cin), dtype=np.int8),
+                rng.integers(-128, 128, (kh, kw, cin, cout), dtype=np.int8))
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+    if dt == "bf16":
+        return f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    return x.astype(np.float16), f.astype(np.float16)
 
-    mod = K.conv2d(1, 8, 8, 32, 32, 3, 3, 4, 8, dtype=xt.int8)
-    x = torch.zeros((1, 8, 8, 32), dtype=torch.int8, device=cuda)
-    f = torch.zeros((3, 3, 32, 32), dtype=torch.int8, device=cuda)
-    o = torch.zeros((1, 8, 8, 32), dtype=torch.float32, device=cuda)
-    with pytest.raises(ValueError, match="i8 conv2d runs on the band kernel only"):
-        xt.launch(mod, x, f, o)
+
+_DT = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}
 
 
-def test_conv2d_filter_too_large_is_refused(cuda):
-    """The whole filter lives in LDS; a 5x5x64x80 filter (411 KB transposed)
-    cannot, and the launch is refused on the host before any kernel runs."""
-    import torch
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil,dt",
+    [
+        (1, 8, 16, 3, 16, 3, 3, 4, 8, (1, 1, 1, 1), (1, 1), (1, 1), "i8"),     # RGB input: element gathers
+        (1, 8, 8, 32, 32, 3, 3, 4, 8, (1, 1, 1, 1), (1, 1), (1, 1), "i8"),     # Cin < 64
+        (1, 8, 8, 64, 256, 3, 3, 4, 8, (1, 1, 1, 1), (1, 1), (1, 1), "i8"),    # Cout > 128
+        (2, 9, 11, 48, 40, 3, 3, 3, 11, (1, 1, 1, 1), (1, 1), (1, 1), "i8"),   # Cout % 32 != 0
+        (1, 12, 12, 16, 64, 7, 7, 3, 3, (3, 3, 3, 3), (2, 2), (1, 1), "i8"),   # 7x7 stride 2, small tile
+        (2, 10, 10, 8, 24, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # one K step spans two taps
+        (1, 11, 13, 3, 5, 5, 5, 2, 7, (2, 2, 2, 2), (2, 2), (1, 1), "f16"),    # Cin 3, Cout 5
+        (1, 10, 14, 64, 80, 5, 5, 2, 14, (2, 2, 2, 2), (1, 1), (1, 1), "f16"),  # filter beyond LDS
+        (1, 9, 9, 20, 36, 3, 3, 4, 5, (2, 0, 1, 2), (1, 2), (2, 1), "bf16"),   # Cin % 8 != 0, odd everything
+    ],
+)
+def test_conv2d_generic_kernel(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
+    """Shapes outside the band and persistent kernels (Cin not a multiple of
+    32 or 64, Cout not a multiple of 32 or above 128, filters beyond LDS, 7x7
+    stride 2) run on the generic implicit-GEMM kernel.  i8 is bit-exact; f16 /
+    bf16 within the Frobenius bar."""
+    rng = np.random.default_rng(7)
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=_DT[dt], pad=pad, stride=stride, dilation=dil)
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
+    x, f = _conv_inputs(rng, dt, n, h, w, cin, cout, kh, kw)
+    o = np.zeros((n, oh, ow, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
+                  case=f"generic conv {dt} {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    if dt == "i8":
+        assert np.array_equal(got, want)
+    else:
+        assert frob_rel(got, want) <= MM_FROB
 
-    mod = K.conv2d(1, 10, 14, 64, 80, 5, 5, 2, 14)
-    x = torch.zeros((1, 10, 14, 64), dtype=torch.float16, device=cuda)
-    f = torch.zeros((5, 5, 64, 80), dtype=torch.float16, device=cuda)
-    o = torch.zeros((1, 10, 14, 80), dtype=torch.float32, device=cuda)
-    with pytest.raises(ValueError, match="does not fit the LDS budget"):
-        xt.launch(mod, x, f, o)
+
+def _conv_text(src, filt, out, res, grid, coords, out_coords, pad, stride, dil, et, rt):
+    """A load_conv2d program in xt text (the DSL fixes the batch tile at 1, the
+    result at all filter channels and f32)."""
+    s = "x".join(map(str, src))
+    f = "x".join(map(str, filt))
+    o = "x".join(map(str, out))
+    r = "x".join(map(str, res))
+    g = ", ".join(map(str, grid))
+    return f"""
+func.func @conv(%src: memref<{s}x{et}>, %filt: memref<{f}x{et}>, %out: memref<{o}x{rt}>) attributes {{xt.grid = array<i32: {g}>}} {{
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %c0 = arith.constant 0 : i32
+  %c1 = arith.constant 1 : i32
+  %w = xt.load(%filt, %c0, %c0, %c0, %c0) {{shared = 2 : i64}} : (memref<{f}x{et}>, i32, i32, i32, i32) -> tensor<{f}x{et}>
+  %t = xt.load_conv2d(%src, %w, {coords}) {{dilation = array<i64: {dil[0]}, {dil[1]}>, group = 1 : i64, pad = array<i64: {pad[0]}, {pad[1]}, {pad[2]}, {pad[3]}>, stride = array<i64: {stride[0]}, {stride[1]}>}} : (memref<{s}x{et}>, tensor<{f}x{et}>, i32, i32, i32, i32) -> tensor<{r}x{rt}>
+  xt.store(%t, %out, {out_coords}) : (tensor<{r}x{rt}>, memref<{o}x{rt}>, i32, i32, i32, i32) -> ()
+  func.return
+}}"""
+
+
+@pytest.mark.parametrize("et", ["i8", "bf16"])
+@pytest.mark.parametrize("rt", ["f32", "bf16"])
+def test_conv2d_batch_tile_channel_subset_and_bf16_result(cuda, et, rt):
+    """Forms the verifier allows beyond the DSL's (lib/xt/XTOps.cpp:43-90): a
+    batch tile of 2, a result holding the first 32 of the filter's 48 output
+    channels, a bf16 result, a constant tile-row coordinate (row tile 1) and a
+    permuted grid (bid#2 = batch, bid#0 = column tile)."""
+    rng = np.random.default_rng(8)
+    src, filt = (4, 12, 16, 32), (3, 3, 32, 48)
+    res, out = (2, 4, 8, 32), (4, 12, 16, 32)
+    mod = xt.parse(_conv_text(src, filt, out, res, (2, 1, 2), "%bid#2, %c1, %bid#0, %c0",
+                              "%bid#2, %c1, %bid#0, %c0", (1, 1, 1, 1), (1, 1), (1, 1), et, rt))
+    x, f = _conv_inputs(rng, et, 4, 12, 16, 32, 48, 3, 3)
+    o = np.zeros(out, np.float32 if rt == "f32" else np.uint16)
+    got = run_gpu(mod, [x, f, o], [et, et, rt], cuda, case=f"conv tile 2x4x8x32 of 48 {et}->{rt}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    if rt == "bf16":
+        got, want = bf16_bits_to_f32(got), bf16_bits_to_f32(want)
+    # rows 4..7 of every image hold the result, the rest stays zero
+    assert not np.any(want[:, :4]) and not np.any(want[:, 8:]) and np.any(want[:, 4:8])
+    if et == "i8":
+        assert np.array_equal(got, want)
+    else:
+        assert frob_rel(got, want) <= MM_FROB
 
 
 # -- matmul epilogue and i8 (kernels/matmul.py) ---------------------------------

@@ -31,6 +31,12 @@
 //     stores; halo loads and output stores go through buffer descriptors whose
 //     range check supplies the zero padding and drops the ragged edge.
 //   * Waves 0-3 compute; waves 4-7 only fetch halos (see conv2d_kernel).
+//
+// Kernel choice (launch_conv2d): the band kernel below when the Blocks tile
+// the whole output; else the persistent kernel above for f16 / bf16 with
+// Cin % 32 == 0, Cout % 16 == 0 (<= 128), one image per Block, every output
+// channel and an f32 result; else the generic kernel (conv_general.hip),
+// which takes every tile shape the planner accepts.
 #include <algorithm>
 #include <atomic>
 
@@ -767,6 +773,7 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
   if (c.filt_addr.c0 || c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz) return false;
+  if (c.TB != 1 || c.TC != c.CO || c.out_elem != xt::Elem::F32) return false;
   const bool i8 = c.elem == xt::Elem::I8;
   const long long es = i8 ? 1 : 2;
   // a K step is 32 bytes of a pixel; steps go in pairs within a tap
@@ -905,19 +912,11 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   a.kpitch = 2 * K + 16;
   a.steps = K / 16;
   const int nt = (a.CO + 31) / 32;
-  if (a.C % 32 || a.CO % 16 || a.CO > 128) {
-    why = "conv2d kernel needs Cin % 32 == 0, Cout % 16 == 0 and Cout <= 128";
-    return hipErrorInvalidValue;
-  }
+  bool persistent_ok = c.elem != xt::Elem::I8 && c.out_elem == xt::Elem::F32 && c.TB == 1 && c.TC == c.CO &&
+                       a.C % 32 == 0 && a.CO % 16 == 0 && a.CO <= 128 && a.out_C % 4 == 0 &&
+                       a.tf.c0 % 8 == 0 && a.tf.sx % 8 == 0 && a.tf.sy % 8 == 0 && a.tf.sz % 8 == 0;
   for (const void* ptr : {(const void*)a.src, (const void*)a.filt, (const void*)a.out})
-    if (reinterpret_cast<uintptr_t>(ptr) % 16) {
-      why = "conv2d buffers must be 16-byte aligned";
-      return hipErrorInvalidValue;
-    }
-  if (a.tf.c0 % 8 || a.tf.sx % 8 || a.tf.sy % 8 || a.tf.sz % 8) {
-    why = "conv2d filter tile must start on a 16-byte boundary";
-    return hipErrorInvalidValue;
-  }
+    if (reinterpret_cast<uintptr_t>(ptr) % 16) persistent_ok = false;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -927,11 +926,9 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   if (try_band(p, bufs, s, max_lds, cus, e)) return e;
-  if (c.elem == xt::Elem::I8) {
-    why = "i8 conv2d runs on the band kernel only, which needs Blocks tiling the whole output, Cin % 64 == 0, "
-          "Cout in {32, 64, 128} and the filter plus one band's halo within LDS";
-    return hipErrorInvalidValue;
-  }
+  // the persistent kernel: f16 / bf16 in, f32 out, one image per Block, every
+  // output channel, 16-byte channel runs; anything else takes the generic kernel
+  if (!persistent_ok) return launch_conv2d_general(p, bufs, s, why);
   // Largest work unit (rows dividing TH) whose halo fits beside the filter.
   const int ntp = nt == 3 ? 4 : nt;  // N tiles compiled: 1, 2 or 4
   const size_t filt_bytes = size_t(ntp) * 32 * a.kpitch;
@@ -953,12 +950,7 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
       break;
     }
   }
-  if (a.UR == 0) {
-    why = "conv2d tile row (" + std::to_string(a.TW) + " pixels x " + std::to_string(a.C) +
-          " channels) with a " + std::to_string(a.CO) + "x" + std::to_string(K) +
-          " filter does not fit the LDS budget; use a narrower tile";
-    return hipErrorInvalidValue;
-  }
+  if (a.UR == 0) return launch_conv2d_general(p, bufs, s, why);  // halo + filter exceed LDS
   a.nmt = (a.UR * a.TW + 31) / 32;
   a.m_cv = udiv_magic(a.C / 8);
   a.m_rfw = udiv_magic(a.rf_w);
@@ -966,10 +958,7 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   a.m_cg = udiv_magic(a.CO / 8);
   const long long image_bytes = (long long)a.H * a.W * a.C * 2;
   const long long unit_out_bytes = (long long)a.UR * a.out_W * a.out_C * 4;
-  if (image_bytes >= (1LL << 31) || unit_out_bytes >= (1LL << 31)) {
-    why = "conv2d kernel needs one batch entry of the source and one row band of the output below 2 GiB";
-    return hipErrorInvalidValue;
-  }
+  if (image_bytes >= (1LL << 31) || unit_out_bytes >= (1LL << 31)) return launch_conv2d_general(p, bufs, s, why);
   a.image_bytes = static_cast<unsigned>(image_bytes);
   a.unit_out_bytes = static_cast<unsigned>(unit_out_bytes);
   a.units_per_block = a.TH / a.UR;

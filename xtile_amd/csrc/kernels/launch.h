@@ -17,6 +17,7 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
                               std::string& why);
 hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
 hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
+hipError_t launch_conv2d_general(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
 hipError_t launch_tilevm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
 
 }  // namespace xtk

@@ -8,7 +8,7 @@
 //              (kernels/softmax.py:10-19; test/python/dsl_convert.py:25-40)
 //   Gemm       store([ftoi]((matmul(load A, load B) [* load S]) [+ load Bias]))
 //              f16/bf16/i8 in, f32 or i8 out (kernels/matmul.py:6-19)
-//   Conv2d     store(load_conv2d(S, load F))         i8/f16/bf16 in, f32 out
+//   Conv2d     store(load_conv2d(S, load F))         i8/f16/bf16 in, f32/bf16 out
 //              (kernels/conv2d.py:10-37; conv slice math lib/xt/XTToNova.cpp:110-142)
 #include "plan.h"
 
@@ -391,9 +391,11 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
   const Type& outm = an.f.type_of(st->operands[1]);
   // i8 is the reference's own load_conv2d dtype (xtile/dsl.py:284-285); f16
   // and bf16 are the narrow-float extension
+  // the result is f32 or bf16 (lib/xt/XTOps.cpp:80-82), stored into a memref of its type
   if (!((src.elem == Elem::F16 || src.elem == Elem::BF16 || src.elem == Elem::I8) &&
-        ft.elem == src.elem && res.elem == Elem::F32)) {
-    err = "the HIP conv2d kernels take i8, f16 or bf16 source and filter of one type with an f32 result";
+        ft.elem == src.elem && (res.elem == Elem::F32 || res.elem == Elem::BF16))) {
+    err = "the HIP conv2d kernels take i8, f16 or bf16 source and filter of one type with an f32 or bf16 "
+          "result";
     return false;
   }
   if (ft.shape != fm.shape) {
@@ -423,16 +425,10 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
   c.TB = res.shape[0];
   c.TH = res.shape[1];
   c.TW = res.shape[2];
-  if (res.shape[3] != c.CO) {
-    err = "the HIP conv2d kernel needs the result tile to cover all output channels";
-    return false;
-  }
-  if (c.TB != 1) {
-    err = "the HIP conv2d kernel needs a batch tile of 1";
-    return false;
-  }
-  if (c.C % 32 || c.CO % 16 || c.CO > 128) {
-    err = "the HIP conv2d kernel needs Cin % 32 == 0 and Cout % 16 == 0 (Cout <= 128)";
+  c.TC = res.shape[3];
+  c.out_elem = res.elem;
+  if (c.TB * c.TH * c.TW <= 0 || c.TC <= 0) {
+    err = "load_conv2d result tile must not be empty";
     return false;
   }
   const Attr* pad = find_attr(cv->attrs, "pad");
@@ -479,16 +475,12 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
   c.out_H = outm.shape[1];
   c.out_W = outm.shape[2];
   c.out_C = outm.shape[3];
-  if (c.out_C % 4) {
-    err = "the HIP conv2d kernel needs the output channel count to be a multiple of 4";
-    return false;
-  }
   p.kind = PlanKind::Conv2d;
   double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
   double pixels = blocks * double(c.TB * c.TH * c.TW);
-  p.algo_flops = 2.0 * pixels * double(c.CO) * double(c.KH * c.KW * c.C);
-  p.algo_bytes = double(src.numel()) * elem_bytes(src.elem) +
-                 double(fm.numel()) * elem_bytes(fm.elem) + pixels * double(c.CO) * 4.0;
+  p.algo_flops = 2.0 * pixels * double(c.TC) * double(c.KH * c.KW * c.C);
+  p.algo_bytes = double(src.numel()) * elem_bytes(src.elem) + double(fm.numel()) * elem_bytes(fm.elem) +
+                 pixels * double(c.TC) * elem_bytes(res.elem);
   return true;
 }
 
@@ -757,8 +749,8 @@ std::string Plan::describe() const {
       break;
     }
     case PlanKind::Conv2d:
-      os << "conv2d_nhwc " << elem_name(conv.elem) << "->f32 tile=" << conv.TB << "x" << conv.TH
-         << "x" << conv.TW << "x" << conv.CO << " filter=" << conv.KH << "x" << conv.KW << "x"
+      os << "conv2d_nhwc " << elem_name(conv.elem) << "->" << elem_name(conv.out_elem) << " tile=" << conv.TB
+         << "x" << conv.TH << "x" << conv.TW << "x" << conv.TC << " filter=" << conv.KH << "x" << conv.KW << "x"
          << conv.C << "x" << conv.CO;
       break;
   }

@@ -48,7 +48,8 @@ struct ConvPlan {
   Elem elem = Elem::None;                 // source / filter element type
   int64_t N = 0, H = 0, W = 0, C = 0;     // source memref
   int64_t KH = 0, KW = 0, CO = 0;         // filter
-  int64_t TB = 0, TH = 0, TW = 0;         // output tile per block
+  int64_t TB = 0, TH = 0, TW = 0, TC = 0; // output tile per block (TC <= CO: the first TC channels)
+  Elem out_elem = Elem::F32;              // result / output element type (f32 or bf16)
   int64_t pad_top = 0, pad_left = 0, stride_h = 1, stride_w = 1, dil_h = 1, dil_w = 1;
   Coord cb, ch, cw;                       // conv tile coordinates (batch, row, col)
   TileAddr filt_addr;                     // filter tile origin
