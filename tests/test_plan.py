@@ -46,14 +46,21 @@ def test_out_of_bounds_tiles_are_rejected():
 
 
 def test_unsupported_program_names_its_ops():
-    """i8 xt.mma (test/python/dsl_convert.py:142-166) has no HIP kernel."""
-    from tests.golden.dsl_programs import programs
-    from xtile_amd import dsl
-
-    kernel, args, grid, db = programs(dsl)["compute_ops"]
-    m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
-    with pytest.raises(NotImplementedError, match="unsupported tile program.*xt.mma"):
+    """Two convolutions in one Block: no kernel takes it, and the error lists the ops."""
+    text = K.conv2d(1, 8, 8, 32, 32, 3, 3, 4, 8).__str__()
+    lines = text.splitlines()
+    conv = next(i for i, l in enumerate(lines) if "xt.load_conv2d" in l)
+    second = lines[conv].replace("%load_conv =", "%load_conv2 =")
+    m = xt.parse("\n".join(lines[: conv + 1] + [second] + lines[conv + 1 :]))
+    with pytest.raises(NotImplementedError, match="unsupported tile program.*xt.load_conv2d xt.load_conv2d"):
         xt.plan(m)
+
+
+def test_conv_inside_a_larger_program_gives_the_conv_form():
+    text = K.conv2d(1, 8, 8, 32, 32, 3, 3, 4, 8).__str__()
+    text = text.replace("xt.store(%load_conv,", "%e = xt.exp(%load_conv) : tensor<1x4x8x32xf32> -> tensor<1x4x8x32xf32>\n  xt.store(%e,")
+    with pytest.raises(NotImplementedError, match=r"conv2d programs must be store\(load_conv2d"):
+        xt.plan(xt.parse(text))
 
 
 @pytest.mark.parametrize(
@@ -62,6 +69,7 @@ def test_unsupported_program_names_its_ops():
         ("unary_and_shape", "tile_vm f32 insts=12 loads=2 stores=3 lds="),
         ("column_reduce", "tile_vm f32 insts=3 loads=1 stores=1 lds="),
         ("divide_kernel", "tile_vm f32 insts=5 loads=2 stores=1 lds="),
+        ("compute_ops", "tile_vm f32 insts=5 loads=3 stores=1 lds="),
     ],
 )
 def test_general_programs_plan_onto_the_tile_interpreter(name, kernel):
@@ -93,19 +101,31 @@ def test_epilogue_matmul_plans():
     assert xt.plan(m)["kernel"] == "gemm i8->f32 tile=64x64 k=256 epilogue=scale,bias,ftoi->i8 grid=(16,8,1)"
 
 
-def test_unsupported_matmul_epilogue_is_reported():
-    text = """
-func.func @k(%a: memref<64x64xf16>, %b: memref<64x64xf16>, %c: memref<64x64xf32>) attributes {xt.grid = array<i32: 1, 1, 1>} {
+_MM_EXP = """
+func.func @k(%a: memref<MxKxf16>, %b: memref<KxNxf16>, %c: memref<MxNxf32>) attributes {xt.grid = array<i32: 1, 1, 1>} {
   %z = arith.constant 0 : i32
-  %0 = xt.load(%a, %z, %z) : (memref<64x64xf16>, i32, i32) -> tensor<64x64xf16>
-  %1 = xt.load(%b, %z, %z) : (memref<64x64xf16>, i32, i32) -> tensor<64x64xf16>
-  %2 = xt.matmul(%0, %1) : tensor<64x64xf16>, tensor<64x64xf16> -> tensor<64x64xf32>
-  %3 = xt.exp(%2) : tensor<64x64xf32> -> tensor<64x64xf32>
-  xt.store(%3, %c, %z, %z) : (tensor<64x64xf32>, memref<64x64xf32>, i32, i32) -> ()
+  %0 = xt.load(%a, %z, %z) : (memref<MxKxf16>, i32, i32) -> tensor<MxKxf16>
+  %1 = xt.load(%b, %z, %z) : (memref<KxNxf16>, i32, i32) -> tensor<KxNxf16>
+  %2 = xt.matmul(%0, %1) : tensor<MxKxf16>, tensor<KxNxf16> -> tensor<MxNxf32>
+  %3 = xt.exp(%2) : tensor<MxNxf32> -> tensor<MxNxf32>
+  xt.store(%3, %c, %z, %z) : (tensor<MxNxf32>, memref<MxNxf32>, i32, i32) -> ()
   func.return
 }"""
-    with pytest.raises(NotImplementedError, match=r"matmul programs must be store\(\[ftoi\]"):
-        xt.plan(xt.parse(text))
+
+
+def _mm_exp(m, k, n):
+    return xt.parse(_MM_EXP.replace("MxK", f"{m}x{k}").replace("KxN", f"{k}x{n}").replace("MxN", f"{m}x{n}"))
+
+
+def test_matmul_outside_the_gemm_forms_runs_on_the_tile_interpreter():
+    assert xt.plan(_mm_exp(64, 64, 64))["kernel"].startswith("tile_vm f32 insts=5 loads=2 stores=1")
+
+
+def test_unsupported_matmul_epilogue_is_reported():
+    """Too large for the interpreter's LDS: both reasons are given."""
+    with pytest.raises(NotImplementedError, match=r"matmul programs must be store\(\[ftoi\].*declines it too: "
+                       r"tile program needs 320 KB of LDS"):
+        xt.plan(_mm_exp(128, 256, 128))
 
 
 def test_nova_stages_raise():

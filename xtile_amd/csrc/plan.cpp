@@ -13,6 +13,7 @@
 #include "plan.h"
 
 #include <map>
+#include <set>
 #include <sstream>
 
 namespace xt {
@@ -486,17 +487,19 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
 
 // -- TileVM ----------------------------------------------------------------------
 //
-// Every other f32 program without matmul / conv: the Block's ops, in program
-// order, become tile instructions over LDS slots (one workgroup per Block).
-// Slots are assigned by liveness, first fit; reshape renames a slot (the data
-// is row-major either way, xtile/dsl.py reshape); transpose swaps the last two
-// dims and permute reorders dims (include/xt/XTOps.td), both as a Permute.
+// Every other program without conv: the Block's ops, in program order, become
+// tile instructions over LDS slots (one workgroup per Block).  Values are held
+// as f32 whatever their element type, as the reference's loop-lowered
+// execution holds them; loads and stores convert.  Slots are assigned by
+// liveness, first fit; reshape and itof rename a slot (row-major data, and an
+// i8 value is already held exactly); transpose swaps the last two dims and
+// permute reorders dims (include/xt/XTOps.td), both as a Permute.
 
 bool vm_unary(const std::string& n, VmUnary& k) {
   static const std::pair<const char*, VmUnary> table[] = {
       {"xt.exp", VmUnary::Exp},       {"xt.cos", VmUnary::Cos},         {"xt.sin", VmUnary::Sin},
       {"xt.reciprocal", VmUnary::Recip}, {"xt.rsqrt", VmUnary::Rsqrt}, {"xt.sigmoid", VmUnary::Sigmoid},
-      {"xt.tanh", VmUnary::Tanh},     {"xt.silu", VmUnary::Silu}};
+      {"xt.tanh", VmUnary::Tanh},     {"xt.silu", VmUnary::Silu},       {"xt.ftoi", VmUnary::Ftoi}};
   for (auto& e : table)
     if (n == e.first) {
       k = e.second;
@@ -516,27 +519,30 @@ bool pad3(const std::vector<int64_t>& s, int dims[3], std::string& err) {
   return true;
 }
 
+bool vm_elem(Elem e) { return e == Elem::F32 || e == Elem::F16 || e == Elem::BF16 || e == Elem::I8; }
+
 bool match_vm(const Analysis& an, Plan& p, std::string& err) {
   const int nops = static_cast<int>(an.compute.size());
-  // every op must be one the interpreter runs, on f32 tensors
+  // every op must be one the interpreter runs
   for (const Op* o : an.compute) {
     VmUnary u;
     const std::string& n = o->name;
     const bool ok = n == "xt.load" || n == "xt.store" || n == "xt.add" || n == "xt.sub" || n == "xt.mul" ||
                     n == "xt.reduce_sum" || n == "xt.reduce_max" || n == "xt.reshape" ||
-                    n == "xt.transpose" || n == "xt.permute" || vm_unary(n, u);
+                    n == "xt.transpose" || n == "xt.permute" || n == "xt.matmul" || n == "xt.mma" ||
+                    n == "xt.itof" || vm_unary(n, u);
     if (!ok) return false;
   }
   for (const Op* o : an.compute) {
     const std::string& n = o->name;
     for (int r : o->results)
-      if (an.f.type_of(r).elem != Elem::F32) {
-        err = "tile programs on the HIP backend compute in f32 (" + n + " yields " +
+      if (!vm_elem(an.f.type_of(r).elem)) {
+        err = "tile programs on the HIP backend hold f32, f16, bf16 or i8 tensors (" + n + " yields " +
               elem_name(an.f.type_of(r).elem) + ")";
         return false;
       }
-    if (n == "xt.store" && an.f.type_of(o->operands[1]).elem != Elem::F32) {
-      err = "tile programs on the HIP backend store f32 tiles";
+    if (n == "xt.store" && !vm_elem(an.f.type_of(o->operands[1]).elem)) {
+      err = "tile programs on the HIP backend store f32, f16, bf16 or i8 tiles";
       return false;
     }
   }
@@ -549,7 +555,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
   std::map<int, int> last_use;
   for (int i = 0; i < nops; ++i) {
     const Op* o = an.compute[i];
-    if (o->name == "xt.reshape") root[o->results[0]] = root_of(o->operands[0]);
+    if (o->name == "xt.reshape" || o->name == "xt.itof") root[o->results[0]] = root_of(o->operands[0]);
     for (int v : o->operands) {
       if (!an.f.type_of(v).is_tensor()) continue;
       last_use[root_of(v)] = i;
@@ -584,8 +590,17 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
         break;
       }
   };
+  // values known to be integers in [-128, 127]: i8 loads and ftoi results
+  // (and their renamings, transposes and permutes)
+  std::set<int> small_int;
+  for (const Op* o : an.compute) {
+    const std::string& n = o->name;
+    if ((n == "xt.load" && an.f.type_of(o->results[0]).elem == Elem::I8) || n == "xt.ftoi" ||
+        ((n == "xt.transpose" || n == "xt.permute") && small_int.count(root_of(o->operands[0]))))
+      small_int.insert(o->results[0]);
+  }
   VmPlan vm;
-  double bytes = 0;
+  double bytes = 0, flops = 0;
   for (int i = 0; i < nops; ++i) {
     const Op* o = an.compute[i];
     const std::string& n = o->name;
@@ -597,6 +612,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       const Type& ten = is_load ? an.f.type_of(o->results[0]) : an.f.type_of(o->operands[0]);
       VmAccess acc;
       acc.arg = an.arg_index(mem_v);
+      acc.elem = mem.elem;
       if (acc.arg < 0) {
         err = n + " must access a function argument";
         return false;
@@ -614,7 +630,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       in.op = is_load ? VmOp::Load : VmOp::Store;
       in.kind = static_cast<int16_t>(vm.access.size());
       vm.access.push_back(acc);
-      bytes += double(ten.numel()) * 4;
+      bytes += double(ten.numel()) * elem_bytes(mem.elem);
       if (is_load) {
         auto sl = alloc(static_cast<int>(ten.numel()));
         slot[o->results[0]] = sl;
@@ -622,8 +638,8 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       } else {
         in.a = slot.at(root_of(o->operands[0])).first;
       }
-    } else if (n == "xt.reshape") {
-      continue;  // same slot, new shape
+    } else if (n == "xt.reshape" || n == "xt.itof") {
+      continue;  // same slot, new shape or type
     } else {
       const Type& res = an.f.type_of(o->results[0]);
       const Type& ta = an.f.type_of(o->operands[0]);
@@ -638,14 +654,15 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
         in.op = VmOp::Binary;
         in.kind = static_cast<int16_t>(n == "xt.add" ? VmBinary::Add : n == "xt.sub" ? VmBinary::Sub : VmBinary::Mul);
         in.b = slot.at(root_of(o->operands[1])).first;
-        if (ta.shape != res.shape || tb.rank() != res.rank()) {
-          err = "tile programs on the HIP backend broadcast the right operand only, at equal rank "
-                "(xtile/dsl.py:754-759)";
+        // numpy broadcasting, right-aligned (lib/xt/XTOps.cpp:104-145)
+        if (ta.rank() > res.rank() || tb.rank() > res.rank()) {
+          err = "broadcast operands must not outrank the result";
           return false;
         }
-        if (!pad3(res.shape, in.dims, err) || !pad3(tb.shape, in.aux, err)) return false;
+        if (!pad3(res.shape, in.dims, err) || !pad3(ta.shape, in.lhs, err) || !pad3(tb.shape, in.aux, err))
+          return false;
         for (int d = 0; d < 3; ++d)
-          if (in.aux[d] != in.dims[d] && in.aux[d] != 1) {
+          if ((in.aux[d] != in.dims[d] && in.aux[d] != 1) || (in.lhs[d] != in.dims[d] && in.lhs[d] != 1)) {
             err = "broadcast operand dims must equal the result's or be 1";
             return false;
           }
@@ -660,6 +677,25 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
         in.kind = static_cast<int16_t>(n == "xt.reduce_sum" ? VmReduce::Sum : VmReduce::Max);
         if (!pad3(ta.shape, in.dims, err)) return false;
         in.aux[0] = static_cast<int>(axis);
+      } else if (n == "xt.matmul" || n == "xt.mma") {
+        const Type& tb = an.f.type_of(o->operands[1]);
+        if (ta.rank() != 2 || tb.rank() != 2 || res.rank() != 2 || ta.shape[1] != tb.shape[0]) {
+          err = "matmul takes [M, K] x [K, N] tiles (lib/xt/XTOps.cpp:218-235)";
+          return false;
+        }
+        in.op = VmOp::Matmul;
+        in.b = slot.at(root_of(o->operands[1])).first;
+        if (n == "xt.mma") in.c = slot.at(root_of(o->operands[2])).first;
+        const int64_t K = ta.shape[1];
+        in.dims[0] = 1;
+        in.dims[1] = static_cast<int>(ta.shape[0]);
+        in.dims[2] = static_cast<int>(tb.shape[1]);
+        in.aux[0] = static_cast<int>(K);
+        // i8 x i8 sums stay exact in i32 for K < 2^17 (|a*b| <= 2^14)
+        in.aux[1] = small_int.count(root_of(o->operands[0])) && small_int.count(root_of(o->operands[1])) &&
+                    K < (int64_t(1) << 17);
+        in.aux[2] = 0;
+        flops += 2.0 * double(ta.shape[0]) * double(tb.shape[1]) * double(K);
       } else {  // transpose / permute
         in.op = VmOp::Permute;
         if (!pad3(ta.shape, in.dims, err)) return false;
@@ -707,6 +743,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
   p.vm = std::move(vm);
   const double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
   p.algo_bytes = blocks * bytes;
+  p.algo_flops = blocks * flops;
   return true;
 }
 
@@ -796,12 +833,21 @@ bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& 
       err = "stored values must be computed in the function";
       return false;
     }
+  // the specialised kernels first; what they decline (with a reason) goes to
+  // the tile interpreter, and the first reason is reported if that fails too
   err.clear();
-  if (match_ew(an, p, err) || !err.empty()) return err.empty();
-  if (match_softmax(an, p, err) || !err.empty()) return err.empty();
-  if (match_gemm(an, p, err) || !err.empty()) return err.empty();
-  if (match_conv(an, p, err) || !err.empty()) return err.empty();
-  if (match_vm(an, p, err) || !err.empty()) return err.empty();
+  std::string first;
+  for (auto match : {match_ew, match_softmax, match_gemm, match_conv}) {
+    std::string why;
+    if (match(an, p, why)) return true;
+    if (first.empty()) first = why;
+  }
+  if (match_vm(an, p, err)) return true;
+  if (!first.empty()) {
+    err = first + (err.empty() ? "" : "; the tile interpreter declines it too: " + err);
+    return false;
+  }
+  if (!err.empty()) return false;
   std::ostringstream os;
   os << "unsupported tile program for the HIP backend: @" << f->name << " uses";
   for (const Op* o : an.compute) os << " " << o->name;

@@ -57,17 +57,19 @@ struct ConvPlan {
   int64_t out_H = 0, out_W = 0, out_C = 0;  // output memref dims 1..3
 };
 
-// General f32 tile programs (anything without matmul / conv): the Block's
-// ops become a straight-line list of tile instructions over LDS slots, run by
-// one workgroup per Block (kernels/tilevm.hip).  Shapes are padded to rank 3
-// with leading 1s.
-enum class VmOp : int16_t { Load, Store, Unary, Binary, Reduce, Permute };
-enum class VmUnary : int16_t { Exp, Cos, Sin, Recip, Rsqrt, Sigmoid, Tanh, Silu };
+// General tile programs (anything without conv that the specialised kernels
+// do not take): the Block's ops become a straight-line list of tile
+// instructions over LDS slots, run by one workgroup per Block
+// (kernels/tilevm.hip).  Values are held as f32 whatever their element type.
+// Shapes are padded to rank 3 with leading 1s.
+enum class VmOp : int16_t { Load, Store, Unary, Binary, Reduce, Permute, Matmul };
+enum class VmUnary : int16_t { Exp, Cos, Sin, Recip, Rsqrt, Sigmoid, Tanh, Silu, Ftoi };
 enum class VmBinary : int16_t { Add, Sub, Mul };
 enum class VmReduce : int16_t { Sum, Max };
 
 struct VmAccess {                 // a load or store tile against a memref argument
   int arg = -1;
+  Elem elem = Elem::F32;          // memref element type (converted at the access)
   TileAddr addr;                  // tile origin (element offset), affine in the block id
   int64_t stride[3] = {0, 0, 0};  // memref element strides of the tile's dims
 };
@@ -76,8 +78,11 @@ struct VmInst {
   VmOp op = VmOp::Load;
   int16_t kind = 0;               // VmUnary / VmBinary / VmReduce, or the access index
   int dst = 0, a = 0, b = 0;      // LDS float offsets of the operands' slots
+  int c = -1;                     // Matmul: slot of the mma accumulator, -1 for none
   int dims[3] = {1, 1, 1};        // result dims (Reduce, Permute: source dims)
-  int aux[3] = {1, 1, 1};         // Binary: rhs dims; Reduce: axis in aux[0]; Permute: perm
+  int aux[3] = {1, 1, 1};         // Binary: rhs dims; Reduce: axis in aux[0]; Permute: perm;
+                                  // Matmul: K, exact i32 sums (0/1), unused
+  int lhs[3] = {1, 1, 1};         // Binary: lhs dims
 };
 
 struct VmPlan {
