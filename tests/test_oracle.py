@@ -441,3 +441,66 @@ def test_oracle_unary_chain_transpose_and_reshape():
     np.testing.assert_allclose(bufs[1], v, rtol=2e-6, atol=0)
     assert np.array_equal(bufs[2], bufs[1].reshape(4, 16))
     assert np.array_equal(bufs[4], t.transpose(0, 2, 1))
+
+
+def test_oracle_mma_is_acc_plus_product():
+    """test/python/dsl_convert.py:229-247 (xt.mma, i8 operands, f32
+    accumulator): the exact float64 sum rounded once to f32; a planted
+    accumulator-dropping checker is caught."""
+    from tests.golden.dsl_programs import programs
+    from xtile_amd import dsl
+    import xtile_amd as xt
+
+    kernel, args, grid, db = programs(dsl)["compute_ops"]
+    m = xt.convert(kernel, args=args, grid=grid, double_buffering=db)
+    rng = np.random.default_rng(14)
+    a = rng.integers(-128, 128, (16, 32), dtype=np.int8)
+    b = rng.integers(-128, 128, (32, 8), dtype=np.int8)
+    acc = rng.normal(0, 1000, (16, 8)).astype(np.float32)
+    out = run_c(str(m), [a, b, acc, np.zeros((16, 8), np.float32)])[3]
+    exact = a.astype(np.float64) @ b.astype(np.float64) + acc.astype(np.float64)
+    assert np.array_equal(out, exact.astype(np.float32))
+    assert not np.array_equal(out, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32))
+
+
+def test_oracle_two_sided_broadcast_and_narrow_stores():
+    """numpy broadcasting on both operands (lib/xt/XTOps.cpp:104-145); f16
+    stores equal numpy's nearest-even astype, i8 stores saturate."""
+    import xtile_amd as xt
+
+    text = """
+func.func @bc(%a: memref<8x1xf32>, %b: memref<1x16xf32>, %c: memref<8x16xf32>) attributes {xt.grid = array<i32: 1, 1, 1>} {
+  %z = arith.constant 0 : i32
+  %0 = xt.load(%a, %z, %z) : (memref<8x1xf32>, i32, i32) -> tensor<8x1xf32>
+  %1 = xt.load(%b, %z, %z) : (memref<1x16xf32>, i32, i32) -> tensor<1x16xf32>
+  %2 = xt.sub(%0, %1) : tensor<8x1xf32>, tensor<1x16xf32> -> tensor<8x16xf32>
+  xt.store(%2, %c, %z, %z) : (tensor<8x16xf32>, memref<8x16xf32>, i32, i32) -> ()
+  func.return
+}"""
+    rng = np.random.default_rng(15)
+    a = rng.normal(0, 1, (8, 1)).astype(np.float32)
+    b = rng.normal(0, 1, (1, 16)).astype(np.float32)
+    out = run_c(str(xt.parse(text)), [a, b, np.zeros((8, 16), np.float32)])[2]
+    assert np.array_equal(out, a - b)
+    assert not np.array_equal(out, b.T - a.T)  # operands swapped
+    add = """
+func.func @n(%a: memref<4x64xT>, %b: memref<4x64xT>, %c: memref<4x64xT>) attributes {xt.grid = array<i32: 1, 1, 1>} {
+  %z = arith.constant 0 : i32
+  %0 = xt.load(%a, %z, %z) : (memref<4x64xT>, i32, i32) -> tensor<4x64xT>
+  %1 = xt.load(%b, %z, %z) : (memref<4x64xT>, i32, i32) -> tensor<4x64xT>
+  %2 = xt.add(%0, %1) : tensor<4x64xT>, tensor<4x64xT> -> tensor<4x64xT>
+  xt.store(%2, %c, %z, %z) : (tensor<4x64xT>, memref<4x64xT>, i32, i32) -> ()
+  func.return
+}"""
+    x = rng.normal(0, 3000, (4, 64)).astype(np.float16)
+    y = rng.normal(0, 3000, (4, 64)).astype(np.float16)
+    x[0, :3] = [65504, 1.0, 2048]
+    y[0, :3] = [16, 2.0**-11, 1]
+    out = run_c(str(xt.parse(add.replace("xT", "xf16"))), [x, y, np.zeros_like(x)])[2]
+    with np.errstate(over="ignore"):  # 65504 + 16 rounds to inf, as it should
+        want = (x.astype(np.float32) + y.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(out.view(np.uint16), want.view(np.uint16))
+    i = rng.integers(-128, 128, (4, 64), dtype=np.int8)
+    j = rng.integers(-128, 128, (4, 64), dtype=np.int8)
+    out = run_c(str(xt.parse(add.replace("xT", "xi8"))), [i, j, np.zeros_like(i)])[2]
+    assert np.array_equal(out, np.clip(i.astype(np.int32) + j.astype(np.int32), -128, 127).astype(np.int8))
