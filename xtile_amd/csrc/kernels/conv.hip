@@ -582,38 +582,64 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[t][v] = 0;
 
-  // Cin / 16 is even, so steps s and s+1 share a tap.  The loop body has no
-  // branch: the tap advance is a pair of selects and the read-ahead of step
-  // s+2 always runs (on the last iteration it rereads the last tap and step,
-  // in bounds, and the result is unused), so the compiler can issue it ahead
-  // of the MFMAs of step s+1.
-  short8 a0[MI], a1[MI], b0, b1;
-  int kh = 0, kw = 0, cs = 0;
-  set_tap(0);
-  read(0, 0, a0, b0);
+  // K steps come in pairs (s, s+1) that share a tap (Cin * esize / 32 is
+  // even).  Fragments are read two steps ahead of their MFMAs, through four
+  // register sets: with eight waves queueing on the LDS, one step of
+  // read-ahead left the matrix pipe waiting on most steps.  At most 10 reads
+  // are outstanding per wave (the LGKM counter tracks 15).  The read cursor
+  // (pair pr, tap kh/kw, channel step cs) stops at the last pair: reads past
+  // the end reread it, in bounds, and are not used.
+  const int npairs = p.steps >> 1;
+  int kh = 0, kw = 0, cs = 0, pr = 0;
+  auto read_step = [&](bool odd, short8 (&a)[MI], short8& b) {
+    if (!odd) set_tap(kh * p.dh * p.rf_w + kw * p.dw);
+    read(2 * pr + (odd ? 1 : 0), cs + (odd ? 1 : 0), a, b);
+    if (odd) {  // advance to the next pair, unless this is the last
+      const bool more = pr + 1 < npairs;
+      const int ncs = cs + 2;
+      const bool tap_end = ncs == cs_per_tap;
+      const int nkw = kw + (tap_end ? 1 : 0);
+      const bool row_end = nkw == p.KW;
+      cs = more ? (tap_end ? 0 : ncs) : cs;
+      kw = more ? (row_end ? 0 : nkw) : kw;
+      kh = more ? kh + (row_end ? 1 : 0) : kh;
+      pr = more ? pr + 1 : pr;
+    }
+  };
+  short8 a0[MI], a1[MI], a2[MI], a3[MI], b0, b1, b2, b3;
+  auto mfmas = [&](const short8 (&a)[MI], const short8& b) {
+#pragma unroll
+    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<ELEM>(a[t], b, acc[t]);
+  };
+  read_step(false, a0, b0);
+  read_step(true, a1, b1);
   // Scheduling fences keep each read batch ahead of the MFMAs that do not
   // need it (left alone, the scheduler sinks the reads next to their MFMAs to
   // save registers and the LDS latency shows on every step).
-  for (int s = 0; s < p.steps; s += 2) {
-    read(s + 1, cs + 1, a1, b1);
+  // The loop body has no branch (a branch inside it makes the compiler wait
+  // for every outstanding read at the block boundary); steps % 4 == 2 leaves
+  // one pair for after the loop.
+  for (int s = 0; s + 4 <= p.steps; s += 4) {
+    read_step(false, a2, b2);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<ELEM>(a0[t], b0, acc[t]);
+    mfmas(a0, b0);
     __builtin_amdgcn_sched_barrier(0);
-    cs += 2;
-    const bool tap_end = cs == cs_per_tap;
-    cs = tap_end ? 0 : cs;
-    kw += tap_end ? 1 : 0;
-    const bool row_end = kw == p.KW;
-    kw = row_end ? 0 : kw;
-    kh += row_end ? 1 : 0;
-    const bool last = s + 2 >= p.steps;
-    set_tap(last ? (p.KH - 1) * p.dh * p.rf_w + (p.KW - 1) * p.dw : kh * p.dh * p.rf_w + kw * p.dw);
-    read(last ? p.steps - 1 : s + 2, last ? cs_per_tap - 1 : cs, a0, b0);
+    read_step(true, a3, b3);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < MI; ++t) acc[t] = band_mfma<ELEM>(a1[t], b1, acc[t]);
+    mfmas(a1, b1);
     __builtin_amdgcn_sched_barrier(0);
+    read_step(false, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a2, b2);
+    __builtin_amdgcn_sched_barrier(0);
+    read_step(true, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a3, b3);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (p.steps & 2) {
+    mfmas(a0, b0);
+    mfmas(a1, b1);
   }
 
   // D = P x F: lane l holds channel 32j + l%32; register v holds pixel
