@@ -39,6 +39,7 @@
 // which takes every tile shape the planner accepts.
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "launch.h"
@@ -507,11 +508,14 @@ typedef __attribute__((address_space(3))) unsigned char band_lds_t;
 
 // MI M tiles of the band (first pixel q0, then every tstride pixels) against
 // N tile j, all in one pass so that each filter fragment feeds MI MFMAs.  K
-// runs in steps of 32 bytes per pixel (16 f16 / bf16 or 32 i8 channels): tap
-// s / cs_per_tap, channel step s % cs_per_tap.  The fragments of step s+1 are
-// read while the MFMAs of step s run.  Pixels at or past qend are computed on
-// clamped addresses and not stored.
-template <int MI, int ELEM>
+// runs tap by tap; a tap is CS steps of 32 bytes per pixel (16 f16 / bf16 or
+// 32 i8 channels), CS = Cin * esize / 32.  Within a tap every fragment address
+// is the tap's base plus a compile-time offset, so the per-step work is the
+// reads and the MFMAs alone; the tap bookkeeping (a few scalar selects and
+// MI + 2 vector adds) runs once per tap.  Fragments are read one step pair
+// ahead of their MFMAs.  Pixels at or past qend are computed on clamped
+// addresses and not stored.
+template <int MI, int NT, int CS, int ELEM>
 __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* Fs, const band_lds_t* Hs,
                                            __amdgpu_buffer_rsrc_t orc, int q0, int tstride, int qend, int j,
                                            int lane) {
@@ -519,15 +523,15 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
   const int g = lane >> 4, li = lane & 15;
   constexpr int ES = ELEM == kBandI8 ? 1 : 2;  // bytes per element
   constexpr int RS = 32 / ES;                  // K rows per step
-  const int RB = p.CO * ES;
-  const int cs_per_tap = p.C * ES / 32;
+  constexpr int RB = NT * 32 * ES;             // bytes per filter row (Cout = 32 NT)
+  constexpr int BSTEP = RS * RB;               // filter bytes per K step
   // Filter fragment: two transposed reads per step.  16-bit: each 16-lane
   // group reads a 4 (K) x 16 (Cout) block, lane i at K row i/4 and columns
   // 4*(i%4)..+3 (ds_read_b64_tr_b16).  8-bit: an 8 x 16 block, lane i at K row
   // i/2 and columns 8*(i%2)..+7 (ds_read_b64_tr_b8).  A step moves RS rows,
   // which leaves the row swizzle unchanged, so each read is a per-lane
-  // constant plus RS * RB * s.
-  int boff[2];
+  // constant plus BSTEP * s.
+  int pb[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     int k, ncol;
@@ -539,40 +543,33 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
       ncol = 32 * j + 16 * (g & 1) + 4 * (li & 3);
     }
     const int cb = ncol * ES;  // byte column
-    boff[h] = k * RB + (((cb >> 4) ^ (p.fsw_unit * ((k >> p.fsw_shift) & p.fsw_mask))) << 4) + (cb & 15);
+    pb[h] = k * RB + (((cb >> 4) ^ (p.fsw_unit * ((k >> p.fsw_shift) & p.fsw_mask))) << 4) + (cb & 15);
   }
-  const int bstep = RS * RB;
-  // Pixel fragment of tile t at tap offset `tapoff` (halo pixels) and channel
-  // step cs: Hs + (hp0 + tapoff) * pitch + 16 * (2 * cs + hi).
-  int hbase[MI];
+  // Pixel fragment of tile t in the current tap, channel step c:
+  // Hs + pa[t] + 32 c, pa[t] = (halo pixel of the tap) * pitch + 16 (l/32).
+  int pa[MI];
 #pragma unroll
   for (int t = 0; t < MI; ++t) {
     const int q = min(q0 + t * tstride + lr, qend - 1);
     const int r = (int)udiv((unsigned)q, p.m_ow), c = q - r * p.OW;
-    hbase[t] = (r * p.sh * p.rf_w + c * p.sw) * p.pitch + hi * 16;
+    pa[t] = (r * p.sh * p.rf_w + c * p.sw) * p.pitch + hi * 16;
   }
-  int base[MI];
-  auto set_tap = [&](int tapoff) {
-    const int tb = tapoff * p.pitch;
+  typedef short8 __attribute__((address_space(3))) lds_s8;
+  auto read = [&](const int (&ra)[MI], const int (&rb)[2], int c, short8 (&a)[MI], short8& b) {
 #pragma unroll
-    for (int t = 0; t < MI; ++t) base[t] = hbase[t] + tb;
-  };
-  auto read = [&](int s, int cs, short8 (&a)[MI], short8& b) {
-#pragma unroll
-    for (int t = 0; t < MI; ++t)
-      a[t] = *reinterpret_cast<const short8 __attribute__((address_space(3)))*>(Hs + base[t] + cs * 32);
-    band_lds_t* f = const_cast<band_lds_t*>(Fs) + s * bstep;
+    for (int t = 0; t < MI; ++t) a[t] = *reinterpret_cast<const lds_s8*>(Hs + ra[t] + c * 32);
+    band_lds_t* f = const_cast<band_lds_t*>(Fs) + c * BSTEP;
     if constexpr (ELEM == kBandI8) {
       const int2v lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-          reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[0]));
+          reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + rb[0]));
       const int2v h4 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-          reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[1]));
+          reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + rb[1]));
       b = __builtin_bit_cast(short8, int4v{lo[0], lo[1], h4[0], h4[1]});
     } else {
       const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[0]));
+          reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + rb[0]));
       const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[1]));
+          reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + rb[1]));
       b = short8{lo[0], lo[1], lo[2], lo[3], h4[0], h4[1], h4[2], h4[3]};
     }
   };
@@ -581,66 +578,65 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
   for (int t = 0; t < MI; ++t)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[t][v] = 0;
-
-  // K steps come in pairs (s, s+1) that share a tap (Cin * esize / 32 is
-  // even).  Fragments are read two steps ahead of their MFMAs, through four
-  // register sets: with eight waves queueing on the LDS, one step of
-  // read-ahead left the matrix pipe waiting on most steps.  At most 10 reads
-  // are outstanding per wave (the LGKM counter tracks 15).  The read cursor
-  // (pair pr, tap kh/kw, channel step cs) stops at the last pair: reads past
-  // the end reread it, in bounds, and are not used.
-  const int npairs = p.steps >> 1;
-  int kh = 0, kw = 0, cs = 0, pr = 0;
-  auto read_step = [&](bool odd, short8 (&a)[MI], short8& b) {
-    if (!odd) set_tap(kh * p.dh * p.rf_w + kw * p.dw);
-    read(2 * pr + (odd ? 1 : 0), cs + (odd ? 1 : 0), a, b);
-    if (odd) {  // advance to the next pair, unless this is the last
-      const bool more = pr + 1 < npairs;
-      const int ncs = cs + 2;
-      const bool tap_end = ncs == cs_per_tap;
-      const int nkw = kw + (tap_end ? 1 : 0);
-      const bool row_end = nkw == p.KW;
-      cs = more ? (tap_end ? 0 : ncs) : cs;
-      kw = more ? (row_end ? 0 : nkw) : kw;
-      kh = more ? kh + (row_end ? 1 : 0) : kh;
-      pr = more ? pr + 1 : pr;
-    }
-  };
-  short8 a0[MI], a1[MI], a2[MI], a3[MI], b0, b1, b2, b3;
   auto mfmas = [&](const short8 (&a)[MI], const short8& b) {
 #pragma unroll
     for (int t = 0; t < MI; ++t) acc[t] = band_mfma<ELEM>(a[t], b, acc[t]);
   };
-  read_step(false, a0, b0);
-  read_step(true, a1, b1);
-  // Scheduling fences keep each read batch ahead of the MFMAs that do not
-  // need it (left alone, the scheduler sinks the reads next to their MFMAs to
-  // save registers and the LDS latency shows on every step).
-  // The loop body has no branch (a branch inside it makes the compiler wait
-  // for every outstanding read at the block boundary); steps % 4 == 2 leaves
-  // one pair for after the loop.
-  for (int s = 0; s + 4 <= p.steps; s += 4) {
-    read_step(false, a2, b2);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    read_step(true, a3, b3);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
-    read_step(false, a0, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a2, b2);
-    __builtin_amdgcn_sched_barrier(0);
-    read_step(true, a1, b1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a3, b3);
-    __builtin_amdgcn_sched_barrier(0);
+
+  // Two register sets of one step pair each; the set in use alternates with
+  // the pair index, so a tap of CS / 2 pairs starts on set PAR.
+  short8 a00[MI], a01[MI], a10[MI], a11[MI], b00, b01, b10, b11;
+  const int dcol = p.dw * p.pitch;                                // next tap in the filter row
+  const int drow = (p.dh * p.rf_w - (p.KW - 1) * p.dw) * p.pitch;  // first tap of the next row
+  const int taps = p.KH * p.KW;
+  int tap = 0, kw = 0;
+  read(pa, pb, 0, a00, b00);
+  read(pa, pb, 1, a01, b01);
+  auto tap_body = [&](auto par_c) {
+    constexpr int PAR = decltype(par_c)::value;
+    // the next tap's bases (the last tap's successor is itself: its reads are in bounds and unused)
+    const bool last = tap + 1 >= taps;
+    const bool row_end = kw + 1 == p.KW;
+    const int da = last ? 0 : (row_end ? drow : dcol);
+    const int db = last ? 0 : CS * BSTEP;
+    int na[MI], nb[2];
+#pragma unroll
+    for (int t = 0; t < MI; ++t) na[t] = pa[t] + da;
+    nb[0] = pb[0] + db;
+    nb[1] = pb[1] + db;
+#pragma unroll
+    for (int k = 0; k < CS / 2; ++k) {
+      const bool cur0 = ((PAR + k) & 1) == 0;
+      const bool more = k + 1 < CS / 2;
+      // read pair k + 1 of this tap, or pair 0 of the next, into the other set
+      if (cur0) {
+        if (more) { read(pa, pb, 2 * k + 2, a10, b10); read(pa, pb, 2 * k + 3, a11, b11); }
+        else { read(na, nb, 0, a10, b10); read(na, nb, 1, a11, b11); }
+      } else {
+        if (more) { read(pa, pb, 2 * k + 2, a00, b00); read(pa, pb, 2 * k + 3, a01, b01); }
+        else { read(na, nb, 0, a00, b00); read(na, nb, 1, a01, b01); }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (cur0) { mfmas(a00, b00); mfmas(a01, b01); }
+      else { mfmas(a10, b10); mfmas(a11, b11); }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < MI; ++t) pa[t] = na[t];
+    pb[0] = nb[0];
+    pb[1] = nb[1];
+    kw = row_end ? 0 : kw + 1;
+    ++tap;
+  };
+  // Two taps per iteration keep the set parity static when CS / 2 is odd.
+  // The loop body has no data-dependent branch (one makes the compiler wait
+  // for every outstanding read at the block boundary).
+  int t2 = 0;
+  for (; t2 + 2 <= taps; t2 += 2) {
+    tap_body(std::integral_constant<int, 0>{});
+    tap_body(std::integral_constant<int, (CS / 2) & 1>{});
   }
-  if (p.steps & 2) {
-    mfmas(a0, b0);
-    mfmas(a1, b1);
-  }
+  if (t2 < taps) tap_body(std::integral_constant<int, 0>{});
 
   // D = P x F: lane l holds channel 32j + l%32; register v holds pixel
   // 8*(v/4) + 4*(l/32) + v%4 of the tile.  Pixels at or past qend get an
@@ -661,7 +657,7 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
 
 // Tiles m0, m0 + mstep, ... (< nmt) of pixels [qbeg, qend) against N tile j,
 // up to four per pass.
-template <int ELEM>
+template <int NT, int CS, int ELEM>
 __device__ __forceinline__ void band_wave(const BandArgs& p, const band_lds_t* Fs, const band_lds_t* Hs,
                                           __amdgpu_buffer_rsrc_t orc, int qbeg, int qend, int m0, int mstep,
                                           int j, int lane) {
@@ -672,17 +668,17 @@ __device__ __forceinline__ void band_wave(const BandArgs& p, const band_lds_t* F
   while (n > 0) {
     const int c = min(n, 4);
     switch (c) {
-      case 1: band_tiles<1, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
-      case 2: band_tiles<2, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
-      case 3: band_tiles<3, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
-      default: band_tiles<4, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 1: band_tiles<1, NT, CS, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 2: band_tiles<2, NT, CS, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      case 3: band_tiles<3, NT, CS, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
+      default: band_tiles<4, NT, CS, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
     }
     q0 += c * tstride;
     n -= c;
   }
 }
 
-template <int NT, int ELEM>
+template <int NT, int CS, int ELEM>
 __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char blds[];
   typedef __attribute__((address_space(3))) unsigned char lds_t;
@@ -740,7 +736,7 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
   const __amdgpu_buffer_rsrc_t orc =
       buffer_of(p.out + ((size_t)n * p.OH + r0) * p.OW * p.CO, (unsigned)(M * p.CO * 4));
 
-  band_wave<ELEM>(p, Fs, Hs, orc, 0, M, wave / NT, MSTEP, j, lane);
+  band_wave<NT, CS, ELEM>(p, Fs, Hs, orc, 0, M, wave / NT, MSTEP, j, lane);
 }
 
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
@@ -761,10 +757,10 @@ hipError_t launch_conv_t(const ConvArgs& a, dim3 grid, size_t lds, hipStream_t s
   return hipGetLastError();
 }
 
-template <int NT, int ELEM>
+template <int NT, int CS, int ELEM>
 hipError_t launch_band_t(const BandArgs& a, int bands, size_t lds, hipStream_t s) {
   static std::atomic<int> configured{0};
-  auto fn = conv2d_band_kernel<NT, ELEM>;
+  auto fn = conv2d_band_kernel<NT, CS, ELEM>;
   if (static_cast<int>(lds) > configured.load()) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -803,7 +799,8 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   const bool i8 = c.elem == xt::Elem::I8;
   const long long es = i8 ? 1 : 2;
   // a K step is 32 bytes of a pixel; steps go in pairs within a tap
-  if ((c.C * es) % 64 || c.CO % 32 || c.CO > 128 || c.CO == 96) return false;
+  // (and the unrolled taps take 2, 4, 6 or 8 steps: Cin * esize in {64, 128, 192, 256})
+  if ((c.C * es) % 64 || c.C * es > 256 || c.CO % 32 || c.CO > 128 || c.CO == 96) return false;
   const long long K = c.KH * c.KW * c.C;
   const long long filt_bytes = K * c.CO * es;
   if (filt_bytes % 1024) return false;
@@ -883,11 +880,19 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   if (bands > 0x7fffffff) return false;
   const int el = i8 ? kBandI8 : c.elem == xt::Elem::BF16 ? kBandBF16 : kBandF16;
   const int nt = a.CO / 32;
-#define XT_BAND(NTV)                                                             \
-  do {                                                                          \
-    if (el == kBandI8) e = launch_band_t<NTV, kBandI8>(a, (int)bands, lds, s);   \
-    else if (el == kBandBF16) e = launch_band_t<NTV, kBandBF16>(a, (int)bands, lds, s); \
-    else e = launch_band_t<NTV, kBandF16>(a, (int)bands, lds, s);                \
+  const int cs = (int)(PB / 32);  // K steps per tap: 2, 4, 6 or 8 (checked above)
+#define XT_BAND_E(NTV, CSV)                                                                \
+  do {                                                                                    \
+    if (el == kBandI8) e = launch_band_t<NTV, CSV, kBandI8>(a, (int)bands, lds, s);        \
+    else if (el == kBandBF16) e = launch_band_t<NTV, CSV, kBandBF16>(a, (int)bands, lds, s); \
+    else e = launch_band_t<NTV, CSV, kBandF16>(a, (int)bands, lds, s);                     \
+  } while (0)
+#define XT_BAND(NTV)                      \
+  do {                                    \
+    if (cs == 2) XT_BAND_E(NTV, 2);       \
+    else if (cs == 4) XT_BAND_E(NTV, 4);  \
+    else if (cs == 6) XT_BAND_E(NTV, 6);  \
+    else XT_BAND_E(NTV, 8);               \
   } while (0)
   switch (nt) {
     case 1: XT_BAND(1); break;
@@ -895,6 +900,7 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
     default: XT_BAND(4); break;
   }
 #undef XT_BAND
+#undef XT_BAND_E
   return true;
 }
 
