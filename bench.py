@@ -205,12 +205,10 @@ def gpu_time(module, host, dtypes, steps: int, warmup: int, use_graph: bool):
     return ms, mode, nsets, out
 
 
-def cpu_time(module, host, seconds: float):
-    """Rate of the oracle over whole repetitions of the workload."""
+def cpu_time(text: str, host, seconds: float, threads: int):
+    """Seconds per run of the oracle over whole repetitions of `text`."""
     import oracle
 
-    threads = int(os.environ.get("XT_CPU_THREADS", min(16, os.cpu_count() or 1)))
-    text = str(module)
     bufs = [np.array(h, copy=True) for h in host]
     reps = 0
     t0 = time.perf_counter()
@@ -220,7 +218,60 @@ def cpu_time(module, host, seconds: float):
         elapsed = time.perf_counter() - t0
         if elapsed >= seconds:
             break
-    return elapsed / reps, reps, threads
+    return elapsed / reps, reps
+
+
+_GRID = re.compile(r"xt\.grid = array<i32: (\d+), (\d+), (\d+)>")
+
+
+def grid_subset(text: str, fraction: float):
+    """The same program over a leading sub-grid holding about `fraction` of
+    the Blocks (Blocks are independent and do equal work, so the rate per
+    Block is that of the whole grid).  Returns (text, share of Blocks run)."""
+    m = _GRID.search(text)
+    g = [int(v) for v in m.groups()]
+    axis = max(range(3), key=lambda a: g[a])
+    keep = max(1, min(g[axis], math.ceil(g[axis] * fraction)))
+    share = keep / g[axis]
+    g[axis] = keep
+    return text[: m.start()] + f"xt.grid = array<i32: {g[0]}, {g[1]}, {g[2]}>" + text[m.end():], share
+
+
+def attainable():
+    """What a plain device copy and the vendor GEMM reach on this box: the
+    practical ceilings beside the published peaks."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    out = {}
+    n = (256 << 20) // 4
+    src = [torch.rand(n, device=dev) for _ in range(4)]
+    dst = [torch.empty_like(t) for t in src]
+    for i in range(8):
+        dst[i % 4].copy_(src[i % 4])
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(40):
+        dst[i % 4].copy_(src[i % 4])
+    end.record()
+    torch.cuda.synchronize()
+    out["hbm_copy_GBs"] = 40 * 2 * n * 4 / (start.elapsed_time(end) * 1e-3) / 1e9
+    del src, dst
+    a = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
+    b = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
+    for _ in range(10):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(200):
+        torch.matmul(a, b)
+    end.record()
+    torch.cuda.synchronize()
+    out["torch_matmul_f16_4096_TFLOPs"] = 200 * 2 * 4096**3 / (start.elapsed_time(end) * 1e-3) / 1e12
+    out["note"] = ("device copy of 256 MiB (read + write bytes) and torch.matmul (hipBLASLt) "
+                   "f16 4096^3 with f16 output, same process")
+    return out
 
 
 def measure(name: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool) -> dict:
@@ -264,16 +315,29 @@ def measure(name: str, steps: int, warmup: int, cpu_seconds: float, use_graph: b
         "algo_flops": plan["flops"],
     }
     if cpu_seconds > 0:
-        cpu_s, reps, threads = cpu_time(module, host, cpu_seconds)
-        cpu_value = (plan["bytes"] / cpu_s / 1e9) if meta["unit"] == "GB/s" else (
-            plan["flops"] / cpu_s / 1e12)
+        threads = int(os.environ.get("XT_CPU_THREADS", min(16, os.cpu_count() or 1)))
+        text = str(module)
+        work = plan["bytes"] if meta["unit"] == "GB/s" else plan["flops"]
+        scale = 1e9 if meta["unit"] == "GB/s" else 1e12
+        cpu_s, reps = cpu_time(text, host, cpu_seconds, threads)
+        # one thread, on a sub-grid sized to about 2 s
+        sub, share = grid_subset(text, min(1.0, 2.0 / max(cpu_s * threads, 1e-9)))
+        one_s, one_reps = cpu_time(sub, host, 0.5, 1)
+        try:
+            affinity = len(os.sched_getaffinity(0))
+        except AttributeError:
+            affinity = None
         result["cpu_baseline"] = {
-            "value": cpu_value,
+            "value": work / cpu_s / scale,
             "unit": meta["unit"],
             "cores": threads,
             "kind": "port",
             "sample": f"oracle/xt_oracle.c over the full workload, {reps} repetition(s), "
-                      f"{cpu_s * 1e3:.1f} ms each, {threads} OpenMP threads (nproc={os.cpu_count()})",
+                      f"{cpu_s * 1e3:.1f} ms each, {threads} OpenMP threads (nproc={os.cpu_count()}, "
+                      f"affinity={affinity})",
+            "value_1thread": work * share / one_s / scale,
+            "sample_1thread": f"{share:.4f} of the Blocks (a leading sub-grid), {one_reps} repetition(s), "
+                              f"{one_s * 1e3:.1f} ms each, 1 thread",
         }
     return result
 
@@ -320,6 +384,7 @@ def main(argv=None) -> int:
     headline = "c2" if "c2" in names else names[0]
     results = {n: measure(n, args.steps, args.warmup, args.cpu_seconds, not args.no_graph) for n in names}
     h = results[headline]
+    ceilings = attainable() if args.config == "all" else None
     line = {
         "metric": METRIC,
         "value": h["value"],
@@ -336,6 +401,7 @@ def main(argv=None) -> int:
         "config": {"workload": h["workload"], "kernel": h["kernel"], "timing": h["timing"]},
         "roofline": h["roofline"],
         "cpu_baseline": h.get("cpu_baseline"),
+        "attainable": ceilings,
         "per_config": [results[n] for n in names],
     }
     print(json.dumps(line), flush=True)
