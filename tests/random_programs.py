@@ -1,0 +1,143 @@
+"""Seeded random xt tile programs for the tile interpreter's parity tests.
+
+Each program loads one or two row tiles per Block (f32, f16, bf16 or i8
+memrefs), combines them with broadcast add / sub / mul, applies bounded unary
+ops, reduces along an axis, optionally transposes (through a rank-3 reshape)
+or multiplies by a loaded matrix, and stores an f32 result.  Values stay
+bounded (inputs in [-1, 1], exp of values <= 4) so that no program overflows,
+and the shapes keep every live tile small.
+
+`program(seed)` returns (xt text, host input arrays, dtypes, output index,
+output shape).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import f32_to_bf16_bits
+
+_ELEMS = ["f32", "f16", "bf16", "i8"]
+_UNARY = ["xt.exp", "xt.sin", "xt.cos", "xt.tanh", "xt.sigmoid", "xt.silu"]
+
+
+def _t(shape, e="f32"):
+    return "tensor<" + "x".join(map(str, shape)) + "x" + e + ">"
+
+
+def _m(shape, e="f32"):
+    return "memref<" + "x".join(map(str, shape)) + "x" + e + ">"
+
+
+def _host(rng, shape, e):
+    if e == "i8":
+        return rng.integers(-8, 9, shape, dtype=np.int8)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    if e == "f16":
+        return x.astype(np.float16)
+    if e == "bf16":
+        return f32_to_bf16_bits(x)
+    return x
+
+
+def program(seed: int):
+    rng = np.random.default_rng(seed)
+    grid = int(rng.integers(1, 5))
+    R = int(rng.choice([2, 4, 8, 16]))
+    C = int(rng.choice([4, 8, 16, 32, 64]))
+    ea = str(rng.choice(_ELEMS))
+    rows = grid * R
+    lines, args, host, dtypes = [], [], [], []
+    n = [0]
+
+    def fresh():
+        n[0] += 1
+        return f"%v{n[0]}"
+
+    def add_arg(shape, e):
+        name = f"%a{len(args)}"
+        args.append(f"{name}: {_m(shape, e)}")
+        host.append(_host(rng, shape, e))
+        dtypes.append(e)
+        return name
+
+    # x: the Block's R x C row tile of A
+    A = add_arg((rows, C), ea)
+    x = fresh()
+    lines.append(f"  {x} = xt.load({A}, %bid#0, %z) : ({_m((rows, C), ea)}, i32, i32) -> {_t((R, C), ea)}")
+    cur, cur_e, shape = x, ea, (R, C)
+    if ea == "i8":  # bring it to f32 (itof), the dialect's cast
+        y = fresh()
+        lines.append(f"  {y} = xt.itof({cur}) : {_t(shape, 'i8')} -> {_t(shape)}")
+        cur, cur_e = y, "f32"
+    # a broadcast operand: (1, C), (R, 1) or (R, C), f32, shared along the grid when it is a row
+    kind = int(rng.integers(0, 3))
+    bshape = [(1, C), (R, 1), (R, C)][kind]
+    bmem = (1, C) if kind == 0 else (rows, bshape[1])
+    Bn = add_arg(bmem, "f32")
+    b = fresh()
+    coords = "%z, %z" if kind == 0 else "%bid#0, %z"
+    shared = " {shared = 1 : i64}" if kind == 0 else ""
+    lines.append(f"  {b} = xt.load({Bn}, {coords}){shared} : ({_m(bmem)}, i32, i32) -> {_t(bshape)}")
+    if cur_e != "f32":  # f16 / bf16 tiles combine with f16 / bf16 operands only; use the load as is
+        y = fresh()
+        op = str(rng.choice(["xt.add", "xt.sub", "xt.mul"]))
+        lines.append(f"  {y} = {op}({cur}, {cur}) : {_t(shape, cur_e)}, {_t(shape, cur_e)} -> {_t(shape, cur_e)}")
+        cur = y
+        # store this narrow tile too (rounded like the oracle), then continue from f32 b
+        On = add_arg((rows, C), cur_e)
+        lines.append(f"  xt.store({cur}, {On}, %bid#0, %z) : ({_t(shape, cur_e)}, {_m((rows, C), cur_e)}, i32, i32) -> ()")
+        y = fresh()
+        lines.append(f"  {y} = xt.mul({b}, {b}) : {_t(bshape)}, {_t(bshape)} -> {_t(bshape)}")
+        cur, shape = y, bshape
+    else:
+        y = fresh()
+        op = str(rng.choice(["xt.add", "xt.sub", "xt.mul"]))
+        lines.append(f"  {y} = {op}({cur}, {b}) : {_t(shape)}, {_t(bshape)} -> {_t(shape)}")
+        cur = y
+    # one or two bounded unary ops
+    for _ in range(int(rng.integers(1, 3))):
+        y = fresh()
+        u = str(rng.choice(_UNARY))
+        lines.append(f"  {y} = {u}({cur}) : {_t(shape)} -> {_t(shape)}")
+        cur = y
+    # a keep-dim reduction broadcast back (rank 2 only)
+    if shape[0] > 1 and shape[1] > 1 and rng.random() < 0.7:
+        axis = int(rng.integers(0, 2))
+        red = str(rng.choice(["xt.reduce_sum", "xt.reduce_max"]))
+        rs = (1, shape[1]) if axis == 0 else (shape[0], 1)
+        r = fresh()
+        lines.append(f"  {r} = {red}({cur}) {{axis = {axis} : i64}} : {_t(shape)} -> {_t(rs)}")
+        y = fresh()
+        lines.append(f"  {y} = xt.sub({cur}, {r}) : {_t(shape)}, {_t(rs)} -> {_t(shape)}")
+        cur = y
+    # optionally a matmul by a loaded (C', N) matrix, or a transpose of the last two dims
+    tail = rng.random()
+    if tail < 0.35:
+        N = int(rng.choice([4, 8, 16]))
+        Wn = add_arg((shape[1], N), "f32")
+        w = fresh()
+        lines.append(f"  {w} = xt.load({Wn}, %z, %z) {{shared = 1 : i64}} : ({_m((shape[1], N))}, i32, i32) -> {_t((shape[1], N))}")
+        y = fresh()
+        lines.append(f"  {y} = xt.matmul({cur}, {w}) : {_t(shape)}, {_t((shape[1], N))} -> {_t((shape[0], N))}")
+        cur, shape = y, (shape[0], N)
+    elif tail < 0.6:
+        r3 = fresh()
+        lines.append(f"  {r3} = xt.reshape({cur}) : {_t(shape)} -> {_t((1,) + shape)}")
+        t3 = fresh()
+        lines.append(f"  {t3} = xt.transpose({r3}) : {_t((1,) + shape)} -> {_t((1, shape[1], shape[0]))}")
+        y = fresh()
+        lines.append(f"  {y} = xt.reshape({t3}) : {_t((1, shape[1], shape[0]))} -> {_t((shape[1], shape[0]))}")
+        cur, shape = y, (shape[1], shape[0])
+    out_shape = (grid * shape[0], shape[1])
+    On = add_arg(out_shape, "f32")
+    host[-1] = np.zeros(out_shape, np.float32)
+    lines.append(f"  xt.store({cur}, {On}, %bid#0, %z) : ({_t(shape)}, {_m(out_shape)}, i32, i32) -> ()")
+    head = (f"func.func @rnd{seed}({', '.join(args)}) attributes {{xt.grid = array<i32: {grid}, 1, 1>}} {{\n"
+            "  %bid:3 = xt.get_tile_block_id : i32, i32, i32\n  %z = arith.constant 0 : i32\n")
+    text = head + "\n".join(lines) + "\n  func.return\n}"
+    # narrow intermediate outputs start at zero too
+    for k, d in enumerate(dtypes):
+        if k > 0 and k != len(dtypes) - 1 and host[k].shape == (rows, C) and d == ea and d != "f32":
+            host[k] = np.zeros_like(host[k])
+    return text, host, dtypes, len(dtypes) - 1

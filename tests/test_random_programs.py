@@ -1,0 +1,22 @@
+"""Seeded random tile programs (tests/random_programs.py): every one plans
+onto a HIP kernel and runs in the oracle (CPU); on the GPU every one matches
+the oracle (test_gpu_random_programs.py)."""
+
+from __future__ import annotations
+
+import pytest
+
+import xtile_amd as xt
+from tests.gpu_util import run_oracle
+from tests.random_programs import program
+
+SEEDS = range(60)
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_program_plans_and_runs_in_the_oracle(seed):
+    text, host, dtypes, out = program(seed)
+    m = xt.parse(text)
+    assert xt.plan(m)["kernel"]
+    got = run_oracle(m, host, 1)
+    assert got[out].shape == host[out].shape
