@@ -20,7 +20,10 @@ from xtile_amd import kernels as K
     ],
 )
 def test_benchmark_configs_plan(name, kernel, nbytes, nflops):
-    """Algorithmic work per launch matches BASELINE.md's per-config table."""
+    """Algorithmic work per launch: C1 reads two and writes one 1024^2 f32
+    array; C2 reads and writes 8192 x 4096 f32; C3 / C5 are 2 M N K FLOP; C4
+    is 2 x pixels x Cout x (3 * 3 * 64) FLOP over input + filter + output
+    bytes."""
     p = xt.plan(K.CONFIGS[name]())
     assert p["kernel"] == kernel
     assert p["bytes"] == nbytes
