@@ -1,0 +1,149 @@
+"""GPU parity of fused tile programs (csrc/fused.cpp, compiled by hiprtc).
+
+Programs of loads, stores, unary / binary ops and reductions over one [R, C]
+tile and its [1, C] / [R, 1] / [1, 1] broadcasts are compiled into one kernel
+that keeps values in registers.  These tests cover the layouts the generator
+picks: a row spread over four waves (cross-wave row reduction through LDS),
+several rows per thread, a column reduction over 32 threads of a column,
+[R, 1] and [1, 1] stores, a buffer not aligned to the row vectors (which runs on
+the interpreter instead), and agreement with the interpreter (XTILE_AMD_FUSE=0).
+
+Bars: layernorm within 2e-5 absolute of the oracle (inputs of unit scale, a
+different summation order); column softmax within 1e-5 relative; programs
+without reductions bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import xtile_amd as xt
+from tests.conftest import oracle_threads
+from tests.gpu_util import run_gpu, run_oracle
+from xtile_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def _ln_inputs(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1.5, (rows, cols)).astype(np.float32)
+    g = rng.normal(1, 0.2, (1, cols)).astype(np.float32)
+    b = rng.normal(0, 0.2, (1, cols)).astype(np.float32)
+    return [x, g, b, np.full((1, 1), 1.0 / cols, np.float32), np.full((1, 1), 1e-5, np.float32), np.zeros_like(x)]
+
+
+@pytest.mark.parametrize(
+    "rows,cols,trow,layout",
+    [
+        (256, 4096, 1, "tile=1x4096 threads=1x256"),   # a row over 4 waves
+        (256, 4096, 4, "tile=4x4096 threads=1x256"),   # 4 rows per thread, 64 values each
+        (512, 1024, 2, "tile=2x1024 threads=1x256"),
+        (96, 48, 16, "tile=16x48 threads=16x4"),       # 48 columns: 12 vectors, 4 threads a row
+    ],
+)
+def test_fused_layernorm(cuda, rows, cols, trow, layout):
+    m = K.layernorm(rows, cols, trow)
+    assert xt.plan(m)["kernel"].startswith("fused f32 " + layout)
+    bufs = _ln_inputs(rows, cols, 41)
+    got = run_gpu(m, bufs, ["f32"] * 6, cuda, case=f"fused layernorm {rows}x{cols}/{trow}")[5]
+    want = run_oracle(m, bufs, oracle_threads())[5]
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("rows,cols,tcol", [(512, 64, 32), (256, 256, 8)])
+def test_fused_column_softmax(cuda, rows, cols, tcol):
+    m = K.column_softmax(rows, cols, tcol)
+    desc = xt.plan(m)["kernel"]
+    assert desc.startswith("fused"), desc
+    rng = np.random.default_rng(42)
+    x = rng.normal(0, 2, (rows, cols)).astype(np.float32)
+    got = run_gpu(m, [x, np.zeros_like(x)], ["f32"] * 2, cuda, case=f"fused column softmax {rows}x{cols}/{tcol}")[1]
+    want = run_oracle(m, [x, np.zeros_like(x)], oracle_threads())[1]
+    assert np.max(np.abs(got - want) / np.abs(want)) <= 1e-5
+    np.testing.assert_allclose(got.sum(axis=0), 1.0, atol=1e-5)
+
+
+_STATS = """
+func.func @stats(%x: memref<64x256xf32>, %rs: memref<64x1xf32>, %cm: memref<4x256xf32>, %t: memref<4x1xf32>, %y: memref<64x256xi8>) attributes {xt.grid = array<i32: 4, 1, 1>} {
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %z = arith.constant 0 : i32
+  %0 = xt.load(%x, %bid#0, %z) : (memref<64x256xf32>, i32, i32) -> tensor<16x256xf32>
+  %1 = xt.reduce_sum(%0) {axis = 1 : i64} : tensor<16x256xf32> -> tensor<16x1xf32>
+  xt.store(%1, %rs, %bid#0, %z) : (tensor<16x1xf32>, memref<64x1xf32>, i32, i32) -> ()
+  %2 = xt.reduce_max(%0) {axis = 0 : i64} : tensor<16x256xf32> -> tensor<1x256xf32>
+  xt.store(%2, %cm, %bid#0, %z) : (tensor<1x256xf32>, memref<4x256xf32>, i32, i32) -> ()
+  %3 = xt.reduce_max(%1) {axis = 0 : i64} : tensor<16x1xf32> -> tensor<1x1xf32>
+  xt.store(%3, %t, %bid#0, %z) : (tensor<1x1xf32>, memref<4x1xf32>, i32, i32) -> ()
+  %4 = xt.sub(%0, %1) : tensor<16x256xf32>, tensor<16x1xf32> -> tensor<16x256xf32>
+  %5 = xt.ftoi(%4) : tensor<16x256xf32> -> tensor<16x256xi8>
+  xt.store(%5, %y, %bid#0, %z) : (tensor<16x256xi8>, memref<64x256xi8>, i32, i32) -> ()
+  func.return
+}
+"""
+
+
+def test_fused_row_column_and_scalar_stores(cuda):
+    """Row sums ([R, 1] store by one thread a row), column maxima of each Block ([1, C]
+    store), the largest row sum ([1, 1] store by one thread) and an i8 store
+    (ftoi: round, saturate) of a two-sided broadcast difference."""
+    m = xt.parse(_STATS)
+    desc = xt.plan(m)["kernel"]
+    assert desc.startswith("fused"), desc
+    rng = np.random.default_rng(43)
+    x = rng.normal(0, 1, (64, 256)).astype(np.float32)
+    bufs = [x, np.zeros((64, 1), np.float32), np.zeros((4, 256), np.float32), np.zeros((4, 1), np.float32),
+            np.zeros((64, 256), np.int8)]
+    dts = ["f32", "f32", "f32", "f32", "i8"]
+    got = run_gpu(m, bufs, dts, cuda, case="fused stats")
+    want = run_oracle(m, bufs, 1)
+    scale = np.abs(x).sum(axis=1).max()
+    np.testing.assert_allclose(got[1], want[1], rtol=0, atol=1e-5 * scale)
+    assert np.array_equal(got[2], want[2])  # max is exact in any order
+    np.testing.assert_allclose(got[3], want[3], rtol=0, atol=1e-5 * scale)
+    # i8 of x - rowsum: one rounding of a difference whose rowsum may differ in the last bits
+    d = np.abs(got[4].astype(np.int32) - want[4].astype(np.int32))
+    assert d.max() <= 1
+
+
+def test_fused_matches_the_interpreter_bit_exact_without_reductions(cuda, monkeypatch):
+    rng = np.random.default_rng(44)
+    a = rng.normal(0, 1, (128, 256)).astype(np.float32)
+    v = rng.normal(0, 1, (1, 256)).astype(np.float32)
+    fused = K.bias_add(128, 256)
+    assert xt.plan(fused)["kernel"].startswith("fused")
+    got = run_gpu(fused, [a, v, np.zeros_like(a)], ["f32"] * 3, cuda, case="fused bias add")[2]
+    monkeypatch.setenv("XTILE_AMD_FUSE", "0")
+    interp = K.bias_add(128, 256)
+    assert xt.plan(interp)["kernel"].startswith("tile_vm")
+    ref = run_gpu(interp, [a, v, np.zeros_like(a)], ["f32"] * 3, cuda, case="interpreted bias add")[2]
+    assert np.array_equal(got, ref)
+    assert np.array_equal(got, a + v)
+
+
+def test_fused_and_interpreted_layernorm_agree(cuda, monkeypatch):
+    bufs = _ln_inputs(128, 64, 45)
+    got = run_gpu(K.layernorm(128, 64, 64), bufs, ["f32"] * 6, cuda, case="fused layernorm 128x64")[5]
+    monkeypatch.setenv("XTILE_AMD_FUSE", "0")
+    ref = run_gpu(K.layernorm(128, 64, 64), bufs, ["f32"] * 6, cuda, case="interpreted layernorm 128x64")[5]
+    np.testing.assert_allclose(got, ref, rtol=0, atol=2e-5)
+
+
+def test_misaligned_buffer_runs_on_the_interpreter(cuda):
+    """A buffer offset by one f32 cannot be read as 16-byte vectors: the
+    launch takes the interpreter for it and the result is unchanged."""
+    import torch
+
+    m = K.bias_add(128, 256)
+    assert "vw=4" in xt.plan(m)["kernel"]
+    rng = np.random.default_rng(46)
+    a = rng.normal(0, 1, (128, 256)).astype(np.float32)
+    v = rng.normal(0, 1, (1, 256)).astype(np.float32)
+    print("[gpu] misaligned bias add", flush=True)
+    store = torch.zeros(128 * 256 + 1, dtype=torch.float32, device=cuda)
+    out = store[1:].view(128, 256)
+    assert out.data_ptr() % 16 == 4
+    xt.launch(m, torch.from_numpy(a).to(cuda), torch.from_numpy(v).to(cuda), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), a + v)

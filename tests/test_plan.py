@@ -70,12 +70,15 @@ def test_conv_inside_a_larger_program_gives_the_conv_form():
     "name,kernel",
     [
         ("unary_and_shape", "tile_vm f32 insts=12 loads=2 stores=3 lds="),
-        ("column_reduce", "tile_vm f32 insts=3 loads=1 stores=1 lds="),
-        ("divide_kernel", "tile_vm f32 insts=5 loads=2 stores=1 lds="),
+        ("column_reduce", "fused f32 tile=8x8 threads=8x2 vw=4 insts=3 "),
+        ("divide_kernel", "fused f32 tile=8x8 threads=8x2 vw=4 insts=5 "),
         ("compute_ops", "tile_vm f32 insts=5 loads=3 stores=1 lds="),
     ],
 )
 def test_general_programs_plan_onto_the_tile_interpreter(name, kernel):
+    """Programs of loads, stores, unary / binary ops and reductions over one
+    [R, C] tile and its broadcasts are compiled into a fused kernel; the rest
+    (rank-3 tiles, matmul, transposes) run on the interpreter."""
     from tests.golden.dsl_programs import programs
     from xtile_amd import dsl
 
@@ -84,10 +87,19 @@ def test_general_programs_plan_onto_the_tile_interpreter(name, kernel):
     assert xt.plan(m)["kernel"].startswith(kernel)
 
 
-def test_interpreter_programs_and_lds_budget():
-    assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith("tile_vm f32 insts=17 loads=5 stores=1")
-    assert xt.plan(K.column_softmax(64, 128, 32))["kernel"].startswith("tile_vm")
-    assert xt.plan(K.bias_add(128, 256))["kernel"].startswith("tile_vm")
+def test_interpreter_programs_and_lds_budget(monkeypatch):
+    assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith("fused f32 tile=64x64 threads=16x16 vw=4 insts=17")
+    assert xt.plan(K.layernorm(8192, 4096, 1))["kernel"].startswith("fused f32 tile=1x4096 threads=1x256 vw=4")
+    # fused kernels hold values in registers, so the interpreter's LDS budget does not bind them
+    assert xt.plan(K.layernorm(8192, 4096, 4))["kernel"].startswith("fused f32 tile=4x4096 threads=1x256 vw=4")
+    assert xt.plan(K.column_softmax(64, 128, 32))["kernel"].startswith("fused f32 tile=64x32 threads=32x8")
+    assert xt.plan(K.bias_add(128, 256))["kernel"].startswith("fused f32 tile=32x64 threads=16x16")
+    monkeypatch.setenv("XTILE_AMD_FUSE", "0")
+    assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith(
+        "tile_vm f32 insts=17 loads=5 stores=1 lds=50208B (not fused: XTILE_AMD_FUSE=0)")
+    with pytest.raises(NotImplementedError, match="KB of LDS"):
+        xt.plan(K.layernorm(8192, 4096, 4))
+    monkeypatch.delenv("XTILE_AMD_FUSE")
     # live tiles beyond 160 KB of LDS are refused on the host
     with pytest.raises(NotImplementedError, match="KB of LDS"):
         xt.plan(K.layernorm(512, 256, 256))

@@ -30,9 +30,9 @@ HIPCC = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
 CXX = shutil.which("g++") or "g++"
 ARCH = "gfx950"
 
-HOST_SOURCES = ["ir.cpp", "verify.cpp", "passes.cpp", "plan.cpp", "to_nova.cpp"]
+HOST_SOURCES = ["ir.cpp", "verify.cpp", "passes.cpp", "plan.cpp", "fused.cpp", "to_nova.cpp"]
 KERNEL_SOURCES = ["kernels/elementwise.hip", "kernels/gemm.hip", "kernels/conv.hip", "kernels/conv_general.hip",
-                  "kernels/tilevm.hip"]
+                  "kernels/tilevm.hip", "kernels/fused_jit.cpp"]
 HOST_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 # Packed-FP32 instruction forms are disabled for every HIP compile.
 HIP_FLAGS = [
@@ -101,6 +101,9 @@ def build(verbose: bool = False) -> Path:
             *map(str, host_objs),
             str(rt_obj),
             *map(str, kern_objs),
+            f"-L{ROCM}/lib",
+            "-lhiprtc",
+            f"-Wl,-rpath,{ROCM}/lib",
             "-o",
             str(tmp),
         ]

@@ -1,0 +1,448 @@
+// Fused tile programs: the tile interpreter's lowering of a program (VmPlan)
+// turned into the source of one HIP kernel that keeps every value in
+// registers.  The runtime compiles the source with hiprtc (jit.cpp).
+//
+// Layout.  The program's main tile is [R, C] (the largest extents of its
+// values); every value is that tile or a [1, C], [R, 1] or [1, 1] broadcast of
+// it.  A workgroup of TR x TC threads runs one Block; thread (tr, tc) owns rows
+// tr + sr TR (sr < SR = R / TR) and column vectors tc + sc TC (sc < SC = C /
+// (VW TC)) of VW consecutive columns, so each row access is a VW-wide vector
+// load or store and consecutive threads touch consecutive vectors.  A [1, C]
+// value is held by every tr, an [R, 1] value by every tc, a [1, 1] value by
+// every thread: broadcasts are register reads.
+//
+// Ops (the interpreter's semantics, kernels/tilevm.hip): loads convert f16 /
+// bf16 / i8 exactly and stores round (nearest even for f16 / bf16; round,
+// saturate and NaN -> 0 for i8); add / sub / mul and the unary ops use the same
+// f32 formulas with contraction off; reductions keep the reduced dim at 1 and
+// combine within a thread, then across the TC threads of a row by lane
+// shuffles (and LDS when a row spans waves), or across the TR threads of a
+// column through LDS.
+#include <algorithm>
+#include <map>
+#include <sstream>
+
+#include "plan.h"
+
+namespace xt {
+namespace {
+
+const char* kPreamble = R"(
+typedef float xf4 __attribute__((ext_vector_type(4)));
+typedef float xf2 __attribute__((ext_vector_type(2)));
+typedef _Float16 xh4 __attribute__((ext_vector_type(4)));
+typedef _Float16 xh2 __attribute__((ext_vector_type(2)));
+typedef unsigned short xu4 __attribute__((ext_vector_type(4)));
+typedef unsigned short xu2 __attribute__((ext_vector_type(2)));
+typedef signed char xc4 __attribute__((ext_vector_type(4)));
+typedef signed char xc2 __attribute__((ext_vector_type(2)));
+struct FusedArgs { void* p[8]; };
+__device__ __forceinline__ float xbf(unsigned short u) { return __uint_as_float((unsigned)u << 16); }
+__device__ __forceinline__ unsigned short xto_f16(float f) {
+  const unsigned u = __float_as_uint(f);
+  const unsigned sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (unsigned short)(sign | 0x7e00u);
+  if (a >= 0x477ff000u) return (unsigned short)(sign | 0x7c00u);
+  if (a < 0x38800000u) return (unsigned short)(sign | (unsigned)rintf(__uint_as_float(a) * 16777216.0f));
+  unsigned out = (((a >> 23) - 112u) << 10) | ((a >> 13) & 0x3ffu);
+  const unsigned rem = a & 0x1fffu;
+  out += (rem > 0x1000u || (rem == 0x1000u && (out & 1u))) ? 1u : 0u;
+  return (unsigned short)(sign | out);
+}
+__device__ __forceinline__ unsigned short xto_bf16(float f) {
+  const unsigned x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((x >> 16) | 0x40u);
+  return (unsigned short)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float xto_i8(float v) {
+  if (v != v) return 0.0f;
+  return fminf(fmaxf(rintf(v), -128.0f), 127.0f);
+}
+)";
+
+struct Layout {
+  int R = 1, C = 1, VW = 1, TR = 1, TC = 1, SR = 1, SC = 1;
+  int threads() const { return TR * TC; }
+  int cols() const { return SC * VW; }  // register columns of a thread
+};
+
+struct VKind {
+  bool r = false, c = false;  // varies along R / along C
+};
+
+int pow2_divisor(int v, int cap) {
+  int p = 1;
+  while (p * 2 <= cap && v % (p * 2) == 0) p *= 2;
+  return p;
+}
+
+const char* unary_expr(int k) {
+  switch (static_cast<VmUnary>(k)) {
+    case VmUnary::Exp: return "expf(X)";
+    case VmUnary::Cos: return "cosf(X)";
+    case VmUnary::Sin: return "sinf(X)";
+    case VmUnary::Recip: return "1.0f / (X)";
+    case VmUnary::Rsqrt: return "1.0f / sqrtf(X)";
+    case VmUnary::Sigmoid: return "1.0f / (1.0f + expf(-(X)))";
+    case VmUnary::Tanh: return "tanhf(X)";
+    case VmUnary::Silu: return "(X) * (1.0f / (1.0f + expf(-(X))))";
+    default: return "xto_i8(X)";
+  }
+}
+
+std::string replace_x(const char* pattern, const std::string& x) {
+  std::string s(pattern), out;
+  for (char ch : s) {
+    if (ch == 'X') out += x;
+    else out += ch;
+  }
+  return out;
+}
+
+class Gen {
+ public:
+  Gen(const VmPlan& vm, const int32_t grid[3]) : vm_(vm) {
+    for (int d = 0; d < 3; ++d) grid_[d] = grid[d];
+  }
+
+  bool run(FusedPlan& out, std::string& why) {
+    if (!shapes(why) || !layout(why)) return false;
+    std::ostringstream k;
+    k << "extern \"C\" __global__ void __launch_bounds__(" << L.threads() << ") xt_fused(FusedArgs a) {\n"
+      << "#pragma clang fp contract(off)\n"
+      << "  const int t = threadIdx.x, tc = t % " << L.TC << ", tr = t / " << L.TC << ";\n"
+      << "  const int bid = blockIdx.x, x = bid % " << grid_[0] << ", y = (bid / " << grid_[0] << ") % " << grid_[1]
+      << ", z = bid / " << (long long)grid_[0] * grid_[1] << ";\n"
+      << "  (void)x; (void)y; (void)z; (void)tr; (void)tc;\n";
+    body_.str("");
+    for (size_t i = 0; i < vm_.inst.size(); ++i)
+      if (!emit(static_cast<int>(i), why)) return false;
+    if (red_floats_ > 0) k << "  __shared__ float red[" << red_floats_ << "];\n";
+    k << body_.str() << "}\n";
+    out.source = std::string(kPreamble) + k.str();
+    out.threads = L.threads();
+    out.vw = L.VW;
+    std::ostringstream lay;
+    lay << "fused f32 tile=" << L.R << "x" << L.C << " threads=" << L.TR << "x" << L.TC << " vw=" << L.VW;
+    out.layout = lay.str();
+    return true;
+  }
+
+ private:
+  const VmPlan& vm_;
+  int grid_[3];
+  Layout L;
+  std::map<int, std::pair<int, VKind>> slot_;  // LDS slot -> (value id, kind)
+  std::ostringstream body_;
+  int red_floats_ = 0;
+
+  static void dims2(const int d[3], int& a, int& b) {
+    a = d[1];
+    b = d[2];
+  }
+
+  // every value: rank <= 2 and a broadcast of one [R, C]
+  bool shapes(std::string& why) {
+    int R = 1, C = 1;
+    std::vector<std::pair<int, int>> all;
+    for (const VmInst& in : vm_.inst) {
+      if (in.op != VmOp::Load && in.op != VmOp::Store && in.op != VmOp::Unary && in.op != VmOp::Binary &&
+          in.op != VmOp::Reduce) {
+        why = "fused kernels take loads, stores, unary, binary and reduce ops";
+        return false;
+      }
+      if (in.dims[0] != 1 || (in.op == VmOp::Binary && (in.aux[0] != 1 || in.lhs[0] != 1))) {
+        why = "fused kernels take tiles of rank <= 2";
+        return false;
+      }
+      all.push_back({in.dims[1], in.dims[2]});
+      if (in.op == VmOp::Binary) {
+        all.push_back({in.aux[1], in.aux[2]});
+        all.push_back({in.lhs[1], in.lhs[2]});
+      }
+    }
+    for (auto& s : all) {
+      R = std::max(R, s.first);
+      C = std::max(C, s.second);
+    }
+    for (auto& s : all)
+      if ((s.first != 1 && s.first != R) || (s.second != 1 && s.second != C)) {
+        why = "fused kernels need every value to be one [R, C] tile or a broadcast of it";
+        return false;
+      }
+    L.R = R;
+    L.C = C;
+    return true;
+  }
+
+  bool layout(std::string& why) {
+    int vw = 4;
+    for (; vw > 1; vw /= 2) {
+      if (L.C % vw) continue;
+      bool ok = true;
+      for (size_t k = 0; k < vm_.inst.size() && ok; ++k) {
+        const VmInst& in = vm_.inst[k];
+        if ((in.op != VmOp::Load && in.op != VmOp::Store) || in.dims[2] == 1) continue;
+        const VmAccess& acc = vm_.access[in.kind];
+        const TileAddr& o = acc.addr;
+        ok = acc.stride[2] == 1 && acc.stride[1] % vw == 0 && o.c0 % vw == 0 && o.sx % vw == 0 &&
+             o.sy % vw == 0 && o.sz % vw == 0;
+      }
+      if (ok) break;
+    }
+    L.VW = vw;
+    const int cv = L.C / L.VW;
+    L.TC = pow2_divisor(cv, 256);
+    L.TR = pow2_divisor(L.R, 256 / L.TC);
+    L.SR = L.R / L.TR;
+    L.SC = cv / L.TC;
+    if (L.SR * L.cols() > 64) {
+      why = "fused kernels keep at most 64 elements of a tile per thread";
+      return false;
+    }
+    return true;
+  }
+
+  int size_of(VKind k) const { return (k.r ? L.SR : 1) * (k.c ? L.cols() : 1); }
+  std::string idx(VKind k, const std::string& sr, const std::string& j) const {
+    std::string s;
+    if (k.r) s += sr + " * " + std::to_string(k.c ? L.cols() : 1);
+    if (k.c) s += (s.empty() ? "" : " + ") + j;
+    return s.empty() ? "0" : s;
+  }
+  static VKind kind_of(int d1, int d2) { return VKind{d1 != 1, d2 != 1}; }
+
+  std::string origin(const TileAddr& o) const {
+    std::ostringstream s;
+    s << "(" << o.c0 << "LL + (long long)x * " << o.sx << "LL + (long long)y * " << o.sy << "LL + (long long)z * "
+      << o.sz << "LL)";
+    return s.str();
+  }
+
+  // element offset of register (sr, sc) of a tile of kind k (row pitch ld)
+  std::string elem_off(VKind k, long long ld) const {
+    std::string s = "0";
+    if (k.r) s = "(long long)(tr + sr * " + std::to_string(L.TR) + ") * " + std::to_string(ld) + "LL";
+    if (k.c) s += " + (long long)(tc + sc * " + std::to_string(L.TC) + ") * " + std::to_string(L.VW);
+    return s;
+  }
+
+  bool emit(int i, std::string& why) {
+    const VmInst& in = vm_.inst[i];
+    std::ostringstream& b = body_;
+    const std::string v = "v" + std::to_string(i);
+    switch (in.op) {
+      case VmOp::Load: {
+        const VmAccess& acc = vm_.access[in.kind];
+        const VKind k = kind_of(in.dims[1], in.dims[2]);
+        const int vw = k.c ? L.VW : 1;
+        b << "  float " << v << "[" << size_of(k) << "];\n  {\n";
+        b << "    const long long org = " << origin(acc.addr) << ";\n";
+        b << "#pragma unroll\n    for (int sr = 0; sr < " << (k.r ? L.SR : 1) << "; ++sr)\n";
+        b << "#pragma unroll\n    for (int sc = 0; sc < " << (k.c ? L.SC : 1) << "; ++sc) {\n";
+        b << "      const long long off = org + " << elem_off(k, acc.stride[1]) << ";\n";
+        const std::string dst = v + "[" + idx(k, "sr", "sc * " + std::to_string(vw) + " + e") + "]";
+        load_code(b, in.kind, acc.elem, vw, dst);
+        b << "    }\n  }\n";
+        slot_[in.dst] = {i, k};
+        return true;
+      }
+      case VmOp::Store: {
+        const VmAccess& acc = vm_.access[in.kind];
+        const VKind k = kind_of(in.dims[1], in.dims[2]);
+        auto it = slot_.find(in.a);
+        if (it == slot_.end()) return fail(why, "store of an unknown value");
+        const VKind vk = it->second.second;
+        if (vk.r != k.r || vk.c != k.c) return fail(why, "store of a value with another shape");
+        const std::string src = "v" + std::to_string(it->second.first);
+        const int vw = k.c ? L.VW : 1;
+        // a broadcast value is held by every thread along its unit dim; one stores it
+        std::string guard;
+        if (!k.r && L.TR > 1) guard = "tr == 0";
+        if (!k.c && L.TC > 1) guard += std::string(guard.empty() ? "" : " && ") + "tc == 0";
+        b << "  if (" << (guard.empty() ? "true" : guard) << ") {\n";
+        b << "    const long long org = " << origin(acc.addr) << ";\n";
+        b << "#pragma unroll\n    for (int sr = 0; sr < " << (k.r ? L.SR : 1) << "; ++sr)\n";
+        b << "#pragma unroll\n    for (int sc = 0; sc < " << (k.c ? L.SC : 1) << "; ++sc) {\n";
+        b << "      const long long off = org + " << elem_off(k, acc.stride[1]) << ";\n";
+        const std::string s = src + "[" + idx(k, "sr", "sc * " + std::to_string(vw) + " + e") + "]";
+        store_code(b, in.kind, acc.elem, vw, s);
+        b << "    }\n  }\n";
+        return true;
+      }
+      case VmOp::Unary: {
+        auto it = slot_.find(in.a);
+        if (it == slot_.end()) return fail(why, "unary op of an unknown value");
+        const VKind k = it->second.second;
+        const std::string a = "v" + std::to_string(it->second.first);
+        b << "  float " << v << "[" << size_of(k) << "];\n";
+        b << "#pragma unroll\n  for (int q = 0; q < " << size_of(k) << "; ++q) " << v
+          << "[q] = " << replace_x(unary_expr(in.kind), a + "[q]") << ";\n";
+        slot_[in.dst] = {i, k};
+        return true;
+      }
+      case VmOp::Binary: {
+        auto ia = slot_.find(in.a), ib = slot_.find(in.b);
+        if (ia == slot_.end() || ib == slot_.end()) return fail(why, "binary op of an unknown value");
+        const VKind ka = ia->second.second, kb = ib->second.second;
+        const VKind ko = VKind{ka.r || kb.r, ka.c || kb.c};
+        if (ko.r != (in.dims[1] != 1) || ko.c != (in.dims[2] != 1))
+          return fail(why, "binary op result shape outside the fused layout");
+        const char* op = in.kind == 0 ? "+" : in.kind == 1 ? "-" : "*";
+        const std::string a = "v" + std::to_string(ia->second.first), c = "v" + std::to_string(ib->second.first);
+        b << "  float " << v << "[" << size_of(ko) << "];\n";
+        b << "#pragma unroll\n  for (int sr = 0; sr < " << (ko.r ? L.SR : 1) << "; ++sr)\n";
+        b << "#pragma unroll\n  for (int j = 0; j < " << (ko.c ? L.cols() : 1) << "; ++j) " << v << "["
+          << idx(ko, "sr", "j") << "] = " << a << "[" << idx(ka, "sr", "j") << "] " << op << " " << c << "["
+          << idx(kb, "sr", "j") << "];\n";
+        slot_[in.dst] = {i, ko};
+        return true;
+      }
+      case VmOp::Reduce: {
+        auto it = slot_.find(in.a);
+        if (it == slot_.end()) return fail(why, "reduction of an unknown value");
+        const VKind ks = it->second.second;
+        const std::string s = "v" + std::to_string(it->second.first);
+        const bool is_max = in.kind == 1;
+        const std::string init = is_max ? "-__builtin_huge_valf()" : "0.0f";
+        auto comb = [&](const std::string& p, const std::string& q) {
+          return is_max ? "fmaxf(" + p + ", " + q + ")" : p + " + " + q;
+        };
+        const int axis = in.aux[0];
+        if ((axis == 1 && !ks.c) || (axis == 0 && !ks.r)) {  // over an extent of 1: a copy
+          b << "  float " << v << "[" << size_of(ks) << "];\n";
+          b << "#pragma unroll\n  for (int q = 0; q < " << size_of(ks) << "; ++q) " << v << "[q] = " << s
+            << "[q];\n";
+          slot_[in.dst] = {i, ks};
+          return true;
+        }
+        if (axis == 1) {  // over columns: within the thread, then across the TC threads of the row
+          const VKind ko{ks.r, false};
+          const int nr = ks.r ? L.SR : 1;
+          b << "  float " << v << "[" << nr << "];\n";
+          b << "#pragma unroll\n  for (int sr = 0; sr < " << nr << "; ++sr) {\n    float m = " << init << ";\n";
+          b << "#pragma unroll\n    for (int j = 0; j < " << L.cols() << "; ++j) m = "
+            << comb("m", s + "[" + idx(ks, "sr", "j") + "]") << ";\n";
+          const int w = std::min(L.TC, 64);
+          b << "#pragma unroll\n    for (int o = " << w / 2 << "; o > 0; o >>= 1) m = "
+            << comb("m", "__shfl_xor(m, o, 64)") << ";\n";
+          b << "    " << v << "[sr] = m;\n  }\n";
+          if (L.TC > 64) {  // the row spans TC / 64 waves: combine through LDS
+            const int W = L.TC / 64;
+            red_floats_ = std::max(red_floats_, nr * L.TR * W);
+            b << "  __syncthreads();\n";
+            b << "  if ((tc & 63) == 0) {\n#pragma unroll\n    for (int sr = 0; sr < " << nr
+              << "; ++sr) red[(sr * " << L.TR << " + tr) * " << W << " + (tc >> 6)] = " << v << "[sr];\n  }\n";
+            b << "  __syncthreads();\n";
+            b << "#pragma unroll\n  for (int sr = 0; sr < " << nr << "; ++sr) {\n    float m = red[(sr * " << L.TR
+              << " + tr) * " << W << "];\n";
+            b << "#pragma unroll\n    for (int q = 1; q < " << W << "; ++q) m = "
+              << comb("m", "red[(sr * " + std::to_string(L.TR) + " + tr) * " + std::to_string(W) + " + q]")
+              << ";\n    " << v << "[sr] = m;\n  }\n";
+          }
+          slot_[in.dst] = {i, ko};
+          return true;
+        }
+        // over rows: within the thread, then across the TR threads of the column through LDS
+        const VKind ko{false, ks.c};
+        const int nc = ks.c ? L.cols() : 1;
+        b << "  float " << v << "[" << nc << "];\n";
+        b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) {\n    float m = " << init << ";\n";
+        b << "#pragma unroll\n    for (int sr = 0; sr < " << L.SR << "; ++sr) m = "
+          << comb("m", s + "[" + idx(ks, "sr", "j") + "]") << ";\n    " << v << "[j] = m;\n  }\n";
+        if (L.TR > 1) {
+          red_floats_ = std::max(red_floats_, L.threads() * nc);
+          b << "  __syncthreads();\n";
+          b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) red[t * " << nc << " + j] = " << v
+            << "[j];\n";
+          b << "  __syncthreads();\n";
+          b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) {\n    float m = red[tc * " << nc
+            << " + j];\n";
+          b << "#pragma unroll\n    for (int q = 1; q < " << L.TR << "; ++q) m = "
+            << comb("m", "red[(q * " + std::to_string(L.TC) + " + tc) * " + std::to_string(nc) + " + j]")
+            << ";\n    " << v << "[j] = m;\n  }\n";
+        }
+        slot_[in.dst] = {i, ko};
+        return true;
+      }
+      default:
+        return fail(why, "unsupported op in a fused kernel");
+    }
+  }
+
+  static bool fail(std::string& why, const char* msg) {
+    why = msg;
+    return false;
+  }
+
+  // vw consecutive elements at `off` -> dst (an expression in e = 0..vw-1)
+  void load_code(std::ostringstream& b, int acc, Elem e, int vw, const std::string& dst) const {
+    const std::string P = "a.p[" + std::to_string(acc) + "]";
+    std::string ty, conv;
+    switch (e) {
+      case Elem::F32: ty = vw == 4 ? "xf4" : vw == 2 ? "xf2" : "float"; conv = "q"; break;
+      case Elem::F16: ty = vw == 4 ? "xh4" : vw == 2 ? "xh2" : "_Float16"; conv = "(float)q"; break;
+      case Elem::BF16: ty = vw == 4 ? "xu4" : vw == 2 ? "xu2" : "unsigned short"; conv = "xbf(q)"; break;
+      default: ty = vw == 4 ? "xc4" : vw == 2 ? "xc2" : "signed char"; conv = "(float)q"; break;
+    }
+    const char* base = e == Elem::F32 ? "float" : e == Elem::F16 ? "_Float16" : e == Elem::BF16 ? "unsigned short"
+                                                                                                 : "signed char";
+    b << "      const " << ty << " qv = *reinterpret_cast<const " << ty << "*>(static_cast<const " << base
+      << "*>(" << P << ") + off);\n";
+    if (vw == 1) {
+      b << "      { const int e = 0; const auto q = qv; " << dst << " = " << conv << "; }\n";
+    } else {
+      b << "#pragma unroll\n      for (int e = 0; e < " << vw << "; ++e) { const auto q = qv[e]; " << dst << " = "
+        << conv << "; }\n";
+    }
+  }
+
+  void store_code(std::ostringstream& b, int acc, Elem e, int vw, const std::string& src) const {
+    const std::string P = "a.p[" + std::to_string(acc) + "]";
+    std::string ty, conv;
+    switch (e) {
+      case Elem::F32: ty = vw == 4 ? "xf4" : vw == 2 ? "xf2" : "float"; conv = "w"; break;
+      case Elem::F16: ty = vw == 4 ? "xu4" : vw == 2 ? "xu2" : "unsigned short"; conv = "xto_f16(w)"; break;
+      case Elem::BF16: ty = vw == 4 ? "xu4" : vw == 2 ? "xu2" : "unsigned short"; conv = "xto_bf16(w)"; break;
+      default: ty = vw == 4 ? "xc4" : vw == 2 ? "xc2" : "signed char"; conv = "(signed char)xto_i8(w)"; break;
+    }
+    const char* base = e == Elem::F32 ? "float" : (e == Elem::F16 || e == Elem::BF16) ? "unsigned short"
+                                                                                         : "signed char";
+    if (vw == 1) {
+      b << "      { const int e = 0; const float w = " << src << "; *(static_cast<" << base
+        << "*>(" << P << ") + off) = " << conv << "; }\n";
+    } else {
+      b << "      " << ty << " qv;\n#pragma unroll\n      for (int e = 0; e < " << vw << "; ++e) { const float w = "
+        << src << "; qv[e] = " << conv << "; }\n";
+      b << "      *reinterpret_cast<" << ty << "*>(static_cast<" << base << "*>(" << P << ") + off) = qv;\n";
+    }
+  }
+};
+
+}  // namespace
+
+bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why) {
+  if (vm.access.size() > 8) {
+    why = "fused kernels take at most 8 loads and stores";
+    return false;
+  }
+  // values stay in registers, so no load may read what the program stored
+  std::vector<int> stored;
+  for (const VmInst& in : vm.inst) {
+    if (in.op != VmOp::Load && in.op != VmOp::Store) continue;
+    const VmAccess& acc = vm.access[in.kind];
+    if (in.dims[2] != 1 && acc.stride[2] != 1) {
+      why = "fused kernels read and write rows of contiguous elements";
+      return false;
+    }
+    if (in.op == VmOp::Store) stored.push_back(acc.arg);
+    else if (std::find(stored.begin(), stored.end(), acc.arg) != stored.end()) {
+      why = "fused kernels do not load a memref the program has stored to";
+      return false;
+    }
+  }
+  Gen g(vm, grid);
+  return g.run(out, why);
+}
+
+}  // namespace xt

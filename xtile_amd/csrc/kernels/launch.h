@@ -20,4 +20,9 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
 hipError_t launch_conv2d_general(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
 hipError_t launch_tilevm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
 
+// Fused tile programs (fused_jit.cpp): compile_fused fills fp.code from
+// fp.source with hiprtc (or the code-object cache); launch_fused runs it.
+bool compile_fused(xt::FusedPlan& fp, std::string& err);
+hipError_t launch_fused(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
+
 }  // namespace xtk

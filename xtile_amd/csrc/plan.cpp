@@ -14,6 +14,7 @@
 
 #include <map>
 #include <set>
+#include <cstdlib>
 #include <sstream>
 
 namespace xt {
@@ -730,8 +731,19 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
     }
   }
   vm.lds_floats = high;
-  if (int64_t(high) * 4 > 160 * 1024) {
-    err = "tile program needs " + std::to_string((int64_t(high) * 4 + 1023) / 1024) +
+  p.kind = PlanKind::TileVM;
+  p.vm = std::move(vm);
+  const double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
+  p.algo_bytes = blocks * bytes;
+  p.algo_flops = blocks * flops;
+  return true;
+}
+
+// The interpreter holds every live tile in LDS and takes its instruction list
+// as a kernel argument.
+bool vm_fits_interpreter(const VmPlan& vm, std::string& err) {
+  if (int64_t(vm.lds_floats) * 4 > 160 * 1024) {
+    err = "tile program needs " + std::to_string((int64_t(vm.lds_floats) * 4 + 1023) / 1024) +
           " KB of LDS for its live tiles (at most 160 KB per workgroup)";
     return false;
   }
@@ -739,11 +751,6 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
     err = "tile program too long for the HIP interpreter (at most 40 instructions and 8 loads/stores)";
     return false;
   }
-  p.kind = PlanKind::TileVM;
-  p.vm = std::move(vm);
-  const double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
-  p.algo_bytes = blocks * bytes;
-  p.algo_flops = blocks * flops;
   return true;
 }
 
@@ -783,8 +790,12 @@ std::string Plan::describe() const {
       }
       os << "tile_vm f32 insts=" << vm.inst.size() << " loads=" << loads << " stores=" << stores
          << " lds=" << vm.lds_floats * 4 << "B";
+      if (!unfused.empty()) os << " (not fused: " << unfused << ")";
       break;
     }
+    case PlanKind::Fused:
+      os << fused->layout << " insts=" << vm.inst.size();
+      break;
     case PlanKind::Conv2d:
       os << "conv2d_nhwc " << elem_name(conv.elem) << "->" << elem_name(conv.out_elem) << " tile=" << conv.TB
          << "x" << conv.TH << "x" << conv.TW << "x" << conv.TC << " filter=" << conv.KH << "x" << conv.KW << "x"
@@ -842,7 +853,20 @@ bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& 
     if (match(an, p, why)) return true;
     if (first.empty()) first = why;
   }
-  if (match_vm(an, p, err)) return true;
+  if (match_vm(an, p, err)) {
+    // compiled for itself when it fits the fused layout (XTILE_AMD_FUSE=0 keeps the interpreter)
+    const char* env = std::getenv("XTILE_AMD_FUSE");
+    FusedPlan fp;
+    std::string why;
+    if (!(env && std::string(env) == "0") && fuse_vm(p.vm, p.grid, fp, why)) {
+      p.kind = PlanKind::Fused;
+      p.fused = std::make_shared<FusedPlan>(std::move(fp));
+      return true;
+    }
+    p.unfused = env && std::string(env) == "0" ? "XTILE_AMD_FUSE=0" : why;
+    if (vm_fits_interpreter(p.vm, err)) return true;
+    err += " (not fused: " + p.unfused + ")";
+  }
   if (!first.empty()) {
     err = first + (err.empty() ? "" : "; the tile interpreter declines it too: " + err);
     return false;

@@ -12,6 +12,7 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -40,7 +41,7 @@ struct Coord {
   int64_t value = 0;
 };
 
-enum class PlanKind { EwBinary, RowSoftmax, Gemm, Conv2d, TileVM };
+enum class PlanKind { EwBinary, RowSoftmax, Gemm, Conv2d, TileVM, Fused };
 enum class EwOp { Add = 0, Sub = 1, Mul = 2 };
 
 struct ConvPlan {
@@ -91,6 +92,18 @@ struct VmPlan {
   int lds_floats = 0;             // LDS slots, in floats
 };
 
+// A tile program compiled for itself (fused.cpp): the tile interpreter's
+// lowering (VmPlan) turned into the source of one HIP kernel with every value
+// in registers, compiled at run time by hiprtc.  The kernel `xt_fused` takes
+// one argument: the memref pointers of the VmPlan's accesses, in order.
+struct FusedPlan {
+  std::string source;
+  int threads = 0;
+  int vw = 1;                // vector width of the row accesses (elements)
+  std::string layout;        // for describe()
+  std::string code;          // the gfx950 code object (filled by the runtime's compile)
+};
+
 struct Plan {
   PlanKind kind = PlanKind::EwBinary;
   std::string func;
@@ -106,10 +119,18 @@ struct Plan {
   Access2D scale, bias;
   ConvPlan conv;
   VmPlan vm;
+  std::shared_ptr<FusedPlan> fused;  // Fused: the generated kernel (vm keeps the accesses)
+  std::string unfused;               // TileVM: why the program is not fused
   double algo_bytes = 0;  // algorithmic HBM bytes per launch
   double algo_flops = 0;  // algorithmic FLOPs per launch
   std::string describe() const;
 };
+
+// The fused kernel for a tile-interpreter plan, when every value is the
+// program's main [R, C] tile or a [1, C] / [R, 1] / [1, 1] broadcast of it and
+// the ops are loads, stores, unary, binary and reductions (fused.cpp).
+// Returns false, with `why` set, when the program does not fit.
+bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why);
 
 // Builds the plan of function `func` (empty name: the only function).
 // Returns false and sets `error` when the program is not one the HIP

@@ -50,6 +50,8 @@ int get_plan(xt_module* m, const std::string& func, xt::Plan& out, char** err) {
   xt::Plan p;
   std::string why;
   if (!xt::build_plan(*m->ir, func, p, why)) return fail(err, XT_ERR_UNSUPPORTED, why);
+  if (p.kind == xt::PlanKind::Fused && !xtk::compile_fused(*p.fused, why))
+    return fail(err, XT_ERR_UNSUPPORTED, "@" + p.func + ": " + why);
   m->plans.emplace(func, p);
   out = p;
   return XT_OK;
@@ -197,6 +199,7 @@ int xt_gpu_run(xt_module* m, const char* func, void* const* bufs, const size_t* 
     case xt::PlanKind::Gemm: e = xtk::launch_gemm(p, bufs, s, why); break;
     case xt::PlanKind::Conv2d: e = xtk::launch_conv2d(p, bufs, s, why); break;
     case xt::PlanKind::TileVM: e = xtk::launch_tilevm(p, bufs, s, why); break;
+    case xt::PlanKind::Fused: e = xtk::launch_fused(p, bufs, s, why); break;
   }
   if (!why.empty()) return fail(err, XT_ERR_ARGUMENT, why);
   if (e != hipSuccess)
