@@ -1,11 +1,12 @@
 """Benchmark of the xtile_amd HIP path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c6]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c7]
 
 One step = one launch of the tile program over one batch of synthetic input
 (numpy PCG64, seed = config index, shapes of BASELINE.json's configs).  The
 headline line is C2 (row softmax fp32 8192x4096);
-all five configurations are measured and reported under "per_config".
+the six BASELINE.json configurations (C1-C6) and C7, a row layernorm run as a
+fused tile program, are measured and reported under "per_config".
 
 Timing: W untimed warm-up launches, then K launches captured in a HIP graph and
 replayed once between two HIP events on the replay stream, with device
@@ -75,6 +76,21 @@ def make_config(name: str):
             "bound": "hbm",
             "dtype": "f32",
             "data": "synthetic: numpy PCG64 seed=2, normal(0,2)",
+        }
+    if name == "c7":
+        rng = np.random.default_rng(7)
+        x = _f32(rng.normal(0.0, 1.5, (8192, 4096)))
+        g = _f32(rng.normal(1.0, 0.2, (1, 4096)))
+        b = _f32(rng.normal(0.0, 0.2, (1, 4096)))
+        n = np.full((1, 1), 1.0 / 4096, np.float32)
+        e = np.full((1, 1), 1e-5, np.float32)
+        return K.layernorm(8192, 4096, 1), [x, g, b, n, e, np.zeros_like(x)], ["f32"] * 6, {
+            "workload": "c7_layernorm: row layernorm fp32 8192x4096 (a program outside the four benchmark "
+                        "families, run as a fused tile program), one 1x4096 row per Block, grid (8192,1,1)",
+            "unit": "GB/s",
+            "bound": "hbm",
+            "dtype": "f32",
+            "data": "synthetic: numpy PCG64 seed=7, x normal(0,1.5), gamma normal(1,0.2), beta normal(0,0.2)",
         }
     if name == "c3":
         rng = np.random.default_rng(3)
@@ -350,7 +366,7 @@ def main(argv=None) -> int:
     # clock's ramp
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", default="all", help="all, or one of c1..c6")
+    ap.add_argument("--config", default="all", help="all, or one of c1..c7")
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument(
@@ -380,7 +396,7 @@ def main(argv=None) -> int:
             file=sys.stderr,
         )
         return 2
-    names = ["c1", "c2", "c3", "c4", "c5", "c6"] if args.config == "all" else [args.config]
+    names = ["c1", "c2", "c3", "c4", "c5", "c6", "c7"] if args.config == "all" else [args.config]
     headline = "c2" if "c2" in names else names[0]
     results = {n: measure(n, args.steps, args.warmup, args.cpu_seconds, not args.no_graph) for n in names}
     h = results[headline]

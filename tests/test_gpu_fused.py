@@ -3,8 +3,10 @@
 Programs of loads, stores, unary / binary ops and reductions over one [R, C]
 tile and its [1, C] / [R, 1] / [1, 1] broadcasts are compiled into one kernel
 that keeps values in registers.  These tests cover the layouts the generator
-picks: a row spread over four waves (cross-wave row reduction through LDS),
-several rows per thread, a column reduction over 32 threads of a column,
+picks: a row spread over four or eight waves (cross-wave row reduction
+through LDS),
+several rows per thread, a column reduction over 64 or 256 threads of a
+column,
 [R, 1] and [1, 1] stores, a buffer not aligned to the row vectors (which runs on
 the interpreter instead), and agreement with the interpreter (XTILE_AMD_FUSE=0).
 
@@ -37,10 +39,12 @@ def _ln_inputs(rows, cols, seed):
 @pytest.mark.parametrize(
     "rows,cols,trow,layout",
     [
-        (256, 4096, 1, "tile=1x4096 threads=1x256"),   # a row over 4 waves
-        (256, 4096, 4, "tile=4x4096 threads=1x256"),   # 4 rows per thread, 64 values each
-        (512, 1024, 2, "tile=2x1024 threads=1x256"),
+        (256, 4096, 1, "tile=1x4096 threads=1x512"),   # a row over 8 waves
+        (256, 4096, 4, "tile=4x4096 threads=1x512"),   # 4 rows per thread, 32 values each
+        (512, 1024, 2, "tile=2x1024 threads=2x256"),   # two rows, each over 4 waves
         (96, 48, 16, "tile=16x48 threads=16x4"),       # 48 columns: 12 vectors, 4 threads a row
+        # more Blocks than the chip holds: 2048 workgroups walk 8192 Blocks with gamma / beta in registers
+        (8192, 1024, 1, "tile=1x1024 threads=1x256 vw=4 workgroups=2048"),
     ],
 )
 def test_fused_layernorm(cuda, rows, cols, trow, layout):
@@ -105,6 +109,36 @@ def test_fused_row_column_and_scalar_stores(cuda):
     # i8 of x - rowsum: one rounding of a difference whose rowsum may differ in the last bits
     d = np.abs(got[4].astype(np.int32) - want[4].astype(np.int32))
     assert d.max() <= 1
+
+
+_CENTER = """
+func.func @center(%x: memref<8192x4096xf32>, %b: memref<1x4096xf32>, %y: memref<8192x4096xf32>) attributes {xt.grid = array<i32: 8192, 1, 1>} {
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %z = arith.constant 0 : i32
+  %0 = xt.load(%x, %bid#0, %z) : (memref<8192x4096xf32>, i32, i32) -> tensor<1x4096xf32>
+  %1 = xt.load(%b, %z, %z) {shared = 1 : i64} : (memref<1x4096xf32>, i32, i32) -> tensor<1x4096xf32>
+  %2 = xt.reduce_max(%0) {axis = 1 : i64} : tensor<1x4096xf32> -> tensor<1x1xf32>
+  %3 = xt.sub(%0, %2) : tensor<1x4096xf32>, tensor<1x1xf32> -> tensor<1x4096xf32>
+  %4 = xt.add(%3, %1) : tensor<1x4096xf32>, tensor<1x4096xf32> -> tensor<1x4096xf32>
+  xt.store(%4, %y, %bid#0, %z) : (tensor<1x4096xf32>, memref<8192x4096xf32>, i32, i32) -> ()
+  func.return
+}
+"""
+
+
+def test_fused_block_loop_with_one_lds_reduction_is_bit_exact(cuda):
+    """x - rowmax(x) + b over 8192 rows: 1024 workgroups walk the Blocks with
+    b in registers, and the one LDS reduction region is reused Block after
+    Block (a barrier closes each Block).  max, sub and add are exact in any
+    order, so the result is bit-exact."""
+    m = xt.parse(_CENTER)
+    assert xt.plan(m)["kernel"].startswith("fused f32 tile=1x4096 threads=1x512 vw=4 workgroups=1024")
+    rng = np.random.default_rng(47)
+    x = rng.normal(0, 1, (8192, 4096)).astype(np.float32)
+    b = rng.normal(0, 1, (1, 4096)).astype(np.float32)
+    got = run_gpu(m, [x, b, np.zeros_like(x)], ["f32"] * 3, cuda, case="fused center 8192x4096")[2]
+    want = (x - x.max(axis=1, keepdims=True)) + b
+    assert np.array_equal(got, want)
 
 
 def test_fused_matches_the_interpreter_bit_exact_without_reductions(cuda, monkeypatch):

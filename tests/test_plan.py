@@ -88,12 +88,12 @@ def test_general_programs_plan_onto_the_tile_interpreter(name, kernel):
 
 
 def test_interpreter_programs_and_lds_budget(monkeypatch):
-    assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith("fused f32 tile=64x64 threads=16x16 vw=4 insts=17")
-    assert xt.plan(K.layernorm(8192, 4096, 1))["kernel"].startswith("fused f32 tile=1x4096 threads=1x256 vw=4")
+    assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith("fused f32 tile=64x64 threads=32x16 vw=4 insts=17")
+    assert xt.plan(K.layernorm(8192, 4096, 1))["kernel"].startswith("fused f32 tile=1x4096 threads=1x512 vw=4")
     # fused kernels hold values in registers, so the interpreter's LDS budget does not bind them
-    assert xt.plan(K.layernorm(8192, 4096, 4))["kernel"].startswith("fused f32 tile=4x4096 threads=1x256 vw=4")
-    assert xt.plan(K.column_softmax(64, 128, 32))["kernel"].startswith("fused f32 tile=64x32 threads=32x8")
-    assert xt.plan(K.bias_add(128, 256))["kernel"].startswith("fused f32 tile=32x64 threads=16x16")
+    assert xt.plan(K.layernorm(8192, 4096, 4))["kernel"].startswith("fused f32 tile=4x4096 threads=1x512 vw=4")
+    assert xt.plan(K.column_softmax(64, 128, 32))["kernel"].startswith("fused f32 tile=64x32 threads=64x8")
+    assert xt.plan(K.bias_add(128, 256))["kernel"].startswith("fused f32 tile=32x64 threads=32x16")
     monkeypatch.setenv("XTILE_AMD_FUSE", "0")
     assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith(
         "tile_vm f32 insts=17 loads=5 stores=1 lds=50208B (not fused: XTILE_AMD_FUSE=0)")

@@ -19,6 +19,7 @@
 // shuffles (and LDS when a row spans waves), or across the TR threads of a
 // column through LDS.
 #include <algorithm>
+#include <cstdlib>
 #include <map>
 #include <sstream>
 
@@ -107,23 +108,46 @@ class Gen {
 
   bool run(FusedPlan& out, std::string& why) {
     if (!shapes(why) || !layout(why)) return false;
+    // Block-invariant loads (weights, scalars) are read once per workgroup when
+    // workgroups outnumber what the chip holds: each workgroup then walks a
+    // grid-stride list of Blocks with those values kept in registers.
+    const long long blocks = (long long)grid_[0] * grid_[1] * grid_[2];
+    const long long resident = 256LL * std::max(1, std::min(32, 2048 / L.threads()));
+    bool invariant = false;
+    for (const VmInst& in : vm_.inst) invariant |= in.op == VmOp::Load && !streamed(in.kind);
+    hoist_ = invariant && blocks > 2 * resident;
+    const long long wgs = hoist_ ? resident : blocks;
+    pre_.str("");
+    body_.str("");
+    for (size_t i = 0; i < vm_.inst.size(); ++i)
+      if (!emit(static_cast<int>(i), why)) return false;
+    if (red_floats_ * 4 > 64 * 1024) {
+      why = "fused kernel reductions need more than 64 KB of LDS";
+      return false;
+    }
     std::ostringstream k;
     k << "extern \"C\" __global__ void __launch_bounds__(" << L.threads() << ") xt_fused(FusedArgs a) {\n"
       << "#pragma clang fp contract(off)\n"
       << "  const int t = threadIdx.x, tc = t % " << L.TC << ", tr = t / " << L.TC << ";\n"
-      << "  const int bid = blockIdx.x, x = bid % " << grid_[0] << ", y = (bid / " << grid_[0] << ") % " << grid_[1]
-      << ", z = bid / " << (long long)grid_[0] * grid_[1] << ";\n"
-      << "  (void)x; (void)y; (void)z; (void)tr; (void)tc;\n";
-    body_.str("");
-    for (size_t i = 0; i < vm_.inst.size(); ++i)
-      if (!emit(static_cast<int>(i), why)) return false;
+      << "  (void)tr; (void)tc;\n";
     if (red_floats_ > 0) k << "  __shared__ float red[" << red_floats_ << "];\n";
-    k << body_.str() << "}\n";
+    k << pre_.str();
+    if (hoist_) k << "  for (int bid = blockIdx.x; bid < " << blocks << "; bid += " << wgs << ") {\n";
+    else k << "  {\n    const int bid = blockIdx.x;\n";
+    k << "  const int x = bid % " << grid_[0] << ", y = (bid / " << grid_[0] << ") % " << grid_[1]
+      << ", z = bid / " << (long long)grid_[0] * grid_[1] << ";\n"
+      << "  (void)x; (void)y; (void)z;\n";
+    k << body_.str();
+    // with one LDS region, the next Block's write to it waits for this Block's reads
+    if (hoist_ && n_red_ == 1) k << "  __syncthreads();\n";
+    k << "  }\n}\n";
     out.source = std::string(kPreamble) + k.str();
     out.threads = L.threads();
     out.vw = L.VW;
+    out.workgroups = static_cast<int>(wgs);
     std::ostringstream lay;
     lay << "fused f32 tile=" << L.R << "x" << L.C << " threads=" << L.TR << "x" << L.TC << " vw=" << L.VW;
+    if (hoist_) lay << " workgroups=" << wgs;
     out.layout = lay.str();
     return true;
   }
@@ -133,8 +157,10 @@ class Gen {
   int grid_[3];
   Layout L;
   std::map<int, std::pair<int, VKind>> slot_;  // LDS slot -> (value id, kind)
-  std::ostringstream body_;
+  std::ostringstream pre_, body_;  // hoisted Block-invariant loads; the per-Block body
+  bool hoist_ = false;
   int red_floats_ = 0;
+  int n_red_ = 0;                   // reductions that go through LDS
 
   static void dims2(const int d[3], int& a, int& b) {
     a = d[1];
@@ -192,8 +218,10 @@ class Gen {
     }
     L.VW = vw;
     const int cv = L.C / L.VW;
-    L.TC = pow2_divisor(cv, 256);
-    L.TR = pow2_divisor(L.R, 256 / L.TC);
+    const char* cap_env = std::getenv("XT_FUSED_CAP");
+    const int cap = cap_env ? std::atoi(cap_env) : 512;
+    L.TC = pow2_divisor(cv, cap);
+    L.TR = pow2_divisor(L.R, cap / L.TC);
     L.SR = L.R / L.TR;
     L.SC = cv / L.TC;
     if (L.SR * L.cols() > 64) {
@@ -214,8 +242,11 @@ class Gen {
 
   std::string origin(const TileAddr& o) const {
     std::ostringstream s;
-    s << "(" << o.c0 << "LL + (long long)x * " << o.sx << "LL + (long long)y * " << o.sy << "LL + (long long)z * "
-      << o.sz << "LL)";
+    s << "(" << o.c0 << "LL";
+    if (o.sx) s << " + (long long)x * " << o.sx << "LL";
+    if (o.sy) s << " + (long long)y * " << o.sy << "LL";
+    if (o.sz) s << " + (long long)z * " << o.sz << "LL";
+    s << ")";
     return s.str();
   }
 
@@ -229,7 +260,7 @@ class Gen {
 
   bool emit(int i, std::string& why) {
     const VmInst& in = vm_.inst[i];
-    std::ostringstream& b = body_;
+    std::ostringstream& b = in.op == VmOp::Load && hoist_ && !streamed(in.kind) ? pre_ : body_;
     const std::string v = "v" + std::to_string(i);
     switch (in.op) {
       case VmOp::Load: {
@@ -328,16 +359,18 @@ class Gen {
             << comb("m", "__shfl_xor(m, o, 64)") << ";\n";
           b << "    " << v << "[sr] = m;\n  }\n";
           if (L.TC > 64) {  // the row spans TC / 64 waves: combine through LDS
+            // each reduction has LDS of its own, so one barrier orders its writes before its reads
             const int W = L.TC / 64;
-            red_floats_ = std::max(red_floats_, nr * L.TR * W);
+            const std::string base = std::to_string(red_floats_) + " + ";
+            red_floats_ += nr * L.TR * W;
+            ++n_red_;
+            b << "  if ((tc & 63) == 0) {\n#pragma unroll\n    for (int sr = 0; sr < " << nr << "; ++sr) red[" << base
+              << "(sr * " << L.TR << " + tr) * " << W << " + (tc >> 6)] = " << v << "[sr];\n  }\n";
             b << "  __syncthreads();\n";
-            b << "  if ((tc & 63) == 0) {\n#pragma unroll\n    for (int sr = 0; sr < " << nr
-              << "; ++sr) red[(sr * " << L.TR << " + tr) * " << W << " + (tc >> 6)] = " << v << "[sr];\n  }\n";
-            b << "  __syncthreads();\n";
-            b << "#pragma unroll\n  for (int sr = 0; sr < " << nr << "; ++sr) {\n    float m = red[(sr * " << L.TR
-              << " + tr) * " << W << "];\n";
+            b << "#pragma unroll\n  for (int sr = 0; sr < " << nr << "; ++sr) {\n    float m = red[" << base
+              << "(sr * " << L.TR << " + tr) * " << W << "];\n";
             b << "#pragma unroll\n    for (int q = 1; q < " << W << "; ++q) m = "
-              << comb("m", "red[(sr * " + std::to_string(L.TR) + " + tr) * " + std::to_string(W) + " + q]")
+              << comb("m", "red[" + base + "(sr * " + std::to_string(L.TR) + " + tr) * " + std::to_string(W) + " + q]")
               << ";\n    " << v << "[sr] = m;\n  }\n";
           }
           slot_[in.dst] = {i, ko};
@@ -351,15 +384,16 @@ class Gen {
         b << "#pragma unroll\n    for (int sr = 0; sr < " << L.SR << "; ++sr) m = "
           << comb("m", s + "[" + idx(ks, "sr", "j") + "]") << ";\n    " << v << "[j] = m;\n  }\n";
         if (L.TR > 1) {
-          red_floats_ = std::max(red_floats_, L.threads() * nc);
+          const std::string base = std::to_string(red_floats_) + " + ";
+          red_floats_ += L.threads() * nc;
+          ++n_red_;
+          b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) red[" << base << "t * " << nc
+            << " + j] = " << v << "[j];\n";
           b << "  __syncthreads();\n";
-          b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) red[t * " << nc << " + j] = " << v
-            << "[j];\n";
-          b << "  __syncthreads();\n";
-          b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) {\n    float m = red[tc * " << nc
-            << " + j];\n";
+          b << "#pragma unroll\n  for (int j = 0; j < " << nc << "; ++j) {\n    float m = red[" << base << "tc * "
+            << nc << " + j];\n";
           b << "#pragma unroll\n    for (int q = 1; q < " << L.TR << "; ++q) m = "
-            << comb("m", "red[(q * " + std::to_string(L.TC) + " + tc) * " + std::to_string(nc) + " + j]")
+            << comb("m", "red[" + base + "(q * " + std::to_string(L.TC) + " + tc) * " + std::to_string(nc) + " + j]")
             << ";\n    " << v << "[j] = m;\n  }\n";
         }
         slot_[in.dst] = {i, ko};
@@ -376,8 +410,16 @@ class Gen {
   }
 
   // vw consecutive elements at `off` -> dst (an expression in e = 0..vw-1)
+  // Tiles that move with the block id stream through once: nontemporal loads
+  // and stores keep them from displacing what every Block reads (weights).
+  bool streamed(int acc) const {
+    const TileAddr& o = vm_.access[acc].addr;
+    return o.sx != 0 || o.sy != 0 || o.sz != 0;
+  }
+
   void load_code(std::ostringstream& b, int acc, Elem e, int vw, const std::string& dst) const {
     const std::string P = "a.p[" + std::to_string(acc) + "]";
+    const bool stream = streamed(acc);
     std::string ty, conv;
     switch (e) {
       case Elem::F32: ty = vw == 4 ? "xf4" : vw == 2 ? "xf2" : "float"; conv = "q"; break;
@@ -387,8 +429,8 @@ class Gen {
     }
     const char* base = e == Elem::F32 ? "float" : e == Elem::F16 ? "_Float16" : e == Elem::BF16 ? "unsigned short"
                                                                                                  : "signed char";
-    b << "      const " << ty << " qv = *reinterpret_cast<const " << ty << "*>(static_cast<const " << base
-      << "*>(" << P << ") + off);\n";
+    b << "      const " << ty << " qv = " << (stream ? "__builtin_nontemporal_load(" : "*(") << "reinterpret_cast<const "
+      << ty << "*>(static_cast<const " << base << "*>(" << P << ") + off));\n";
     if (vw == 1) {
       b << "      { const int e = 0; const auto q = qv; " << dst << " = " << conv << "; }\n";
     } else {
@@ -399,6 +441,7 @@ class Gen {
 
   void store_code(std::ostringstream& b, int acc, Elem e, int vw, const std::string& src) const {
     const std::string P = "a.p[" + std::to_string(acc) + "]";
+    const bool stream = streamed(acc);
     std::string ty, conv;
     switch (e) {
       case Elem::F32: ty = vw == 4 ? "xf4" : vw == 2 ? "xf2" : "float"; conv = "w"; break;
@@ -414,7 +457,11 @@ class Gen {
     } else {
       b << "      " << ty << " qv;\n#pragma unroll\n      for (int e = 0; e < " << vw << "; ++e) { const float w = "
         << src << "; qv[e] = " << conv << "; }\n";
-      b << "      *reinterpret_cast<" << ty << "*>(static_cast<" << base << "*>(" << P << ") + off) = qv;\n";
+      if (stream)
+        b << "      __builtin_nontemporal_store(qv, reinterpret_cast<" << ty << "*>(static_cast<" << base << "*>(" << P
+          << ") + off));\n";
+      else
+        b << "      *reinterpret_cast<" << ty << "*>(static_cast<" << base << "*>(" << P << ") + off) = qv;\n";
     }
   }
 };

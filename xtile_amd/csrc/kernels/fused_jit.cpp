@@ -3,10 +3,10 @@
 // hiprtc compiles a program's kernel for gfx950 when its plan is built (no GPU
 // is needed for that), with the flags of every other kernel of the library.
 // Code objects are kept in memory by source, and on disk under `jit/` beside
-// the library (XTILE_AMD_JIT_CACHE names another directory, "off" turns the
-// disk cache off), so a program is compiled once per machine.  A launch loads
-// the code object once per device (hipModuleLoadData) and enqueues `xt_fused`
-// on the caller's stream.
+// the library with their source (XTILE_AMD_JIT_CACHE names another directory,
+// "off" turns the disk cache off), so a program is compiled once per machine.
+// A launch loads the code object once per device (hipModuleLoadData) and
+// enqueues `xt_fused` on the caller's stream.
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
@@ -31,7 +31,7 @@ const char* kOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang
 
 std::mutex g_mu;
 std::map<std::string, std::string> g_code;                          // source -> code object
-std::map<std::pair<std::string, int>, hipFunction_t> g_func;        // (source, device) -> kernel
+std::map<std::pair<uint64_t, int>, hipFunction_t> g_func;           // (source hash, device) -> kernel
 
 uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
   for (unsigned char c : s) h = (h ^ c) * 1099511628211ull;
@@ -49,8 +49,6 @@ std::string cache_dir() {
 }
 
 std::string cache_key(const std::string& src) {
-  int ver = 0;
-  hiprtcVersion(&ver, &ver);
   std::string all = src;
   for (const char* o : kOptions) all += std::string("\n//") + o;
   char buf[40];
@@ -110,6 +108,7 @@ bool rtc(const std::string& src, std::string& code, std::string& err) {
 
 bool compile_fused(xt::FusedPlan& fp, std::string& err) {
   std::lock_guard<std::mutex> lock(g_mu);
+  fp.id = fnv1a(fp.source);
   auto it = g_code.find(fp.source);
   if (it != g_code.end()) {
     fp.code = it->second;
@@ -120,6 +119,7 @@ bool compile_fused(xt::FusedPlan& fp, std::string& err) {
   if (dir.empty() || !read_file(dir + "/" + key + ".co", code)) {
     if (!rtc(fp.source, code, err)) return false;
     write_file(dir, key + ".co", code);
+    write_file(dir, key + ".hip", fp.source);  // the source beside its code object, for reading
   }
   g_code.emplace(fp.source, code);
   fp.code = std::move(code);
@@ -153,7 +153,7 @@ hipError_t launch_fused(const xt::Plan& p, void* const* bufs, hipStream_t s, std
   hipFunction_t fn = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_mu);
-    auto key = std::make_pair(fp->source, dev);
+    auto key = std::make_pair(fp->id, dev);
     auto it = g_func.find(key);
     if (it == g_func.end()) {
       hipModule_t mod = nullptr;
@@ -171,7 +171,11 @@ hipError_t launch_fused(const xt::Plan& p, void* const* bufs, hipStream_t s, std
   } args = {};
   for (size_t k = 0; k < vm.access.size(); ++k) args.p[k] = bufs[vm.access[k].arg];
   void* params[] = {&args};
-  return hipModuleLaunchKernel(fn, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(fp->threads), 1, 1, 0,
+  if (fp->workgroups < 1 || fp->workgroups > blocks) {
+    why = "fused kernel launch size out of range";
+    return hipErrorInvalidValue;
+  }
+  return hipModuleLaunchKernel(fn, static_cast<unsigned>(fp->workgroups), 1, 1, static_cast<unsigned>(fp->threads), 1, 1, 0,
                                s, params, nullptr);
 }
 

@@ -601,7 +601,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       small_int.insert(o->results[0]);
   }
   VmPlan vm;
-  double bytes = 0, flops = 0;
+  double bytes = 0, once_bytes = 0, flops = 0;
   for (int i = 0; i < nops; ++i) {
     const Op* o = an.compute[i];
     const std::string& n = o->name;
@@ -631,7 +631,10 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       in.op = is_load ? VmOp::Load : VmOp::Store;
       in.kind = static_cast<int16_t>(vm.access.size());
       vm.access.push_back(acc);
-      bytes += double(ten.numel()) * elem_bytes(mem.elem);
+      // a tile at the same place in every Block (weights, scalars) moves from HBM once
+      const double tb = double(ten.numel()) * elem_bytes(mem.elem);
+      if (acc.addr.sx == 0 && acc.addr.sy == 0 && acc.addr.sz == 0) once_bytes += tb;
+      else bytes += tb;
       if (is_load) {
         auto sl = alloc(static_cast<int>(ten.numel()));
         slot[o->results[0]] = sl;
@@ -734,7 +737,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
   p.kind = PlanKind::TileVM;
   p.vm = std::move(vm);
   const double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
-  p.algo_bytes = blocks * bytes;
+  p.algo_bytes = blocks * bytes + once_bytes;
   p.algo_flops = blocks * flops;
   return true;
 }

@@ -100,8 +100,10 @@ struct FusedPlan {
   std::string source;
   int threads = 0;
   int vw = 1;                // vector width of the row accesses (elements)
+  int workgroups = 0;        // launch size: one per Block, or fewer walking the Blocks
   std::string layout;        // for describe()
   std::string code;          // the gfx950 code object (filled by the runtime's compile)
+  uint64_t id = 0;           // hash of `source` (filled with `code`), keys the loaded kernels
 };
 
 struct Plan {
