@@ -80,7 +80,9 @@ int xt_func_signature(xt_module* m, const char* func, char** out_json, char** er
  * ("gemm f16->f32 tile=128x128 k=4096 grid=(32,32,1)"), and the algorithmic
  * bytes and FLOPs of one launch.  Stands in for the reference's lowering
  * pipeline `compile` (xtile/__init__.py:160-168), whose x1 command stream the
- * GPU backend replaces with a kernel launch. */
+ * GPU backend replaces with a kernel launch.  A program planned as a fused
+ * kernel is compiled here (hiprtc, no GPU needed; cached per process and on
+ * disk), so a first call may take a fraction of a second. */
 int xt_plan(xt_module* m, const char* func, char** out_desc, double* algo_bytes,
             double* algo_flops, char** err);
 

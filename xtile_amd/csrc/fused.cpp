@@ -115,7 +115,7 @@ class Gen {
     const long long resident = 256LL * std::max(1, std::min(32, 2048 / L.threads()));
     bool invariant = false;
     for (const VmInst& in : vm_.inst) invariant |= in.op == VmOp::Load && !streamed(in.kind);
-    hoist_ = invariant && blocks > 2 * resident;
+    hoist_ = invariant && blocks > 2 * resident && blocks < (1LL << 30);
     const long long wgs = hoist_ ? resident : blocks;
     pre_.str("");
     body_.str("");
