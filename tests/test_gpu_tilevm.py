@@ -248,10 +248,14 @@ def _as_f32(x, et):
     return bf16_bits_to_f32(x) if et == "bf16" else x.astype(np.float32)
 
 
+@pytest.mark.parametrize("fuse", ["1", "0"])
 @pytest.mark.parametrize("et", ["f16", "bf16", "i8"])
-def test_narrow_loads_and_stores_round_like_the_oracle(cuda, et):
+def test_narrow_loads_and_stores_round_like_the_oracle(cuda, et, fuse, monkeypatch):
+    """On the fused kernel and (XTILE_AMD_FUSE=0) on the interpreter."""
+    monkeypatch.setenv("XTILE_AMD_FUSE", fuse)
     rng = np.random.default_rng(31)
     m = xt.parse(_NARROW.replace("xT", "x" + et))
+    assert xt.plan(m)["kernel"].startswith("fused" if fuse == "1" else "tile_vm")
     if et == "f16":
         a, b = _f16_edges(rng)
     elif et == "bf16":
@@ -280,8 +284,11 @@ def test_narrow_loads_and_stores_round_like_the_oracle(cuda, et):
         assert list(w[1, :4]) == [1.0, 1.0 + 2.0**-10, 2048, 2052]
 
 
-def test_two_sided_broadcast(cuda):
-    """(8, 1) - (1, 16) -> (8, 16) and a rank-1 operand (lib/xt/XTOps.cpp:104-145)."""
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_two_sided_broadcast(cuda, fuse, monkeypatch):
+    """(8, 1) - (1, 16) -> (8, 16) and a rank-1 operand (lib/xt/XTOps.cpp:104-145),
+    on the fused kernel and on the interpreter."""
+    monkeypatch.setenv("XTILE_AMD_FUSE", fuse)
     text = """
 func.func @bc(%a: memref<8x1xf32>, %b: memref<1x16xf32>, %v: memref<16xf32>, %c: memref<8x16xf32>) attributes {xt.grid = array<i32: 1, 1, 1>} {
   %z = arith.constant 0 : i32
@@ -294,6 +301,7 @@ func.func @bc(%a: memref<8x1xf32>, %b: memref<1x16xf32>, %v: memref<16xf32>, %c:
   func.return
 }"""
     m = xt.parse(text)
+    assert xt.plan(m)["kernel"].startswith("fused" if fuse == "1" else "tile_vm")
     rng = np.random.default_rng(32)
     a = rng.normal(0, 1, (8, 1)).astype(np.float32)
     b = rng.normal(0, 1, (1, 16)).astype(np.float32)

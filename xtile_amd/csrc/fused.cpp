@@ -19,7 +19,6 @@
 // shuffles (and LDS when a row spans waves), or across the TR threads of a
 // column through LDS.
 #include <algorithm>
-#include <cstdlib>
 #include <map>
 #include <sstream>
 
@@ -218,10 +217,9 @@ class Gen {
     }
     L.VW = vw;
     const int cv = L.C / L.VW;
-    const char* cap_env = std::getenv("XT_FUSED_CAP");
-    const int cap = cap_env ? std::atoi(cap_env) : 512;
-    L.TC = pow2_divisor(cv, cap);
-    L.TR = pow2_divisor(L.R, cap / L.TC);
+    // up to 512 threads (8 waves) a workgroup: 4096-float rows at two float4 a thread
+    L.TC = pow2_divisor(cv, 512);
+    L.TR = pow2_divisor(L.R, 512 / L.TC);
     L.SR = L.R / L.TR;
     L.SC = cv / L.TC;
     if (L.SR * L.cols() > 64) {

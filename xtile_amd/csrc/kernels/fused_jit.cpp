@@ -19,7 +19,6 @@
 #include <map>
 #include <mutex>
 #include <sstream>
-#include <vector>
 
 #include "launch.h"
 
