@@ -141,3 +141,93 @@ def program(seed: int):
         if k > 0 and k != len(dtypes) - 1 and host[k].shape == (rows, C) and d == ea and d != "f32":
             host[k] = np.zeros_like(host[k])
     return text, host, dtypes, len(dtypes) - 1
+
+
+# (R, C) tiles of the fused kernel's layouts: rows across up to 8 waves, several
+# rows per thread, tall tiles whose column reductions span many threads
+_FUSED_TILES = [(1, 4096), (2, 2048), (4, 1024), (8, 512), (16, 256), (64, 64), (128, 32), (256, 8), (3, 20), (6, 12)]
+
+
+def fused_program(seed: int):
+    """A random program over one [R, C] tile and its broadcasts, the form the
+    fused kernel takes: a loaded tile (any element type), a shared [1, C]
+    weight and [1, 1] scalar, a per-Block [R, 1] operand, bounded unary ops,
+    keep-dim reductions broadcast back, and stores of the f32 result and of a
+    reduction.  Grids up to 6000 Blocks, so that workgroups walk several Blocks
+    with the shared tiles in registers.  Returns (text, host arrays, dtypes,
+    indices of the f32 outputs)."""
+    rng = np.random.default_rng(10_000 + seed)
+    R, C = _FUSED_TILES[int(rng.integers(0, len(_FUSED_TILES)))]
+    big = rng.random() < 0.3 and R * C <= 4096
+    grid = int(rng.integers(4097, 6001)) if big else int(rng.integers(1, 9))
+    rows = grid * R
+    ea = str(rng.choice(_ELEMS))
+    lines, args, host, dtypes, outs = [], [], [], [], []
+    n = [0]
+
+    def fresh():
+        n[0] += 1
+        return f"%v{n[0]}"
+
+    def add_arg(shape, e, out=False):
+        args.append(f"%a{len(args)}: {_m(shape, e)}")
+        host.append(np.zeros(shape, np.float32) if out else _host(rng, shape, e))
+        dtypes.append(e)
+        if out:
+            outs.append(len(args) - 1)
+        return f"%a{len(args) - 1}"
+
+    A = add_arg((rows, C), ea)
+    x = fresh()
+    lines.append(f"  {x} = xt.load({A}, %bid#0, %z) : ({_m((rows, C), ea)}, i32, i32) -> {_t((R, C), ea)}")
+    if ea == "i8":
+        y = fresh()
+        lines.append(f"  {y} = xt.itof({x}) : {_t((R, C), 'i8')} -> {_t((R, C))}")
+        x = y
+    elif ea != "f32":  # f16 / bf16 values combine with their own type; square, then restart from an f32 load
+        y = fresh()
+        lines.append(f"  {y} = xt.mul({x}, {x}) : {_t((R, C), ea)}, {_t((R, C), ea)} -> {_t((R, C), ea)}")
+        On = add_arg((rows, C), ea)
+        host[-1] = np.zeros_like(host[-1])
+        lines.append(f"  xt.store({y}, {On}, %bid#0, %z) : ({_t((R, C), ea)}, {_m((rows, C), ea)}, i32, i32) -> ()")
+        F = add_arg((rows, C), "f32")
+        x = fresh()
+        lines.append(f"  {x} = xt.load({F}, %bid#0, %z) : ({_m((rows, C))}, i32, i32) -> {_t((R, C))}")
+    W = add_arg((1, C), "f32")
+    w = fresh()
+    lines.append(f"  {w} = xt.load({W}, %z, %z) {{shared = 1 : i64}} : ({_m((1, C))}, i32, i32) -> {_t((1, C))}")
+    S = add_arg((1, 1), "f32")
+    sc = fresh()
+    lines.append(f"  {sc} = xt.load({S}, %z, %z) {{shared = 1 : i64}} : ({_m((1, 1))}, i32, i32) -> {_t((1, 1))}")
+    P = add_arg((rows, 1), "f32")
+    pr = fresh()
+    lines.append(f"  {pr} = xt.load({P}, %bid#0, %z) : ({_m((rows, 1))}, i32, i32) -> {_t((R, 1))}")
+    cur = x
+    ops = ["xt.add", "xt.sub", "xt.mul"]
+    for operand, shape in [(w, (1, C)), (sc, (1, 1)), (pr, (R, 1))]:
+        y = fresh()
+        lines.append(f"  {y} = {rng.choice(ops)}({cur}, {operand}) : {_t((R, C))}, {_t(shape)} -> {_t((R, C))}")
+        cur = y
+    y = fresh()
+    lines.append(f"  {y} = {rng.choice(_UNARY)}({cur}) : {_t((R, C))} -> {_t((R, C))}")
+    cur = y
+    red_out = None
+    for _ in range(int(rng.integers(1, 3))):
+        axis = int(rng.integers(0, 2))
+        rs = (1, C) if axis == 0 else (R, 1)
+        r = fresh()
+        lines.append(f"  {r} = {rng.choice(['xt.reduce_sum', 'xt.reduce_max'])}({cur}) {{axis = {axis} : i64}} : "
+                     f"{_t((R, C))} -> {_t(rs)}")
+        y = fresh()
+        lines.append(f"  {y} = xt.sub({cur}, {r}) : {_t((R, C))}, {_t(rs)} -> {_t((R, C))}")
+        cur = y
+        red_out = (r, rs)
+    r, rs = red_out
+    mem = (grid, C) if rs[0] == 1 else (rows, 1)
+    Rn = add_arg(mem, "f32", out=True)
+    lines.append(f"  xt.store({r}, {Rn}, %bid#0, %z) : ({_t(rs)}, {_m(mem)}, i32, i32) -> ()")
+    On = add_arg((rows, C), "f32", out=True)
+    lines.append(f"  xt.store({cur}, {On}, %bid#0, %z) : ({_t((R, C))}, {_m((rows, C))}, i32, i32) -> ()")
+    head = (f"func.func @fz{seed}({', '.join(args)}) attributes {{xt.grid = array<i32: {grid}, 1, 1>}} {{\n"
+            "  %bid:3 = xt.get_tile_block_id : i32, i32, i32\n  %z = arith.constant 0 : i32\n")
+    return head + "\n".join(lines) + "\n  func.return\n}", host, dtypes, outs

@@ -20,3 +20,11 @@ def test_random_program_plans_and_runs_in_the_oracle(seed):
     assert xt.plan(m)["kernel"]
     got = run_oracle(m, host, 1)
     assert got[out].shape == host[out].shape
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_fusable_random_program_plans_onto_a_fused_kernel(seed):
+    from tests.random_programs import fused_program
+
+    text, host, dtypes, outs = fused_program(seed)
+    assert xt.plan(xt.parse(text))["kernel"].startswith("fused f32 tile=")
