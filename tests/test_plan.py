@@ -187,3 +187,20 @@ func.func @s(%a: memref<64x64xf32>, %b: memref<64x64xf32>, %c: memref<64x64xf32>
   func.return
 }"""
     assert xt.plan(xt.parse(text))["kernel"].startswith("ew_binary")
+
+
+def test_fused_kernels_are_compiled_into_the_code_object_cache(tmp_path, monkeypatch):
+    """Planning a fused program compiles it with hiprtc (no GPU needed) and
+    writes the code object and its source under XTILE_AMD_JIT_CACHE."""
+    monkeypatch.setenv("XTILE_AMD_JIT_CACHE", str(tmp_path))
+    # a shape no other test plans, so the in-process cache does not hold it
+    assert xt.plan(K.layernorm(24, 40, 8))["kernel"].startswith("fused f32 tile=8x40 threads=8x2 vw=4")
+    cos = list(tmp_path.glob("*.co"))
+    srcs = list(tmp_path.glob("*.hip"))
+    assert len(cos) == 1 and len(srcs) == 1 and cos[0].stem == srcs[0].stem
+    assert cos[0].read_bytes()[:4] == b"\x7fELF"  # an AMDGPU code object
+    assert 'extern "C" __global__' in srcs[0].read_text() and "xt_fused" in srcs[0].read_text()
+    monkeypatch.setenv("XTILE_AMD_JIT_CACHE", "off")
+    other = tmp_path / "none"
+    xt.plan(K.layernorm(24, 80, 8))
+    assert not other.exists() and len(list(tmp_path.glob("*.co"))) == 1
