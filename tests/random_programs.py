@@ -30,8 +30,8 @@ def _m(shape, e="f32"):
 
 
 def _host(rng, shape, e):
-    if e == "i8":
-        return rng.integers(-8, 9, shape, dtype=np.int8)
+    if e == "i8":  # small integers keep exp of them (+ a uniform operand) at most e^4
+        return rng.integers(-3, 4, shape, dtype=np.int8)
     x = rng.uniform(-1, 1, shape).astype(np.float32)
     if e == "f16":
         return x.astype(np.float16)
@@ -152,7 +152,7 @@ def fused_program(seed: int):
     """A random program over one [R, C] tile and its broadcasts, the form the
     fused kernel takes: a loaded tile (any element type), a shared [1, C]
     weight and [1, 1] scalar, a per-Block [R, 1] operand, bounded unary ops,
-    keep-dim reductions broadcast back, and stores of the f32 result and of a
+    keep-dim reductions broadcast back (max subtracted, sum multiplied), and stores of the f32 result and of a
     reduction.  Grids up to 6000 Blocks, so that workgroups walk several Blocks
     with the shared tiles in registers.  Returns (text, host arrays, dtypes,
     indices of the f32 outputs)."""
@@ -216,10 +216,12 @@ def fused_program(seed: int):
         axis = int(rng.integers(0, 2))
         rs = (1, C) if axis == 0 else (R, 1)
         r = fresh()
-        lines.append(f"  {r} = {rng.choice(['xt.reduce_sum', 'xt.reduce_max'])}({cur}) {{axis = {axis} : i64}} : "
-                     f"{_t((R, C))} -> {_t(rs)}")
+        red = str(rng.choice(["xt.reduce_sum", "xt.reduce_max"]))
+        lines.append(f"  {r} = {red}({cur}) {{axis = {axis} : i64}} : {_t((R, C))} -> {_t(rs)}")
+        # a max is subtracted (exact); a sum scales (a difference from a sum of C values would cancel)
         y = fresh()
-        lines.append(f"  {y} = xt.sub({cur}, {r}) : {_t((R, C))}, {_t(rs)} -> {_t((R, C))}")
+        op = "xt.sub" if red == "xt.reduce_max" else "xt.mul"
+        lines.append(f"  {y} = {op}({cur}, {r}) : {_t((R, C))}, {_t(rs)} -> {_t((R, C))}")
         cur = y
         red_out = (r, rs)
     r, rs = red_out
