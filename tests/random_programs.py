@@ -233,3 +233,50 @@ def fused_program(seed: int):
     head = (f"func.func @fz{seed}({', '.join(args)}) attributes {{xt.grid = array<i32: {grid}, 1, 1>}} {{\n"
             "  %bid:3 = xt.get_tile_block_id : i32, i32, i32\n  %z = arith.constant 0 : i32\n")
     return head + "\n".join(lines) + "\n  func.return\n}", host, dtypes, outs
+
+
+def conv_case(seed: int):
+    """Random `load_conv2d` parameters the planner takes (any kernel): element
+    type, batch, image, channels, filter, asymmetric pads, strides, dilations,
+    and output tiles dividing the output.  Returns (module, host inputs,
+    dtypes, description); the module is built by xtile_amd.kernels.conv2d."""
+    import xtile_amd as xt
+    from xtile_amd import kernels as K
+
+    rng = np.random.default_rng(20_000 + seed)
+    dts = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}
+    for _ in range(200):
+        dt = str(rng.choice(list(dts)))
+        n = int(rng.integers(1, 3))
+        kh, kw = int(rng.choice([1, 3, 5])), int(rng.choice([1, 3, 5]))
+        sh, sw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        dh, dw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        pad = tuple(int(rng.integers(0, k // 2 + 1)) for k in (kh, kw, kh, kw))
+        h, w = int(rng.integers(6, 21)), int(rng.integers(6, 21))
+        cin = int(rng.choice([3, 8, 16, 32, 48, 64, 96, 128]))
+        cout = int(rng.choice([8, 16, 24, 32, 48, 64, 128]))
+        oh = (h + pad[0] + pad[2] - dh * (kh - 1) - 1) // sh + 1
+        ow = (w + pad[1] + pad[3] - dw * (kw - 1) - 1) // sw + 1
+        if oh < 1 or ow < 1:
+            continue
+        th = int(rng.choice([d for d in range(1, oh + 1) if oh % d == 0]))
+        tw = int(rng.choice([d for d in range(1, ow + 1) if ow % d == 0]))
+        try:
+            mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=dts[dt], pad=pad, stride=(sh, sw),
+                           dilation=(dh, dw))
+            xt.plan(mod)
+        except (ValueError, NotImplementedError):
+            continue
+        if dt == "i8":
+            x = rng.integers(-128, 128, (n, h, w, cin), dtype=np.int8)
+            f = rng.integers(-128, 128, (kh, kw, cin, cout), dtype=np.int8)
+        else:
+            x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+            f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+            x, f = (f32_to_bf16_bits(x), f32_to_bf16_bits(f)) if dt == "bf16" else (x.astype(np.float16),
+                                                                                     f.astype(np.float16))
+        o = np.zeros((n, oh, ow, cout), np.float32)
+        desc = (f"{dt} {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{sh},{sw} d{dh},{dw} pad{pad} "
+                f"tile {th}x{tw}")
+        return mod, [x, f, o], [dt, dt, "f32"], desc
+    raise RuntimeError("no plannable conv drawn")

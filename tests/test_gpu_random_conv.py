@@ -1,0 +1,30 @@
+"""GPU parity of seeded random `load_conv2d` programs (tests/random_programs.py:
+conv_case): i8 / f16 / bf16, 1x1 to 5x5 filters, strides and dilations of 1 or
+2, asymmetric pads, channel counts from 3 to 128, output tiles of every divisor
+of the output, on whichever conv kernel the planner picks.
+
+Bars: i8 bit-exact (exact i32 sums, one rounding to f32); f16 / bf16 within a
+Frobenius relative error of 1e-3 of the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import xtile_amd as xt
+from tests.gpu_util import frob_rel, run_gpu, run_oracle
+from tests.random_programs import conv_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_conv_matches_the_oracle(cuda, seed):
+    mod, host, dtypes, desc = conv_case(seed)
+    got = run_gpu(mod, host, dtypes, cuda, case=f"random conv {seed}: {desc}")[2]
+    want = run_oracle(mod, host, 4)[2]
+    if dtypes[0] == "i8":
+        assert np.array_equal(got, want)
+    else:
+        assert frob_rel(got, want) <= 1e-3

@@ -28,3 +28,11 @@ def test_fusable_random_program_plans_onto_a_fused_kernel(seed):
 
     text, host, dtypes, outs = fused_program(seed)
     assert xt.plan(xt.parse(text))["kernel"].startswith("fused f32 tile=")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_conv_plans(seed):
+    from tests.random_programs import conv_case
+
+    mod, host, dtypes, desc = conv_case(seed)
+    assert xt.plan(mod)["kernel"].startswith("conv2d_nhwc")
