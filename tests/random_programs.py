@@ -280,3 +280,34 @@ def conv_case(seed: int):
                 f"tile {th}x{tw}")
         return mod, [x, f, o], [dt, dt, "f32"], desc
     raise RuntimeError("no plannable conv drawn")
+
+
+def gemm_case(seed: int):
+    """A random matmul program of xtile_amd.kernels: f16 / bf16 (f32 result)
+    or the i8 epilogue form (i8 result of A @ B * scale + bias), M, N, K
+    multiples of 64 up to 1024 (K of 128 for i8), Block tiles of 64, 128 or 256 dividing them.
+    Returns (module, host inputs, dtypes, output index, description)."""
+    from xtile_amd import kernels as K
+
+    rng = np.random.default_rng(30_000 + seed)
+    dt = str(rng.choice(["f16", "bf16", "i8"]))
+    m, n, k = (64 * int(rng.integers(1, 17)) for _ in range(3))
+    if dt == "i8":  # the i8 MFMA steps K by 128 (32x32x32, two steps in flight)
+        k = 128 * max(1, k // 128)
+    tm = int(rng.choice([t for t in (64, 128, 256) if m % t == 0]))
+    tn = int(rng.choice([t for t in (64, 128, 256) if n % t == 0]))
+    desc = f"{dt} {m}x{n}x{k} tile {tm}x{tn}"
+    if dt == "i8":
+        a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+        b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        s = (rng.uniform(0.5, 2.0, (1, n)) / (np.sqrt(k) * 64)).astype(np.float32)
+        bias = rng.uniform(-20, 20, (1, n)).astype(np.float32)
+        return K.matmul_i8(m, n, k, tm, tn), [a, b, np.zeros((m, n), np.int8), s, bias], \
+            ["i8", "i8", "i8", "f32", "f32"], 2, desc
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    if dt == "f16":
+        mod, a, b = K.matmul_f16(m, n, k, tm, tn), a.astype(np.float16), b.astype(np.float16)
+    else:
+        mod, a, b = K.matmul_bf16(m, n, k, tm, tn), f32_to_bf16_bits(a), f32_to_bf16_bits(b)
+    return mod, [a, b, np.zeros((m, n), np.float32)], [dt, dt, "f32"], 2, desc

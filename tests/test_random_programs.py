@@ -36,3 +36,11 @@ def test_random_conv_plans(seed):
 
     mod, host, dtypes, desc = conv_case(seed)
     assert xt.plan(mod)["kernel"].startswith("conv2d_nhwc")
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_gemm_plans_onto_the_gemm_kernel(seed):
+    from tests.random_programs import gemm_case
+
+    mod, host, dtypes, out, desc = gemm_case(seed)
+    assert xt.plan(mod)["kernel"].startswith("gemm")
