@@ -311,3 +311,46 @@ def gemm_case(seed: int):
     else:
         mod, a, b = K.matmul_bf16(m, n, k, tm, tn), f32_to_bf16_bits(a), f32_to_bf16_bits(b)
     return mod, [a, b, np.zeros((m, n), np.float32)], [dt, dt, "f32"], 2, desc
+
+
+def stream_case(seed: int):
+    """A random program of the two streaming families: f32 add over 2-D tiles
+    (any tile dividing the array, odd sizes included) or row softmax with
+    full-width row tiles of 1-16 rows and 1-8192 columns.  Returns (module,
+    host inputs, dtypes, output index, description)."""
+    from xtile_amd import kernels as K
+
+    rng = np.random.default_rng(40_000 + seed)
+
+    def divisor(v):
+        return int(rng.choice([d for d in range(1, min(v, 256) + 1) if v % d == 0]))
+
+    if rng.random() < 0.5:
+        rows, cols = int(rng.integers(1, 1025)), int(rng.integers(1, 1025))
+        th, tw = divisor(rows), divisor(cols)
+        a = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+        b = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+        return K.add(rows, cols, th, tw), [a, b, np.zeros_like(a)], ["f32"] * 3, 2, \
+            f"add {rows}x{cols} tile {th}x{tw}"
+    import xtile_amd as xt
+
+    for _ in range(100):  # long rows that are not float4-aligned go elsewhere or are refused: draw again
+        cols = int(rng.choice([int(rng.integers(1, 8193)), 2048 * int(rng.integers(1, 5)),
+                               64 * int(rng.integers(1, 65))]))
+        trow = int(rng.choice([1, 2, 4, 8, 16]))
+        rows = trow * int(rng.integers(1, 65))
+        mod = K.softmax(rows, cols, trow)
+        if xt.plan(mod)["kernel"].startswith("row_softmax") if _plans(mod) else False:
+            break
+    x = rng.normal(0, 2, (rows, cols)).astype(np.float32)
+    return mod, [x, np.zeros_like(x)], ["f32"] * 2, 1, f"softmax {rows}x{cols} tile {trow}x{cols}"
+
+
+def _plans(mod) -> bool:
+    import xtile_amd as xt
+
+    try:
+        xt.plan(mod)
+        return True
+    except NotImplementedError:
+        return False

@@ -204,3 +204,9 @@ def test_fused_kernels_are_compiled_into_the_code_object_cache(tmp_path, monkeyp
     other = tmp_path / "none"
     xt.plan(K.layernorm(24, 80, 8))
     assert not other.exists() and len(list(tmp_path.glob("*.co"))) == 1
+
+
+def test_softmax_rows_above_2048_need_float4_vectors():
+    assert xt.plan(K.softmax(64, 4096, 1))["kernel"].startswith("row_softmax")
+    assert xt.plan(K.softmax(64, 2047, 1))["kernel"].startswith("row_softmax")
+    assert xt.plan(K.softmax(122, 3798, 2))["kernel"].startswith("tile_vm")

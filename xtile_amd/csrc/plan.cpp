@@ -263,6 +263,14 @@ bool match_softmax(const Analysis& an, Plan& p, std::string& err) {
   // other shapes and types run on the tile interpreter
   if (t.elem != Elem::F32 || t.rank() != 2 || t.shape[1] > 8192) return false;
   if (!access_of(an, *ld, p.a, err) || !access_of(an, *st, p.c, err)) return false;
+  // rows above 2048 floats are held as float4 vectors: columns, pitches and
+  // tile origins must be multiples of 4 (the buffers' 16-byte alignment is
+  // checked at launch)
+  auto vec4 = [](const Access2D& a) {
+    return a.cols % 4 == 0 && a.ld % 4 == 0 && a.addr.c0 % 4 == 0 && a.addr.sx % 4 == 0 && a.addr.sy % 4 == 0 &&
+           a.addr.sz % 4 == 0;
+  };
+  if (t.shape[1] > 2048 && !(vec4(p.a) && vec4(p.c))) return false;
   p.kind = PlanKind::RowSoftmax;
   double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
   p.algo_bytes = blocks * double(t.numel()) * 8;
