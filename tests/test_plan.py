@@ -210,3 +210,86 @@ def test_softmax_rows_above_2048_need_float4_vectors():
     assert xt.plan(K.softmax(64, 4096, 1))["kernel"].startswith("row_softmax")
     assert xt.plan(K.softmax(64, 2047, 1))["kernel"].startswith("row_softmax")
     assert xt.plan(K.softmax(122, 3798, 2))["kernel"].startswith("tile_vm")
+
+
+def test_native_binding_has_the_reference_stage_names():
+    """A reference facade pointed at this binding (xtile/__init__.py:130-168
+    calls _native.nova_optimize ... nova_to_x1) gets NotImplementedError for
+    a module and TypeError for anything else, never AttributeError."""
+    from xtile_amd import _xtile as native
+
+    m = K.add(64, 128, 32, 64)
+    for name in ("nova_optimize", "nova_threading", "nova_barrier", "nova_allocate", "nova_to_x1"):
+        stage = getattr(native, name)
+        with pytest.raises(NotImplementedError, match="x1 NPU lowering"):
+            stage(m)
+        with pytest.raises(TypeError):
+            stage("not a module")
+        with pytest.raises(NotImplementedError):
+            getattr(xt, name)(m)
+
+
+def _add_program(rows, cols, th, tw, grid):
+    return xt.parse(f"""
+func.func @k(%a: memref<{rows}x{cols}xf32>, %b: memref<{rows}x{cols}xf32>, %c: memref<{rows}x{cols}xf32>) attributes {{xt.grid = array<i32: {grid[0]}, {grid[1]}, 1>}} {{
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %0 = xt.load(%a, %bid#0, %bid#1) : (memref<{rows}x{cols}xf32>, i32, i32) -> tensor<{th}x{tw}xf32>
+  %1 = xt.load(%b, %bid#0, %bid#1) : (memref<{rows}x{cols}xf32>, i32, i32) -> tensor<{th}x{tw}xf32>
+  %2 = xt.add(%0, %1) : tensor<{th}x{tw}xf32>, tensor<{th}x{tw}xf32> -> tensor<{th}x{tw}xf32>
+  xt.store(%2, %c, %bid#0, %bid#1) : (tensor<{th}x{tw}xf32>, memref<{rows}x{cols}xf32>, i32, i32) -> ()
+  func.return
+}}""")
+
+
+def test_grid_beyond_one_launch_is_refused_before_any_device_call():
+    """2^31 Blocks of 1x1 tiles over an 8 GiB array: the Block count is
+    computed in 64 bits and the launcher refuses it (XT_ERR_ARGUMENT ->
+    ValueError) before it makes any HIP call, so this runs without a GPU."""
+    from xtile_amd import _xtile as native
+
+    m = _add_program(65536, 32768, 1, 1, (65536, 32768))
+    assert xt.plan(m)["kernel"].startswith("ew_binary")
+    nbytes = 65536 * 32768 * 4
+    fake = [0x10000, 0x20000, 0x30000]  # never dereferenced: the launch is refused first
+    with pytest.raises(ValueError, match="exceeds one launch"):
+        native.launch(m, None, fake, [nbytes] * 3)
+    # just inside the limit (2^24 workgroups of 256 work-items) the plan is unchanged
+    ok = _add_program(4096, 4096, 1, 1, (4096, 4095))
+    assert xt.plan(ok)["kernel"].startswith("ew_binary")
+
+
+INDEPENDENCE = """
+func.func @k(%a: memref<64x64xf32>, %c: memref<64x64xf32>) attributes {{xt.grid = array<i32: 2, 2, 1>}} {{
+  %bid:3 = xt.get_tile_block_id : i32, i32, i32
+  %c0 = arith.constant 0 : i32
+  %0 = xt.load(%a, {load}) : (memref<64x64xf32>, i32, i32) -> tensor<32x32xf32>
+  %1 = xt.exp(%0) : tensor<32x32xf32> -> tensor<32x32xf32>
+  xt.store(%1, %c, {store}) : (tensor<32x32xf32>, memref<64x64xf32>, i32, i32) -> ()
+  func.return
+}}"""
+
+
+def test_blocks_storing_different_values_to_one_tile_are_refused():
+    """Every Block stores to tile (0, bid1) a value that depends on bid0: the
+    reference's serial order keeps the last Block's (XTSerialize.cpp:68-104),
+    concurrent Blocks race, so the plan is refused."""
+    m = xt.parse(INDEPENDENCE.format(load="%bid#0, %bid#1", store="%c0, %bid#1"))
+    with pytest.raises(NotImplementedError, match="grid axis 0 store different values"):
+        xt.plan(m)
+    # the same store of a value that does not depend on bid0 writes equal values: allowed
+    same = xt.parse(INDEPENDENCE.format(load="%c0, %bid#1", store="%c0, %bid#1"))
+    assert xt.plan(same)["kernel"]
+    # a shared=1 load reads the leader's tile, so its value does not vary along axis 0
+    shared = xt.parse(INDEPENDENCE.format(load="%bid#0, %bid#1", store="%c0, %bid#1").replace(
+        "%0 = xt.load(%a, %bid#0, %bid#1)", "%0 = xt.load(%a, %bid#0, %bid#1) {shared = 1 : i64}"))
+    assert xt.plan(shared)["kernel"]
+
+
+def test_in_place_programs_must_touch_only_their_own_tile():
+    """A memref loaded and stored: allowed at the same tile (in place), refused
+    when Blocks read tiles other Blocks store (a transposed in-place store)."""
+    inplace = INDEPENDENCE.format(load="%bid#0, %bid#1", store="%bid#0, %bid#1").replace("%c,", "%a,")
+    assert xt.plan(xt.parse(inplace))["kernel"]
+    transposed = INDEPENDENCE.format(load="%bid#0, %bid#1", store="%bid#1, %bid#0").replace("%c,", "%a,")
+    with pytest.raises(NotImplementedError, match="stored and also accessed at another tile"):
+        xt.plan(xt.parse(transposed))

@@ -121,22 +121,24 @@ def xt_to_nova(module: Any):
     return _after_pass(module, _native.xt_to_nova(module))
 
 
-def _x1_unavailable(name: str):
+def _x1_stage(name: str):
+    native = getattr(_native, name)
+
     def stage(module: Any):
-        raise NotImplementedError(
-            f"xt.{name} belongs to the reference's x1 NPU lowering, which the MI355X "
-            "backend replaces with HIP kernels; use xt.compile / xt.launch"
-        )
+        """A stage of the reference's x1 NPU lowering: raises
+        NotImplementedError (the MI355X backend runs HIP kernels instead)."""
+        return native(module)
 
     stage.__name__ = name
+    stage.__qualname__ = name
     return stage
 
 
-nova_optimize = _x1_unavailable("nova_optimize")
-nova_threading = _x1_unavailable("nova_threading")
-nova_barrier = _x1_unavailable("nova_barrier")
-nova_allocate = _x1_unavailable("nova_allocate")
-nova_to_x1 = _x1_unavailable("nova_to_x1")
+nova_optimize = _x1_stage("nova_optimize")
+nova_threading = _x1_stage("nova_threading")
+nova_barrier = _x1_stage("nova_barrier")
+nova_allocate = _x1_stage("nova_allocate")
+nova_to_x1 = _x1_stage("nova_to_x1")
 
 
 def plan(module: Any, func: str | None = None) -> dict:

@@ -9,8 +9,10 @@ exception types:
   _module_asm(module)               str
   TypeError for objects that are not xtile modules (XTModule.cpp:40-51)
 
-plus what the GPU backend adds: ``canonicalize``, ``signature``, ``plan`` and
-``launch``.  The library is loaded from ``xtile_amd/lib``; if it is missing the
+and ``nova_optimize`` / ``nova_threading`` / ``nova_barrier`` /
+``nova_allocate`` / ``nova_to_x1``, which raise NotImplementedError (there is
+no x1 NPU target), plus what the GPU backend adds: ``canonicalize``,
+``xt_to_nova``, ``signature``, ``plan`` and ``launch``.  The library is loaded from ``xtile_amd/lib``; if it is missing the
 import fails loudly - there is no fallback path.
 """
 
@@ -190,6 +192,33 @@ def canonicalize(module: object) -> object:
 
 def xt_to_nova(module: object) -> object:
     return _run_pass(module, "xt-to-nova")
+
+
+def _x1_stage(name: str):
+    """The reference module's NPU lowering stages (python/XTModule.cpp:
+    nova_optimize, nova_threading, nova_barrier, nova_allocate, nova_to_x1),
+    which the reference facade calls from compile and save_compile_results
+    (xtile/__init__.py:130-168).  The HIP backend has no x1 NPU target, so
+    each checks its argument as the reference's runPass does (TypeError for a
+    non-module) and then raises NotImplementedError naming what to use."""
+
+    def stage(module: object) -> object:
+        _unwrap(module)
+        raise NotImplementedError(
+            f"{name} belongs to the reference's x1 NPU lowering, which the MI355X "
+            "backend replaces with HIP kernels; use xt.compile / xt.launch"
+        )
+
+    stage.__name__ = name
+    stage.__qualname__ = name
+    return stage
+
+
+nova_optimize = _x1_stage("nova_optimize")
+nova_threading = _x1_stage("nova_threading")
+nova_barrier = _x1_stage("nova_barrier")
+nova_allocate = _x1_stage("nova_allocate")
+nova_to_x1 = _x1_stage("nova_to_x1")
 
 
 def _module_asm(module: object) -> str:

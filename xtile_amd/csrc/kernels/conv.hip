@@ -877,7 +877,7 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   a.filt_bytes = (unsigned)filt_bytes;
   a.image_bytes = (unsigned)image_bytes;
   const long long bands = gB * a.bands_per_image;
-  if (bands > 0x7fffffff) return false;
+  if (!grid_fits(bands, 512)) return false;
   const int el = i8 ? kBandI8 : c.elem == xt::Elem::BF16 ? kBandBF16 : kBandF16;
   const int nt = a.CO / 32;
   const int cs = (int)(PB / 32);  // K steps per tap: 2, 4, 6 or 8 (checked above)

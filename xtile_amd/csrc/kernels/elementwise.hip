@@ -293,8 +293,6 @@ bool aligned4(const xt::Access2D& a, const void* base) {
          a.addr.c0 % 4 == 0 && a.addr.sx % 4 == 0 && a.addr.sy % 4 == 0 && a.addr.sz % 4 == 0;
 }
 
-int num_blocks(const xt::Plan& p) { return p.grid[0] * p.grid[1] * p.grid[2]; }
-
 }  // namespace
 
 hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why) {
@@ -331,7 +329,12 @@ hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s,
   const long long sx = p.c.addr.sx < 0 ? -p.c.addr.sx : p.c.addr.sx;
   const long long sy = p.c.addr.sy < 0 ? -p.c.addr.sy : p.c.addr.sy;
   a.y_fastest = (p.grid[1] > 1 && (sx == 0 || (sy != 0 && sy < sx))) ? 1 : 0;
-  dim3 grid(num_blocks(p)), block(256);
+  const long long blocks = grid_blocks(p);
+  if (!grid_fits(blocks, 256)) {
+    why = "elementwise grid of " + std::to_string(blocks) + " Blocks exceeds one launch (2^24 workgroups of 256)";
+    return hipErrorInvalidValue;
+  }
+  dim3 grid(static_cast<unsigned>(blocks)), block(256);
   const int op = static_cast<int>(p.ew_op);
   const bool pow2 = a.cv_shift >= 0;
   // kernel variant index: op (3) x vector width (2) x U (3) x pow2 (2)
@@ -378,8 +381,14 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
     return hipErrorInvalidValue;
   }
   const int vw = (aligned4(p.a, a.x) && aligned4(p.c, a.y)) ? 4 : 1;
-  dim3 grid(num_blocks(p));
-  if (vw == 4 && a.cols % 2048 == 0 && a.cols <= 8 * 2048) {
+  const long long blocks = grid_blocks(p);
+  const bool wide = vw == 4 && a.cols % 2048 == 0 && a.cols <= 8 * 2048;
+  if (!grid_fits(blocks, wide ? 512 : 256)) {
+    why = "softmax grid of " + std::to_string(blocks) + " Blocks exceeds one launch";
+    return hipErrorInvalidValue;
+  }
+  dim3 grid(static_cast<unsigned>(blocks));
+  if (wide) {
     a.tpr = 512;
     switch (a.cols / 2048) {
 #define XT_SMW(NVV) \
@@ -394,7 +403,12 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
   int nv = 1;
   while (nv < 8 && nv * vw * 256 < a.cols) nv *= 2;
   if (nv * vw * 256 < a.cols) {
-    why = "softmax row too long for the register-resident kernel";
+    // rows above 2048 floats are planned here only as float4 vectors; a buffer
+    // that is not 16-byte aligned runs on the tile interpreter instead
+    if (p.vm_fallback) return launch_tilevm(p, bufs, s, why);
+    why = "softmax rows of " + std::to_string(a.cols) +
+          " floats need 16-byte aligned buffers, and the tile interpreter cannot run this program: " +
+          p.vm_fallback_why;
     return hipErrorInvalidValue;
   }
   int need = (a.cols + nv * vw - 1) / (nv * vw);

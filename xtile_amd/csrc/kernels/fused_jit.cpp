@@ -139,7 +139,13 @@ hipError_t launch_fused(const xt::Plan& p, void* const* bufs, hipStream_t s, std
   // row accesses are vw-element vectors: a buffer not aligned to one goes to the interpreter
   for (const xt::VmAccess& a : vm.access) {
     const uintptr_t align = static_cast<uintptr_t>(fp->vw) * xt::elem_bytes(a.elem);
-    if (reinterpret_cast<uintptr_t>(bufs[a.arg]) % align) return launch_tilevm(p, bufs, s, why);
+    if (reinterpret_cast<uintptr_t>(bufs[a.arg]) % align) {
+      if (p.vm_fallback) return launch_tilevm(p, bufs, s, why);
+      why = "buffer " + std::to_string(a.arg) + " is not aligned to " + std::to_string(align) +
+            " bytes, which the fused kernel's row vectors need, and the tile interpreter cannot run "
+            "this program: " + p.vm_fallback_why;
+      return hipErrorInvalidValue;
+    }
   }
   const long long blocks = static_cast<long long>(p.grid[0]) * p.grid[1] * p.grid[2];
   if (blocks < 1 || blocks > 0x7fffffffLL || blocks * fp->threads >= (1LL << 32)) {

@@ -528,8 +528,8 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   a.sub_m = cm.sub;
   a.sub_n = cn.sub;
   long long nwg = (long long)vg[0] * vg[1] * vg[2] * a.sub_m * a.sub_n;
-  if (nwg > 0x7fffffff) {
-    why = "matmul grid too large";
+  if (!grid_fits(nwg, 256)) {
+    why = "matmul grid of " + std::to_string(nwg) + " workgroup tiles exceeds one launch";
     return hipErrorInvalidValue;
   }
   a.nwg = static_cast<int>(nwg);

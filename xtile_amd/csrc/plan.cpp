@@ -188,6 +188,101 @@ const Op* def_of(const Analysis& an, int v) {
   return it == an.def.end() ? nullptr : it->second;
 }
 
+// -- Block independence --------------------------------------------------------
+
+// The reference's xt-serialize runs the Blocks one after another in z -> y ->
+// x order (lib/xt/XTSerialize.cpp:68-104), so where two Blocks store to one
+// tile the later one's values remain, and a Block that loads a tile another
+// Block stores sees it before or after that store depending on the order.
+// Every kernel here runs Blocks concurrently and in any order.  The two agree
+// exactly when no two Blocks store different values to one tile and no Block
+// loads a tile that another Block stores; programs outside that are refused
+// (README.md:85-89 leaves multi-writer results undefined).
+bool check_independent(const Analysis& an, std::string& err) {
+  unsigned live = 0;  // grid axes with more than one Block
+  for (int k = 0; k < 3; ++k)
+    if (an.grid[k] > 1) live |= 1u << k;
+  auto axes_of = [&](const Op* o, size_t first, size_t last, int shared, unsigned& out) {
+    out = 0;
+    for (size_t i = first; i < last && i < o->operands.size(); ++i) {
+      Coord c;
+      if (!coord_of(an, o->operands[i], shared, c, err)) return false;
+      if (c.axis >= 0) out |= 1u << c.axis;
+    }
+    return true;
+  };
+  std::map<int, unsigned> dep;  // tensor value -> grid axes its elements vary along
+  std::map<int, std::vector<const Op*>> loads, stores;  // by memref value
+  for (const Op* o : an.compute) {
+    unsigned d = 0;
+    if (o->name == "xt.load") {
+      int shared = 0;
+      if (const Attr* sh = find_attr(o->attrs, "shared")) shared = static_cast<int>(sh->i);
+      if (!axes_of(o, 1, o->operands.size(), shared, d)) return false;
+      loads[o->operands[0]].push_back(o);
+    } else if (o->name == "xt.load_conv2d") {
+      if (!axes_of(o, 2, o->operands.size(), 0, d)) return false;
+      if (o->operands.size() > 1 && dep.count(o->operands[1])) d |= dep[o->operands[1]];
+      loads[o->operands[0]].push_back(o);
+    } else if (o->name == "xt.store") {
+      unsigned at = 0;
+      if (!axes_of(o, 2, o->operands.size(), 0, at)) return false;
+      const unsigned vd = (dep.count(o->operands[0]) ? dep[o->operands[0]] : 0) & live & ~at;
+      if (vd) {
+        const int ax = __builtin_ctz(vd);
+        err = "Blocks along grid axis " + std::to_string(ax) + " store different values to the same tile of " +
+              "memref argument #" + std::to_string(an.arg_index(o->operands[1])) +
+              "; the reference's serial Block order keeps the last one's, which concurrent Blocks do not "
+              "reproduce (give the store a coordinate on that axis)";
+        return false;
+      }
+      stores[o->operands[1]].push_back(o);
+      continue;
+    } else {
+      for (int v : o->operands)
+        if (dep.count(v)) d |= dep[v];
+    }
+    for (int r : o->results) dep[r] = d;
+  }
+  // a memref that is stored and also loaded (or stored twice): every access
+  // must be the same tile at the same coordinates, so a Block only ever reads
+  // and writes its own tile
+  for (const auto& kv : stores) {
+    std::vector<const Op*> acc = kv.second;
+    auto it = loads.find(kv.first);
+    if (it != loads.end()) acc.insert(acc.end(), it->second.begin(), it->second.end());
+    if (acc.size() < 2) continue;
+    auto key = [&](const Op* o) {
+      std::vector<int64_t> k;
+      const bool st = o->name == "xt.store";
+      const Type& t = st ? an.f.type_of(o->operands[0]) : an.f.type_of(o->results[0]);
+      k.insert(k.end(), t.shape.begin(), t.shape.end());
+      k.push_back(o->name == "xt.load_conv2d" ? 1 : 0);
+      const size_t first = st ? 2 : (o->name == "xt.load_conv2d" ? 2 : 1);
+      int shared = 0;
+      if (const Attr* sh = find_attr(o->attrs, "shared")) shared = static_cast<int>(sh->i);
+      for (size_t i = first; i < o->operands.size(); ++i) {
+        Coord c;
+        std::string e;
+        coord_of(an, o->operands[i], shared, c, e);
+        k.push_back(c.axis);
+        k.push_back(c.value);
+      }
+      return k;
+    };
+    const auto k0 = key(acc[0]);
+    for (size_t i = 1; i < acc.size(); ++i)
+      if (key(acc[i]) != k0) {
+        err = "memref argument #" + std::to_string(an.arg_index(kv.first)) +
+              " is stored and also accessed at another tile; concurrent Blocks would read or overwrite "
+              "tiles other Blocks store, which the reference's serial Block order defines and this "
+              "backend does not reproduce";
+        return false;
+      }
+  }
+  return true;
+}
+
 // -- EwBinary ----------------------------------------------------------------
 
 bool match_ew(const Analysis& an, Plan& p, std::string& err) {
@@ -855,13 +950,30 @@ bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& 
       err = "stored values must be computed in the function";
       return false;
     }
+  if (!check_independent(an, err)) {
+    err = "@" + f->name + ": " + err;
+    return false;
+  }
   // the specialised kernels first; what they decline (with a reason) goes to
   // the tile interpreter, and the first reason is reported if that fails too
   err.clear();
   std::string first;
   for (auto match : {match_ew, match_softmax, match_gemm, match_conv}) {
     std::string why;
-    if (match(an, p, why)) return true;
+    if (match(an, p, why)) {
+      if (p.kind == PlanKind::RowSoftmax) {
+        // the interpreter lowering, for buffers the softmax kernel cannot vectorise
+        Plan q = p;
+        std::string e2;
+        if (match_vm(an, q, e2) && vm_fits_interpreter(q.vm, e2)) {
+          p.vm = std::move(q.vm);
+          p.vm_fallback = true;
+        } else {
+          p.vm_fallback_why = e2.empty() ? "no interpreter lowering" : e2;
+        }
+      }
+      return true;
+    }
     if (first.empty()) first = why;
   }
   if (match_vm(an, p, err)) {
@@ -872,6 +984,7 @@ bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& 
     if (!(env && std::string(env) == "0") && fuse_vm(p.vm, p.grid, fp, why)) {
       p.kind = PlanKind::Fused;
       p.fused = std::make_shared<FusedPlan>(std::move(fp));
+      p.vm_fallback = vm_fits_interpreter(p.vm, p.vm_fallback_why);
       return true;
     }
     p.unfused = env && std::string(env) == "0" ? "XTILE_AMD_FUSE=0" : why;

@@ -123,6 +123,11 @@ struct Plan {
   VmPlan vm;
   std::shared_ptr<FusedPlan> fused;  // Fused: the generated kernel (vm keeps the accesses)
   std::string unfused;               // TileVM: why the program is not fused
+  // RowSoftmax and Fused plans fall back to the tile interpreter at launch
+  // when a buffer is not aligned to their vectors; vm_fallback says whether
+  // `vm` holds an interpreter lowering that fits, vm_fallback_why why not.
+  bool vm_fallback = false;
+  std::string vm_fallback_why;
   double algo_bytes = 0;  // algorithmic HBM bytes per launch
   double algo_flops = 0;  // algorithmic FLOPs per launch
   std::string describe() const;
