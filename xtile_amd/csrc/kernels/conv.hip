@@ -404,8 +404,9 @@ __global__ __launch_bounds__(WG, 1) void conv2d_kernel(ConvArgs p) {
     load_halo(p, cur, ltid, hv, dst);
     store_halo(Is, hv, dst);
   } else {
-    // The filter tile is the whole filter array (checked by the planner), so
-    // every Block - and every unit of this workgroup - uses the same origin.
+    // Every Block uses the same filter (the launcher sends filters that move
+    // with the Block to the generic kernel), so every unit of this
+    // workgroup uses the first one's origin.
     // The compute waves stage it while the loaders fetch the first halo.
     int x, y, z;
     decode_block(u / p.units_per_block, p.gx, p.gy, x, y, z);
@@ -779,7 +780,7 @@ int ilog2(unsigned v) {
 
 // The band kernel applies when the Blocks tile images [0, gB) x all output
 // rows and columns exactly once, in the output's natural NHWC addressing, and
-// the filter tile is the whole filter.  Returns false (nothing launched) when
+// every Block uses one filter.  Returns false (nothing launched) when
 // it does not apply; `e` carries a launch error otherwise.
 bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, int cus, hipError_t& e) {
   const xt::ConvPlan& c = p.conv;
@@ -794,7 +795,8 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
       (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
-  if (c.filt_addr.c0 || c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz) return false;
+  // one filter for every Block (its origin may be any offset into a stack of filters)
+  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz) return false;
   if (c.TB != 1 || c.TC != c.CO || c.out_elem != xt::Elem::F32) return false;
   const bool i8 = c.elem == xt::Elem::I8;
   const long long es = i8 ? 1 : 2;
@@ -833,7 +835,7 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   if (R * c.out_W * c.CO * 4 >= (1LL << 31)) return false;
   BandArgs a;
   a.src = static_cast<const unsigned char*>(bufs[c.src_arg]);
-  a.filt = static_cast<const unsigned char*>(bufs[c.filt_arg]);
+  a.filt = static_cast<const unsigned char*>(bufs[c.filt_arg]) + c.filt_addr.c0 * es;
   a.out = static_cast<float*>(bufs[c.out_arg]);
   for (const void* ptr : {(const void*)a.src, (const void*)a.filt, (const void*)a.out})
     if (reinterpret_cast<uintptr_t>(ptr) % 16) return false;
@@ -946,7 +948,7 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   const int nt = (a.CO + 31) / 32;
   bool persistent_ok = c.elem != xt::Elem::I8 && c.out_elem == xt::Elem::F32 && c.TB == 1 && c.TC == c.CO &&
                        a.C % 32 == 0 && a.CO % 16 == 0 && a.CO <= 128 && a.out_C % 4 == 0 &&
-                       a.tf.c0 % 8 == 0 && a.tf.sx % 8 == 0 && a.tf.sy % 8 == 0 && a.tf.sz % 8 == 0;
+                       a.tf.c0 % 8 == 0 && a.tf.sx == 0 && a.tf.sy == 0 && a.tf.sz == 0;
   for (const void* ptr : {(const void*)a.src, (const void*)a.filt, (const void*)a.out})
     if (reinterpret_cast<uintptr_t>(ptr) % 16) persistent_ok = false;
   int dev = 0;

@@ -12,6 +12,8 @@
 //              (kernels/conv2d.py:10-37; conv slice math lib/xt/XTToNova.cpp:110-142)
 #include "plan.h"
 
+#include <algorithm>
+
 #include <map>
 #include <set>
 #include <cstdlib>
@@ -503,8 +505,11 @@ bool match_conv(const Analysis& an, Plan& p, std::string& err) {
           "result";
     return false;
   }
-  if (ft.shape != fm.shape) {
-    err = "the HIP conv2d kernel needs the filter tile to be the whole filter array";
+  // the filter tile is one whole filter out of a stack along KH: its last
+  // three dims are the memref's, so it is one contiguous K x Cout block
+  if (ft.shape.size() != 4 || fm.shape.size() != 4 ||
+      !std::equal(ft.shape.begin() + 1, ft.shape.end(), fm.shape.begin() + 1)) {
+    err = "the HIP conv2d kernels need the filter tile to span the filter array's KW, Cin and Cout dims";
     return false;
   }
   if (const Attr* g = find_attr(cv->attrs, "group"))
