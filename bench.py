@@ -8,12 +8,25 @@ headline line is C2 (row softmax fp32 8192x4096, BASELINE.json configs[1]);
 the six BASELINE.json configurations (C1-C6) and C7, a row layernorm run as a
 fused tile program, are measured and reported under "per_config".
 
-Timing: W untimed warm-up launches, then K launches captured in a HIP graph and
-replayed once between two HIP events on the replay stream, with device
-synchronisation on both sides; per-step time = elapsed / K.  Every step reads
-a different input set (buffer rotation over >= 1 GiB) so inputs are not left
-resident in the 256 MB Infinity Cache between steps.  Inputs are in HBM before
-the timed region starts; no host transfer is timed.
+Order of work: every input is generated on the host first; then the GPU
+legs run back to back - the ceiling kernels of include/xt_ceiling.h (an MFMA
+loop, a streaming copy, an empty kernel), then each configuration, then the
+vendor GEMM - and only then the CPU legs (the oracle), so the GPU is never
+left idle between timed regions.
+
+Timing of a configuration: W untimed warm-up launches, one more eager launch
+whose output is kept as the reference, then K launches captured in a HIP
+graph and replayed once between two HIP events on the launch stream, with
+device synchronisation on both sides; per-step time = elapsed / K.  Every step
+reads a different input set (buffer rotation over >= 1 GiB) so inputs are not
+left resident in the 256 MB Infinity Cache between steps.  Inputs are in HBM
+before the timed region starts; no host transfer is timed.
+
+Checks: the output of input set 0 is cleared after the warm-up and the
+capture, just before the timed replay; after the replay it must equal the eager reference bit for bit, and the
+reference must match the oracle (the CPU leg's own output on the same inputs)
+to the configuration's bar.  A failed check fails the run: no JSON line is
+printed and the exit status is 1.
 
 roofline.achieved = algorithmic bytes (or FLOPs) of one launch / per-step
 time; roofline.traffic = measured HBM bytes per launch from the rocprofv3
@@ -27,6 +40,7 @@ same workload for about --cpu-seconds.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -45,36 +59,41 @@ METRIC = "GB/s (add, softmax) & TFLOP/s (matmul, conv2d) on 1 MI355X, % of roofl
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "i8": 5000.0}  # dense; i8 in TOP/s
 ROTATE_BYTES = 1 << 30
+ALL = ["c1", "c2", "c3", "c4", "c5", "c6", "c7"]
 
 
 def _f32(a):
     return np.asarray(a, dtype=np.float32)
 
 
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bit patterns, round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = np.where(nan, (u >> 16) | 0x40, r)
+    return r.astype(np.uint16)
+
+
 def make_config(name: str):
     """(module, host inputs, dtypes, out index, meta) for one configuration."""
-    from oracle import f32_to_bf16_bits
     from xtile_amd import kernels as K
 
     if name == "c1":
         rng = np.random.default_rng(1)
         a = _f32(rng.uniform(-1, 1, (1024, 1024)))
         b = _f32(rng.uniform(-1, 1, (1024, 1024)))
-        return K.CONFIGS["c1_add"](), [a, b, np.zeros_like(a)], ["f32"] * 3, {
+        return K.CONFIGS["c1_add"](), [a, b, np.zeros_like(a)], ["f32"] * 3, 2, {
             "workload": "c1_add: C = A + B fp32 1024x1024, 32x64 tiles, grid (32,16,1)",
-            "unit": "GB/s",
-            "bound": "hbm",
-            "dtype": "f32",
+            "unit": "GB/s", "bound": "hbm", "dtype": "f32", "check": ("exact", 0.0),
             "data": "synthetic: numpy PCG64 seed=1, uniform[-1,1]",
         }
     if name == "c2":
         rng = np.random.default_rng(2)
         x = _f32(rng.normal(0.0, 2.0, (8192, 4096)))
-        return K.CONFIGS["c2_softmax"](), [x, np.zeros_like(x)], ["f32"] * 2, {
+        return K.CONFIGS["c2_softmax"](), [x, np.zeros_like(x)], ["f32"] * 2, 1, {
             "workload": "c2_softmax: row softmax fp32 8192x4096, one 1x4096 row per Block, grid (8192,1,1)",
-            "unit": "GB/s",
-            "bound": "hbm",
-            "dtype": "f32",
+            "unit": "GB/s", "bound": "hbm", "dtype": "f32", "check": ("max_rel", 1e-5),
             "data": "synthetic: numpy PCG64 seed=2, normal(0,2)",
         }
     if name == "c7":
@@ -84,12 +103,10 @@ def make_config(name: str):
         b = _f32(rng.normal(0.0, 0.2, (1, 4096)))
         n = np.full((1, 1), 1.0 / 4096, np.float32)
         e = np.full((1, 1), 1e-5, np.float32)
-        return K.layernorm(8192, 4096, 1), [x, g, b, n, e, np.zeros_like(x)], ["f32"] * 6, {
+        return K.layernorm(8192, 4096, 1), [x, g, b, n, e, np.zeros_like(x)], ["f32"] * 6, 5, {
             "workload": "c7_layernorm: row layernorm fp32 8192x4096 (a program outside the four benchmark "
                         "families, run as a fused tile program), one 1x4096 row per Block, grid (8192,1,1)",
-            "unit": "GB/s",
-            "bound": "hbm",
-            "dtype": "f32",
+            "unit": "GB/s", "bound": "hbm", "dtype": "f32", "check": ("max_abs", 5e-5),
             "data": "synthetic: numpy PCG64 seed=7, x normal(0,1.5), gamma normal(1,0.2), beta normal(0,0.2)",
         }
     if name == "c3":
@@ -97,14 +114,10 @@ def make_config(name: str):
         a = rng.uniform(-1, 1, (4096, 4096)).astype(np.float16)
         b = rng.uniform(-1, 1, (4096, 4096)).astype(np.float16)
         return K.CONFIGS["c3_matmul_f16"](), [a, b, np.zeros((4096, 4096), np.float32)], [
-            "f16",
-            "f16",
-            "f32",
-        ], {
-            "workload": "c3_matmul_f16: C = A @ B, M=N=K=4096, f16 in, f32 acc/out, 128x128 Block tiles, B shared=1, grid (32,32,1)",
-            "unit": "TFLOP/s",
-            "bound": "mfma",
-            "dtype": "f16",
+            "f16", "f16", "f32"], 2, {
+            "workload": "c3_matmul_f16: C = A @ B, M=N=K=4096, f16 in, f32 acc/out, 128x128 Block tiles, "
+                        "B shared=1, grid (32,32,1)",
+            "unit": "TFLOP/s", "bound": "mfma", "dtype": "f16", "check": ("frob", 1e-3),
             "data": "synthetic: numpy PCG64 seed=3, uniform[-1,1] -> f16",
         }
     if name == "c4":
@@ -112,29 +125,21 @@ def make_config(name: str):
         x = rng.normal(0, 0.1, (32, 56, 56, 64)).astype(np.float16)
         f = rng.normal(0, 0.1, (3, 3, 64, 64)).astype(np.float16)
         return K.CONFIGS["c4_conv2d_f16"](), [x, f, np.zeros((32, 56, 56, 64), np.float32)], [
-            "f16",
-            "f16",
-            "f32",
-        ], {
-            "workload": "c4_conv2d_f16: NHWC 32x56x56x64 * 3x3x64x64, stride 1, pad 1, f16 in, f32 out, 1x4x56x64 Block tiles, filter shared=2, grid (32,14,1)",
-            "unit": "TFLOP/s",
-            "bound": "hbm",
-            "dtype": "f16",
+            "f16", "f16", "f32"], 2, {
+            "workload": "c4_conv2d_f16: NHWC 32x56x56x64 * 3x3x64x64, stride 1, pad 1, f16 in, f32 out, "
+                        "1x4x56x64 Block tiles, filter shared=2, grid (32,14,1)",
+            "unit": "TFLOP/s", "bound": "hbm", "dtype": "f16", "check": ("frob", 1e-3),
             "data": "synthetic: numpy PCG64 seed=4, normal(0,0.1) -> f16",
         }
     if name == "c5":
         rng = np.random.default_rng(5)
-        a = f32_to_bf16_bits(_f32(rng.normal(0, 0.02, (4096, 4096))))
-        b = f32_to_bf16_bits(_f32(rng.normal(0, 0.02, (4096, 11008))))
+        a = bf16_bits(_f32(rng.normal(0, 0.02, (4096, 4096))))
+        b = bf16_bits(_f32(rng.normal(0, 0.02, (4096, 11008))))
         return K.CONFIGS["c5_matmul_bf16"](), [a, b, np.zeros((4096, 11008), np.float32)], [
-            "bf16",
-            "bf16",
-            "f32",
-        ], {
-            "workload": "c5_matmul_bf16: C = A @ B, M=4096 N=11008 K=4096, bf16 in (RNE), f32 out, 256x128 Block tiles, A shared=1, grid (86,16,1)",
-            "unit": "TFLOP/s",
-            "bound": "mfma",
-            "dtype": "bf16",
+            "bf16", "bf16", "f32"], 2, {
+            "workload": "c5_matmul_bf16: C = A @ B, M=4096 N=11008 K=4096, bf16 in (RNE), f32 out, "
+                        "256x128 Block tiles, A shared=1, grid (86,16,1)",
+            "unit": "TFLOP/s", "bound": "mfma", "dtype": "bf16", "check": ("frob", 1e-3),
             "data": "synthetic: numpy PCG64 seed=5, normal(0,0.02) -> bf16 (RNE)",
         }
     if name == "c6":
@@ -145,13 +150,10 @@ def make_config(name: str):
         s = _f32(rng.uniform(0.5, 2.0, (1, n)) / (np.sqrt(k) * 64))
         bias = _f32(rng.uniform(-20, 20, (1, n)))
         return K.CONFIGS["c6_matmul_i8"](), [a, b, np.zeros((m, n), np.int8), s, bias], [
-            "i8", "i8", "i8", "f32", "f32"
-        ], {
+            "i8", "i8", "i8", "f32", "f32"], 2, {
             "workload": "c6_matmul_i8: kernels/matmul.py, C = int8(A @ B * scale + bias), M=N=K=4096, "
-            "i8 in, i32 acc, f32 epilogue, i8 out, 64x64 Block tiles, B/scale/bias shared=1, grid (64,64,1)",
-            "unit": "TOP/s",
-            "bound": "mfma",
-            "dtype": "i8",
+                        "i8 in, i32 acc, f32 epilogue, i8 out, 64x64 Block tiles, B/scale/bias shared=1, grid (64,64,1)",
+            "unit": "TOP/s", "bound": "mfma", "dtype": "i8", "check": ("exact", 0.0),
             "data": "synthetic: numpy PCG64 seed=6, A,B uniform int8, scale ~U[0.5,2]/(64 sqrt(K)), bias ~U[-20,20]",
         }
     raise ValueError(f"unknown config {name}")
@@ -172,38 +174,51 @@ def _traffic(name: str):
     return None
 
 
-def gpu_time(module, host, dtypes, steps: int, warmup: int, use_graph: bool):
-    """Average ms per launch over `steps` launches, rotating input sets."""
+# -- device helpers ------------------------------------------------------------------
+
+
+def to_device(arr: np.ndarray, dtype: str, device):
     import torch
 
-    import xtile_amd as xt
-    from tests.gpu_util import to_device
+    if dtype == "bf16":
+        return torch.from_numpy(np.ascontiguousarray(arr).view(np.int16)).view(torch.bfloat16).to(device)
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
 
-    dev = torch.device("cuda:0")
-    set_bytes = sum(h.nbytes for h in host)
-    nsets = max(1, min(128, math.ceil(ROTATE_BYTES / set_bytes)))
-    first = [to_device(h, d, dev) for h, d in zip(host, dtypes)]
-    sets = [first] + [[t.clone() for t in first] for _ in range(nsets - 1)]
-    torch.cuda.synchronize()
-    stream = torch.cuda.Stream(device=dev)
+
+def to_host(t, dtype: str) -> np.ndarray:
+    import torch
+
+    t = t.detach().cpu()
+    if dtype == "bf16":
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool, before_replay=None):
+    """Average ms per launch of `launch(i)` (i = input set) over `steps`
+    launches after `warmup` untimed ones: captured in a HIP graph and replayed
+    once between two events on `stream`, or launched eagerly.
+    `before_replay()` runs after the warm-up and the capture, before the
+    timed region."""
+    import torch
+
     with torch.cuda.stream(stream):
         for i in range(warmup):
-            xt.launch(module, *sets[i % nsets])
+            launch(i % n_sets)
     torch.cuda.synchronize()
-    mode = "eager"
-    graph = None
+    graph, mode = None, "eager"
     if use_graph:
         try:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
                 for i in range(steps):
-                    xt.launch(module, *sets[i % nsets])
-            graph.replay()
-            torch.cuda.synchronize()
+                    launch(i % n_sets)
             mode = "hip_graph"
-        except Exception as exc:  # capture unsupported: fall back to eager launches
+        except Exception as exc:  # capture unsupported: time eager launches
             print(f"[bench] graph capture failed ({exc}); timing eager launches", file=sys.stderr)
             graph = None
+    if before_replay is not None:
+        before_replay()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -213,28 +228,219 @@ def gpu_time(module, host, dtypes, steps: int, warmup: int, use_graph: bool):
             graph.replay()
         else:
             for i in range(steps):
-                xt.launch(module, *sets[i % nsets])
+                launch(i % n_sets)
         end.record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
-    out = sets[0]
-    return ms, mode, nsets, out
+    return start.elapsed_time(end) / steps, mode
+
+
+def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool) -> dict:
+    import torch
+
+    import xtile_amd as xt
+
+    module, host, dtypes, out, meta = cfg
+    plan = xt.plan(module)
+    print(f"[bench] {name}: {plan['kernel']}", file=sys.stderr, flush=True)
+    dev = torch.device("cuda:0")
+    set_bytes = sum(h.nbytes for h in host)
+    nsets = max(1, min(128, math.ceil(ROTATE_BYTES / set_bytes)))
+    first = [to_device(h, d, dev) for h, d in zip(host, dtypes)]
+    sets = [first] + [[t.clone() for t in first] for _ in range(nsets - 1)]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)
+
+    def launch(i):
+        xt.launch(module, *sets[i], stream=stream)
+
+    # eager reference of set 0; its output is cleared again just before the
+    # timed region, so only the timed launches can have rewritten it
+    with torch.cuda.stream(stream):
+        launch(0)
+    torch.cuda.synchronize()
+    reference = to_host(sets[0][out], dtypes[out])
+
+    def clear():
+        sets[0][out].zero_()
+        torch.cuda.synchronize()
+
+    ms, mode = timed(launch, nsets, steps, warmup, stream, use_graph, before_replay=clear)
+    replay = to_host(sets[0][out], dtypes[out])
+    replay_ok = bool(np.array_equal(replay.view(np.uint8), reference.view(np.uint8)))
+    del sets, first
+    torch.cuda.empty_cache()
+    sec = ms * 1e-3
+    value = plan["bytes"] / sec / 1e9 if meta["unit"] == "GB/s" else plan["flops"] / sec / 1e12
+    if meta["bound"] == "hbm":
+        achieved = plan["bytes"] / sec / 1e9
+        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic(name)}
+    else:
+        achieved = plan["flops"] / sec / 1e12
+        peak = MFMA_PEAK_TFLOPS[meta["dtype"]]
+        roof = {"bound": "mfma", "achieved": achieved, "peak": peak,
+                "unit": "TOP/s" if meta["dtype"] == "i8" else "TFLOP/s",
+                "frac": achieved / peak, "traffic": _traffic(name)}
+    if name == "c4":  # report against the MFMA peak as well
+        tf = plan["flops"] / sec / 1e12
+        roof["mfma_tflops"] = tf
+        roof["mfma_frac"] = tf / MFMA_PEAK_TFLOPS["f16"]
+    return {
+        "config": name,
+        "workload": meta["workload"],
+        "kernel": plan["kernel"],
+        "value": value,
+        "unit": meta["unit"],
+        "ms_per_step": ms,
+        "dtype": meta["dtype"],
+        "data": meta["data"],
+        "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets",
+        "roofline": roof,
+        "algo_bytes": plan["bytes"],
+        "algo_flops": plan["flops"],
+        "check": {"replay_equals_eager": replay_ok},
+        "_reference": reference,
+    }
+
+
+def _ceiling_lib():
+    lib = ctypes.CDLL(str(ROOT / "xtile_amd" / "lib" / "libxt_ceiling.so"))
+    lib.xt_ceiling_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.xt_ceiling_noop.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    lib.xt_ceiling_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]
+    for f in (lib.xt_ceiling_copy, lib.xt_ceiling_noop, lib.xt_ceiling_mfma):
+        f.restype = ctypes.c_int
+    return lib
+
+
+def ceilings() -> dict:
+    """What this GPU attains, measured by the kernels of include/xt_ceiling.h
+    in the same graph protocol as the tile programs: an MFMA issue loop per
+    element type on the configurations' own operand distributions, a 256 MiB
+    streaming copy (read + write, rotated over 2 GiB) and a copy and an empty
+    kernel at C1's size (the launch floor of a 12.6 MB program)."""
+    import torch
+
+    import xtile_amd  # noqa: F401  (torch first, then the HIP libraries)
+
+    lib = _ceiling_lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    h = stream.cuda_stream
+    out = {}
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(f"ceiling kernel launch failed (hipError {rc})")
+
+    # MFMA issue loop: 2 workgroups (8 waves) per CU, operands drawn like C3 / C5 / C6
+    wgs, iters = 512, 40000
+    rng = np.random.default_rng(11)
+    nvals = wgs * 256 * 16 * 16
+    operands = {
+        "f16": rng.uniform(-1, 1, nvals // 2).astype(np.float16).view(np.uint8),
+        "bf16": bf16_bits(_f32(rng.normal(0, 0.02, nvals // 2))).view(np.uint8),
+        "i8": rng.integers(-128, 128, nvals, dtype=np.int8).view(np.uint8),
+    }
+    res = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+    for kind, (name, ops) in enumerate(operands.items()):
+        buf = torch.from_numpy(ops).to(dev)
+        ms, _ = timed(lambda i: ok(lib.xt_ceiling_mfma(buf.data_ptr(), res.data_ptr(), wgs, iters, kind, h)),
+                      1, 4, 2, stream, True)
+        work = wgs * 4 * iters * 8 * 32768 * (2 if name == "i8" else 1)
+        out[f"mfma_{name}_T{'OP' if name == 'i8' else 'FLOP'}s"] = work / (ms * 1e-3) / 1e12
+    del buf, res
+    # HBM streaming copy, 256 MiB, four pairs rotated
+    n = 256 << 20
+    src = [torch.empty(n, dtype=torch.uint8, device=dev).random_() for _ in range(4)]
+    dst = [torch.empty_like(t) for t in src]
+    ms, _ = timed(lambda i: ok(lib.xt_ceiling_copy(src[i].data_ptr(), dst[i].data_ptr(), n, h)), 4, 100, 10,
+                  stream, True)
+    out["hbm_copy_GBs"] = 2 * n / (ms * 1e-3) / 1e9
+    del src, dst
+    # C1's size: 12,582,912 bytes moved per launch (a 6 MiB copy), rotated over 86 pairs like C1's inputs
+    n = 6 << 20
+    src = [torch.empty(n, dtype=torch.uint8, device=dev).random_() for _ in range(86)]
+    dst = [torch.empty_like(t) for t in src]
+    ms, _ = timed(lambda i: ok(lib.xt_ceiling_copy(src[i].data_ptr(), dst[i].data_ptr(), n, h)), 86, 2000, 100,
+                  stream, True)
+    out["c1_size_copy_us"] = ms * 1e3
+    out["c1_size_copy_GBs"] = 2 * n / (ms * 1e-3) / 1e9
+    del src, dst
+    ms, _ = timed(lambda i: ok(lib.xt_ceiling_noop(512, h)), 1, 2000, 100, stream, True)
+    out["empty_kernel_512wg_us"] = ms * 1e3
+    torch.cuda.empty_cache()
+    out["note"] = ("include/xt_ceiling.h kernels, HIP graph replay: MFMA loop of 8 independent 32x32 MFMAs per "
+                   "wave, 8 waves per CU, operands distributed like C3 (f16), C5 (bf16), C6 (i8); non-temporal "
+                   "float4 copy; empty kernel of 512 workgroups (C1's grid)")
+    return out
+
+
+def vendor() -> dict:
+    """hipBLASLt through torch on the GEMM configurations' shapes and types,
+    in the same process (eager launches between events, after warm-up)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    out = {}
+
+    def rate(fn, flops, n=50):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return flops / (s.elapsed_time(e) / n * 1e-3) / 1e12
+
+    a = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
+    b = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
+    f = 2 * 4096**3
+    out["hipblaslt_f16_4096_f16out_TFLOPs"] = rate(lambda: torch.mm(a, b), f)
+    try:
+        out["hipblaslt_f16_4096_f32out_TFLOPs"] = rate(lambda: torch.mm(a, b, out_dtype=torch.float32), f)
+    except Exception as exc:  # the out_dtype overload is missing on some builds
+        out["hipblaslt_f16_4096_f32out_TFLOPs"] = None
+        out["f32out_error"] = str(exc)[:200]
+    a = (torch.randn(4096, 4096, device=dev) * 0.02).bfloat16()
+    b = (torch.randn(4096, 11008, device=dev) * 0.02).bfloat16()
+    f = 2 * 4096 * 4096 * 11008
+    out["hipblaslt_bf16_c5_bf16out_TFLOPs"] = rate(lambda: torch.mm(a, b), f)
+    try:
+        out["hipblaslt_bf16_c5_f32out_TFLOPs"] = rate(lambda: torch.mm(a, b, out_dtype=torch.float32), f)
+    except Exception:
+        out["hipblaslt_bf16_c5_f32out_TFLOPs"] = None
+    del a, b
+    torch.cuda.empty_cache()
+    out["note"] = "torch.mm (hipBLASLt); f32out = torch.mm(..., out_dtype=torch.float32), the configurations' own types"
+    return out
+
+
+# -- CPU leg: the oracle as baseline and checker ---------------------------------------
 
 
 def cpu_time(text: str, host, seconds: float, threads: int):
-    """Seconds per run of the oracle over whole repetitions of `text`."""
+    """(seconds per run, repetitions, buffers after the first run) of the
+    oracle over whole repetitions of `text`."""
     import oracle
 
     bufs = [np.array(h, copy=True) for h in host]
+    first = None
     reps = 0
     t0 = time.perf_counter()
     while True:
         oracle.run(text, bufs, threads)
+        if first is None:
+            first = [np.array(b, copy=True) for b in bufs]
         reps += 1
         elapsed = time.perf_counter() - t0
         if elapsed >= seconds:
             break
-    return elapsed / reps, reps
+    return elapsed / reps, reps, first
 
 
 _GRID = re.compile(r"xt\.grid = array<i32: (\d+), (\d+), (\d+)>")
@@ -253,122 +459,66 @@ def grid_subset(text: str, fraction: float):
     return text[: m.start()] + f"xt.grid = array<i32: {g[0]}, {g[1]}, {g[2]}>" + text[m.end():], share
 
 
-def attainable():
-    """What a plain device copy and the vendor GEMM reach on this box: the
-    practical ceilings beside the published peaks."""
-    import torch
-
-    dev = torch.device("cuda:0")
-    out = {}
-    n = (256 << 20) // 4
-    src = [torch.rand(n, device=dev) for _ in range(4)]
-    dst = [torch.empty_like(t) for t in src]
-    for i in range(8):
-        dst[i % 4].copy_(src[i % 4])
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(40):
-        dst[i % 4].copy_(src[i % 4])
-    end.record()
-    torch.cuda.synchronize()
-    out["hbm_copy_GBs"] = 40 * 2 * n * 4 / (start.elapsed_time(end) * 1e-3) / 1e9
-    del src, dst
-    a = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
-    b = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
-    for _ in range(10):
-        torch.matmul(a, b)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(200):
-        torch.matmul(a, b)
-    end.record()
-    torch.cuda.synchronize()
-    out["torch_matmul_f16_4096_TFLOPs"] = 200 * 2 * 4096**3 / (start.elapsed_time(end) * 1e-3) / 1e12
-    out["note"] = ("device copy of 256 MiB (read + write bytes) and torch.matmul (hipBLASLt) "
-                   "f16 4096^3 with f16 output, same process")
-    return out
-
-
-def measure(name: str, steps: int, warmup: int, cpu_seconds: float, use_graph: bool) -> dict:
-    import xtile_amd as xt
-
-    module, host, dtypes, meta = make_config(name)
-    plan = xt.plan(module)
-    print(f"[bench] {name}: {plan['kernel']}", file=sys.stderr, flush=True)
-    ms, mode, nsets, _ = gpu_time(module, host, dtypes, steps, warmup, use_graph)
-    sec = ms * 1e-3
-    if meta["unit"] == "GB/s":
-        value = plan["bytes"] / sec / 1e9
+def compare(kind: str, bar: float, got: np.ndarray, want: np.ndarray, dtype: str) -> tuple[bool, float]:
+    if kind == "exact":
+        return bool(np.array_equal(got.view(np.uint8), want.view(np.uint8))), 0.0
+    if dtype == "bf16":
+        got, want = (np.asarray(x, np.uint32) << 16 for x in (got, want))
+        got, want = got.view(np.float32), want.view(np.float32)
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    if kind == "max_rel":
+        err = float(np.max(np.abs(g - w) / np.maximum(np.abs(w), np.finfo(np.float32).tiny)))
+    elif kind == "max_abs":
+        err = float(np.max(np.abs(g - w)))
     else:
-        value = plan["flops"] / sec / 1e12
-    if meta["bound"] == "hbm":
-        achieved = plan["bytes"] / sec / 1e9
-        roof = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic(name)}
-    else:
-        achieved = plan["flops"] / sec / 1e12
-        peak = MFMA_PEAK_TFLOPS[meta["dtype"]]
-        roof = {"bound": "mfma", "achieved": achieved, "peak": peak,
-                "unit": "TOP/s" if meta["dtype"] == "i8" else "TFLOP/s",
-                "frac": achieved / peak, "traffic": _traffic(name)}
-    if name == "c4":  # report against the MFMA peak as well
-        tf = plan["flops"] / sec / 1e12
-        roof["mfma_tflops"] = tf
-        roof["mfma_frac"] = tf / MFMA_PEAK_TFLOPS["f16"]
-    result = {
-        "config": name,
-        "workload": meta["workload"],
-        "kernel": plan["kernel"],
-        "value": value,
+        err = float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-300))
+    return err <= bar, err
+
+
+def cpu_leg(name: str, cfg, result: dict, cpu_seconds: float) -> None:
+    module, host, dtypes, out, meta = cfg
+    threads = int(os.environ.get("XT_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    text = str(module)
+    work = result["algo_bytes"] if meta["unit"] == "GB/s" else result["algo_flops"]
+    scale = 1e9 if meta["unit"] == "GB/s" else 1e12
+    print(f"[bench] {name}: oracle on {threads} threads", file=sys.stderr, flush=True)
+    cpu_s, reps, first = cpu_time(text, host, cpu_seconds, threads)
+    kind, bar = meta["check"]
+    ok, err = compare(kind, bar, result["_reference"], first[out], dtypes[out])
+    result["check"].update({"vs_oracle": kind, "bar": bar, "error": err, "ok": ok})
+    # one thread, on a sub-grid sized to about 2 s
+    sub, share = grid_subset(text, min(1.0, 2.0 / max(cpu_s * threads, 1e-9)))
+    one_s, one_reps, _ = cpu_time(sub, host, 0.5, 1)
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    result["cpu_baseline"] = {
+        "value": work / cpu_s / scale,
         "unit": meta["unit"],
-        "ms_per_step": ms,
-        "dtype": meta["dtype"],
-        "data": meta["data"],
-        "timing": f"{mode}, {steps} launches, {nsets} rotating input sets",
-        "roofline": roof,
-        "algo_bytes": plan["bytes"],
-        "algo_flops": plan["flops"],
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle/xt_oracle.c over the full workload, {reps} repetition(s), "
+                  f"{cpu_s * 1e3:.1f} ms each, {threads} OpenMP threads (nproc={os.cpu_count()}, "
+                  f"affinity={affinity})",
+        "value_1thread": work * share / one_s / scale,
+        "sample_1thread": f"{share:.4f} of the Blocks (a leading sub-grid), {one_reps} repetition(s), "
+                          f"{one_s * 1e3:.1f} ms each, 1 thread",
     }
-    if cpu_seconds > 0:
-        threads = int(os.environ.get("XT_CPU_THREADS", min(16, os.cpu_count() or 1)))
-        text = str(module)
-        work = plan["bytes"] if meta["unit"] == "GB/s" else plan["flops"]
-        scale = 1e9 if meta["unit"] == "GB/s" else 1e12
-        cpu_s, reps = cpu_time(text, host, cpu_seconds, threads)
-        # one thread, on a sub-grid sized to about 2 s
-        sub, share = grid_subset(text, min(1.0, 2.0 / max(cpu_s * threads, 1e-9)))
-        one_s, one_reps = cpu_time(sub, host, 0.5, 1)
-        try:
-            affinity = len(os.sched_getaffinity(0))
-        except AttributeError:
-            affinity = None
-        result["cpu_baseline"] = {
-            "value": work / cpu_s / scale,
-            "unit": meta["unit"],
-            "cores": threads,
-            "kind": "port",
-            "sample": f"oracle/xt_oracle.c over the full workload, {reps} repetition(s), "
-                      f"{cpu_s * 1e3:.1f} ms each, {threads} OpenMP threads (nproc={os.cpu_count()}, "
-                      f"affinity={affinity})",
-            "value_1thread": work * share / one_s / scale,
-            "sample_1thread": f"{share:.4f} of the Blocks (a leading sub-grid), {one_reps} repetition(s), "
-                              f"{one_s * 1e3:.1f} ms each, 1 thread",
-        }
-    return result
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 2000 launches keep every timed region >= 7 ms (C1) and the clock settled:
-    # 200-launch bursts read up to 10% slower and vary run to run with the
-    # clock's ramp
+    # 2000 launches keep every timed region >= 7 ms (C1) and the clock settled
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", default="all", help="all, or one of c1..c7")
-    ap.add_argument("--cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--config", default="all", help="all, or a comma-separated list of c1..c7")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0,
+                    help="oracle time per configuration; 0 skips the CPU leg (and the oracle check)")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the ceiling and vendor legs")
     ap.add_argument(
         "--copy-probe",
         type=float,
@@ -396,11 +546,25 @@ def main(argv=None) -> int:
             file=sys.stderr,
         )
         return 2
-    names = ["c1", "c2", "c3", "c4", "c5", "c6", "c7"] if args.config == "all" else [args.config]
+    names = ALL if args.config == "all" else args.config.split(",")
     headline = "c2" if "c2" in names else names[0]
-    results = {n: measure(n, args.steps, args.warmup, args.cpu_seconds, not args.no_graph) for n in names}
+    cfgs = {n: make_config(n) for n in names}
+    print("[bench] inputs generated", file=sys.stderr, flush=True)
+    ceil = None if args.no_ceilings else ceilings()
+    results = {n: gpu_leg(n, cfgs[n], args.steps, args.warmup, not args.no_graph) for n in names}
+    vend = None if args.no_ceilings or not ({"c3", "c5"} & set(names)) else vendor()
+    if args.cpu_seconds > 0:
+        for n in names:
+            cpu_leg(n, cfgs[n], results[n], args.cpu_seconds)
+    failed = [n for n in names if not results[n]["check"]["replay_equals_eager"]
+              or not results[n]["check"].get("ok", True)]
+    for r in results.values():
+        r.pop("_reference")
+    if failed:
+        for n in failed:
+            print(f"[bench] {n}: output check failed: {json.dumps(results[n]['check'])}", file=sys.stderr)
+        return 1
     h = results[headline]
-    ceilings = attainable() if args.config == "all" else None
     line = {
         "metric": METRIC,
         "value": h["value"],
@@ -417,7 +581,9 @@ def main(argv=None) -> int:
         "config": {"workload": h["workload"], "kernel": h["kernel"], "timing": h["timing"]},
         "roofline": h["roofline"],
         "cpu_baseline": h.get("cpu_baseline"),
-        "attainable": ceilings,
+        "check": h["check"],
+        "attainable": ceil,
+        "vendor": vend,
         "per_config": [results[n] for n in names],
     }
     print(json.dumps(line), flush=True)

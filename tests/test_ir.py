@@ -14,6 +14,7 @@ import shutil
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 import xtile_amd as xt
@@ -239,6 +240,36 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_xtile.SIGNATURES)
+
+
+def test_ceiling_library_exports_every_declared_symbol():
+    """libxt_ceiling.so (bench.py's measurement kernels) exports what
+    include/xt_ceiling.h declares, and refuses bad arguments on the host."""
+    header = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "xt_ceiling.h").read_text(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(xt_[a-z_]+)\s*\(", header)))
+    assert declared == ["xt_ceiling_copy", "xt_ceiling_mfma", "xt_ceiling_noop"]
+    import bench
+
+    lib = bench._ceiling_lib()
+    for name in declared:
+        assert hasattr(lib, name), name
+    # misaligned sizes, empty grids and unknown kinds are refused before any launch
+    assert lib.xt_ceiling_copy(0x1000, 0x2000, 15, None) != 0
+    assert lib.xt_ceiling_noop(0, None) != 0
+    assert lib.xt_ceiling_mfma(0x1000, 0x2000, 1, 1, 7, None) != 0
+
+
+def test_bench_checks_tell_results_apart():
+    import bench
+
+    x = np.array([1.0, 2.0, 3.0], np.float32)
+    assert bench.compare("exact", 0.0, x, x.copy(), "f32")[0]
+    assert not bench.compare("exact", 0.0, x, x + np.float32(1e-7), "f32")[0]
+    assert bench.compare("max_rel", 1e-5, x * np.float32(1 + 5e-6), x, "f32")[0]
+    assert not bench.compare("max_rel", 1e-5, x * np.float32(1 + 5e-5), x, "f32")[0]
+    assert not bench.compare("frob", 1e-3, x[::-1].copy(), x, "f32")[0]
+    b = bench.bf16_bits(x)
+    assert bench.compare("frob", 1e-3, b, b.copy(), "bf16")[0]
 
 
 def test_version_string():

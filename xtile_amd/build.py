@@ -3,7 +3,10 @@
 Produces, under ``xtile_amd/lib/``:
   * ``libxtile_amd.so`` - the C ABI of ``include/xtile_amd.h``: xt parser,
     verifier, passes, launch planner and the gfx950 HIP kernels;
-  * ``xt-opt``          - the command-line driver (host code only).
+  * ``xt-opt``          - the command-line driver (host code only);
+  * ``libxt_ceiling.so`` - the measurement kernels of ``include/xt_ceiling.h``
+    (a copy, an empty kernel and an MFMA loop) that bench.py times for its
+    ceilings; the tile programs never use it.
 
 Usage: ``python xtile_amd/build.py`` (or ``__graft_entry__.build()``); it runs
 without importing the package, whose __init__ needs the library it builds.
@@ -80,6 +83,8 @@ def build(verbose: bool = False) -> Path:
         obj = OBJ / (Path(src).stem + ".o")
         kern_objs.append(obj)
         jobs.append([HIPCC, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+    ceil_obj = OBJ / "ceiling.o"
+    jobs.append([HIPCC, *HIP_FLAGS, "-c", str(CSRC / "ceiling.hip"), "-o", str(ceil_obj)])
     xt_opt_obj = OBJ / "xt_opt.o"
     jobs.append([CXX, *HOST_FLAGS, "-c", str(CSRC / "xt_opt.cpp"), "-o", str(xt_opt_obj)])
 
@@ -109,6 +114,9 @@ def build(verbose: bool = False) -> Path:
         ]
     )
     os.replace(tmp, lib)
+    ceil_tmp = LIB / "libxt_ceiling.so.tmp"
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", str(ceil_obj), "-o", str(ceil_tmp)])
+    os.replace(ceil_tmp, LIB / "libxt_ceiling.so")
     _run([CXX, *map(str, host_objs), str(xt_opt_obj), "-o", str(LIB / "xt-opt")])
     return lib
 
