@@ -194,18 +194,16 @@ def to_host(t, dtype: str) -> np.ndarray:
     return t.numpy()
 
 
-def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool, before_replay=None):
+def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool, before_replay=None,
+          precondition=None):
     """Average ms per launch of `launch(i)` (i = input set) over `steps`
-    launches after `warmup` untimed ones: captured in a HIP graph and replayed
-    once between two events on `stream`, or launched eagerly.
-    `before_replay()` runs after the warm-up and the capture, before the
-    timed region."""
+    launches.  The launches are captured in a HIP graph first (capture runs
+    nothing); then, on `stream` and with no host wait in between: the
+    optional `precondition()` work, `warmup` untimed eager launches,
+    `before_replay()`, and the graph replay between two events.  Without a
+    graph the timed launches are eager."""
     import torch
 
-    with torch.cuda.stream(stream):
-        for i in range(warmup):
-            launch(i % n_sets)
-    torch.cuda.synchronize()
     graph, mode = None, "eager"
     if use_graph:
         try:
@@ -217,12 +215,16 @@ def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool,
         except Exception as exc:  # capture unsupported: time eager launches
             print(f"[bench] graph capture failed ({exc}); timing eager launches", file=sys.stderr)
             graph = None
-    if before_replay is not None:
-        before_replay()
+    torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     with torch.cuda.stream(stream):
+        if precondition is not None:
+            precondition()
+        for i in range(warmup):
+            launch(i % n_sets)
+        if before_replay is not None:
+            before_replay()
         start.record(stream)
         if graph is not None:
             graph.replay()
@@ -234,7 +236,71 @@ def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool,
     return start.elapsed_time(end) / steps, mode
 
 
-def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool) -> dict:
+class Preconditioner:
+    """Brings the GPU to the clock it sustains under a configuration's kind of
+    load before that configuration is timed.  The power manager ramps the
+    clock over the first ~30 ms of matrix-core load, and restarts the ramp
+    after even 50 ms of idle: the first 20 launches of C3 take 170-180 us,
+    the 200th 142 us.  Short timed runs (the driver's 20 steps) would
+    otherwise measure the ramp.  The work is one of the ceiling kernels of
+    include/xt_ceiling.h (never the configuration's own kernel), enqueued on
+    the timing stream right before the warm-up launches."""
+
+    MS = 100.0
+
+    def __init__(self):
+        import torch
+
+        self.lib = _ceiling_lib()
+        self.dev = torch.device("cuda:0")
+        self.wgs = 512
+        self.ops = {}
+        self.res = torch.empty(self.wgs * 256, dtype=torch.float32, device=self.dev)
+        n = 256 << 20
+        self.copy_bytes = n
+        self.src = torch.empty(n, dtype=torch.uint8, device=self.dev).random_()
+        self.dst = torch.empty_like(self.src)
+
+    def operands(self, kind: str):
+        import torch
+
+        if kind not in self.ops:
+            rng = np.random.default_rng(11)
+            nvals = self.wgs * 256 * 16 * 16
+            if kind == "f16":
+                h = rng.uniform(-1, 1, nvals // 2).astype(np.float16).view(np.uint8)
+            elif kind == "bf16":
+                h = bf16_bits(_f32(rng.normal(0, 0.02, nvals // 2))).view(np.uint8)
+            else:
+                h = rng.integers(-128, 128, nvals, dtype=np.int8).view(np.uint8)
+            self.ops[kind] = torch.from_numpy(h).to(self.dev)
+        return self.ops[kind]
+
+    def mfma(self, kind: str, iters: int, stream_handle):
+        k = {"f16": 0, "bf16": 1, "i8": 2}[kind]
+        rc = self.lib.xt_ceiling_mfma(self.operands(kind).data_ptr(), self.res.data_ptr(), self.wgs, iters, k,
+                                      stream_handle)
+        if rc:
+            raise RuntimeError(f"ceiling MFMA launch failed (hipError {rc})")
+
+    def copy(self, src, dst, nbytes, stream_handle):
+        rc = self.lib.xt_ceiling_copy(src, dst, nbytes, stream_handle)
+        if rc:
+            raise RuntimeError(f"ceiling copy launch failed (hipError {rc})")
+
+    def run(self, bound: str, dtype: str, stream) -> None:
+        """About MS milliseconds of MFMA loop (matrix-bound configurations) or
+        streaming copy (bandwidth-bound ones) on `stream`."""
+        h = stream.cuda_stream
+        if bound == "mfma":
+            for _ in range(int(self.MS / 1.4)):  # one 4000-round launch is about 1.4 ms
+                self.mfma(dtype, 4000, h)
+        else:
+            for _ in range(int(self.MS / 0.09)):  # one 256 MiB copy is about 90 us
+                self.copy(self.src.data_ptr(), self.dst.data_ptr(), self.copy_bytes, h)
+
+
+def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool, pre: "Preconditioner | None") -> dict:
     import torch
 
     import xtile_amd as xt
@@ -262,9 +328,12 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool) -> dict:
 
     def clear():
         sets[0][out].zero_()
-        torch.cuda.synchronize()
 
-    ms, mode = timed(launch, nsets, steps, warmup, stream, use_graph, before_replay=clear)
+    def precondition():
+        pre.run(meta["bound"], meta["dtype"], stream)
+
+    ms, mode = timed(launch, nsets, steps, warmup, stream, use_graph, before_replay=clear,
+                     precondition=precondition if pre is not None else None)
     replay = to_host(sets[0][out], dtypes[out])
     replay_ok = bool(np.array_equal(replay.view(np.uint8), reference.view(np.uint8)))
     del sets, first
@@ -294,7 +363,10 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool) -> dict:
         "ms_per_step": ms,
         "dtype": meta["dtype"],
         "data": meta["data"],
-        "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets",
+        "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets"
+                  + (f", after {Preconditioner.MS:.0f} ms of device pre-conditioning ("
+                     + ("MFMA loop" if meta["bound"] == "mfma" else "streaming copy")
+                     + ", include/xt_ceiling.h)" if pre is not None else ""),
         "roofline": roof,
         "algo_bytes": plan["bytes"],
         "algo_flops": plan["flops"],
@@ -314,66 +386,54 @@ def _ceiling_lib():
     return lib
 
 
-def ceilings() -> dict:
+def ceilings(pre: Preconditioner) -> dict:
     """What this GPU attains, measured by the kernels of include/xt_ceiling.h
     in the same graph protocol as the tile programs: an MFMA issue loop per
     element type on the configurations' own operand distributions, a 256 MiB
     streaming copy (read + write, rotated over 2 GiB) and a copy and an empty
-    kernel at C1's size (the launch floor of a 12.6 MB program)."""
+    kernel at C1's size (the launch floor of a 12.6 MB program).  Each is
+    preceded by the same pre-conditioning as the configurations."""
     import torch
 
-    import xtile_amd  # noqa: F401  (torch first, then the HIP libraries)
-
-    lib = _ceiling_lib()
-    dev = torch.device("cuda:0")
+    dev = pre.dev
     stream = torch.cuda.Stream(device=dev)
     h = stream.cuda_stream
     out = {}
-
-    def ok(rc):
-        if rc:
-            raise RuntimeError(f"ceiling kernel launch failed (hipError {rc})")
-
-    # MFMA issue loop: 2 workgroups (8 waves) per CU, operands drawn like C3 / C5 / C6
-    wgs, iters = 512, 40000
-    rng = np.random.default_rng(11)
-    nvals = wgs * 256 * 16 * 16
-    operands = {
-        "f16": rng.uniform(-1, 1, nvals // 2).astype(np.float16).view(np.uint8),
-        "bf16": bf16_bits(_f32(rng.normal(0, 0.02, nvals // 2))).view(np.uint8),
-        "i8": rng.integers(-128, 128, nvals, dtype=np.int8).view(np.uint8),
-    }
-    res = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
-    for kind, (name, ops) in enumerate(operands.items()):
-        buf = torch.from_numpy(ops).to(dev)
-        ms, _ = timed(lambda i: ok(lib.xt_ceiling_mfma(buf.data_ptr(), res.data_ptr(), wgs, iters, kind, h)),
-                      1, 4, 2, stream, True)
-        work = wgs * 4 * iters * 8 * 32768 * (2 if name == "i8" else 1)
+    iters = 40000
+    for name in ("f16", "bf16", "i8"):
+        ms, _ = timed(lambda i: pre.mfma(name, iters, h), 1, 4, 1, stream, True,
+                      precondition=lambda: pre.run("mfma", name, stream))
+        work = pre.wgs * 4 * iters * 8 * 32768 * (2 if name == "i8" else 1)
         out[f"mfma_{name}_T{'OP' if name == 'i8' else 'FLOP'}s"] = work / (ms * 1e-3) / 1e12
-    del buf, res
     # HBM streaming copy, 256 MiB, four pairs rotated
     n = 256 << 20
     src = [torch.empty(n, dtype=torch.uint8, device=dev).random_() for _ in range(4)]
     dst = [torch.empty_like(t) for t in src]
-    ms, _ = timed(lambda i: ok(lib.xt_ceiling_copy(src[i].data_ptr(), dst[i].data_ptr(), n, h)), 4, 100, 10,
-                  stream, True)
+    ms, _ = timed(lambda i: pre.copy(src[i].data_ptr(), dst[i].data_ptr(), n, h), 4, 100, 10, stream, True,
+                  precondition=lambda: pre.run("hbm", "f32", stream))
     out["hbm_copy_GBs"] = 2 * n / (ms * 1e-3) / 1e9
     del src, dst
     # C1's size: 12,582,912 bytes moved per launch (a 6 MiB copy), rotated over 86 pairs like C1's inputs
     n = 6 << 20
     src = [torch.empty(n, dtype=torch.uint8, device=dev).random_() for _ in range(86)]
     dst = [torch.empty_like(t) for t in src]
-    ms, _ = timed(lambda i: ok(lib.xt_ceiling_copy(src[i].data_ptr(), dst[i].data_ptr(), n, h)), 86, 2000, 100,
-                  stream, True)
+    ms, _ = timed(lambda i: pre.copy(src[i].data_ptr(), dst[i].data_ptr(), n, h), 86, 2000, 100, stream, True,
+                  precondition=lambda: pre.run("hbm", "f32", stream))
     out["c1_size_copy_us"] = ms * 1e3
     out["c1_size_copy_GBs"] = 2 * n / (ms * 1e-3) / 1e9
     del src, dst
-    ms, _ = timed(lambda i: ok(lib.xt_ceiling_noop(512, h)), 1, 2000, 100, stream, True)
+
+    def noop(i):
+        rc = pre.lib.xt_ceiling_noop(512, h)
+        if rc:
+            raise RuntimeError(f"ceiling launch failed (hipError {rc})")
+
+    ms, _ = timed(noop, 1, 2000, 100, stream, True)
     out["empty_kernel_512wg_us"] = ms * 1e3
     torch.cuda.empty_cache()
     out["note"] = ("include/xt_ceiling.h kernels, HIP graph replay: MFMA loop of 8 independent 32x32 MFMAs per "
                    "wave, 8 waves per CU, operands distributed like C3 (f16), C5 (bf16), C6 (i8); non-temporal "
-                   "float4 copy; empty kernel of 512 workgroups (C1's grid)")
+                   "float4 copy, 512 workgroups walking the array; empty kernel of 512 workgroups (C1's grid)")
     return out
 
 
@@ -519,6 +579,8 @@ def main(argv=None) -> int:
                     help="oracle time per configuration; 0 skips the CPU leg (and the oracle check)")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the ceiling and vendor legs")
+    ap.add_argument("--no-precondition", action="store_true",
+                    help="time from whatever clock the GPU is at (no pre-conditioning; no ceilings)")
     ap.add_argument(
         "--copy-probe",
         type=float,
@@ -550,8 +612,10 @@ def main(argv=None) -> int:
     headline = "c2" if "c2" in names else names[0]
     cfgs = {n: make_config(n) for n in names}
     print("[bench] inputs generated", file=sys.stderr, flush=True)
-    ceil = None if args.no_ceilings else ceilings()
-    results = {n: gpu_leg(n, cfgs[n], args.steps, args.warmup, not args.no_graph) for n in names}
+    pre = None if args.no_precondition else Preconditioner()
+    ceil = None if args.no_ceilings or pre is None else ceilings(pre)
+    results = {n: gpu_leg(n, cfgs[n], args.steps, args.warmup, not args.no_graph, pre) for n in names}
+    del pre
     vend = None if args.no_ceilings or not ({"c3", "c5"} & set(names)) else vendor()
     if args.cpu_seconds > 0:
         for n in names:

@@ -18,8 +18,9 @@ extern "C" {
 #endif
 
 /* Streaming copy of `bytes` (a multiple of 16, both pointers 16-byte
- * aligned): 16-byte non-temporal loads and stores, four per thread, the four
- * loads issued before the first store.  Moves 2 * bytes through HBM. */
+ * aligned): at most 512 workgroups of 256 threads walk the array, each pass
+ * issuing four 16-byte non-temporal loads per thread before the first
+ * store.  Moves 2 * bytes through HBM. */
 int xt_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream);
 
 /* A kernel of `workgroups` 256-thread workgroups that does nothing: the

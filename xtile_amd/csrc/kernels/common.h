@@ -44,6 +44,52 @@ inline Magic udiv_magic(unsigned d) {
   return d == 1 ? Magic{0u, ~0u} : Magic{unsigned(((1ull << 32) + d - 1) / d), 0u};
 }
 
+// Exact n / d for 0 <= n < 2^31 and 1 <= d < 2^31 with one 64-bit multiply:
+// with l = ceil(log2 d), s = 31 + l and m = ceil(2^s / d) <= 2^32, m*d = 2^s + e
+// with 0 <= e < d <= 2^l, so n*m / 2^s = n/d + n*e / (d 2^s), and n*e < 2^s
+// keeps the excess below 1/d: the floor is exact.  Replaces the ~30-instruction
+// integer division sequence in kernel prologues.
+struct Div31 {
+  unsigned long long m;
+  unsigned s;
+  __host__ __device__ __forceinline__ unsigned operator()(unsigned n) const {
+    return static_cast<unsigned>((n * m) >> s);
+  }
+};
+
+inline Div31 div31(unsigned d) {
+  unsigned l = 0;
+  while ((1ull << l) < d) ++l;
+  const unsigned s = 31 + l;
+  return Div31{((1ull << s) + d - 1) / d, s};
+}
+
+// Linear Block index -> (x, y, z) for a grid of gx x gy x gz Blocks, either in
+// the reference's z -> y -> x order (x fastest) or, when y_fastest, with y
+// fastest (Blocks are independent, so any order gives the same result).
+struct BlockDecode {
+  Div31 dx, dy;
+  int gx, gy;
+  int y_fastest;
+  __device__ __forceinline__ void operator()(int b, int& x, int& y, int& z) const {
+    if (y_fastest) {
+      const unsigned t = dy(static_cast<unsigned>(b));
+      y = b - static_cast<int>(t) * gy;
+      z = static_cast<int>(dx(t));
+      x = static_cast<int>(t) - z * gx;
+    } else {
+      const unsigned t = dx(static_cast<unsigned>(b));
+      x = b - static_cast<int>(t) * gx;
+      z = static_cast<int>(dy(t));
+      y = static_cast<int>(t) - z * gy;
+    }
+  }
+};
+
+inline BlockDecode block_decode(int gx, int gy, bool y_fastest) {
+  return BlockDecode{div31(static_cast<unsigned>(gx)), div31(static_cast<unsigned>(gy)), gx, gy, y_fastest ? 1 : 0};
+}
+
 // Block id (x, y, z) of the grid point handled by linear index `b`, in the
 // reference's z -> y -> x order (x fastest).
 __device__ __forceinline__ void decode_block(int b, int gx, int gy, int& x, int& y, int& z) {

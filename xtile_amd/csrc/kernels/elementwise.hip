@@ -22,9 +22,8 @@ struct EwArgs {
   TileOff ta, tb, tc;
   long long lda, ldb, ldc;
   int rows, cols;
-  int gx, gy;
-  int y_fastest;  // linearise blocks y-fastest (consecutive groups are adjacent in memory)
-  int cv_shift;   // log2(cols / VW) when that is a power of two, else -1
+  BlockDecode grid;  // y fastest when that makes neighbouring workgroups neighbours in memory
+  int cv_shift;      // log2(cols / VW) when that is a power of two, else -1
 };
 
 template <int OP>
@@ -41,20 +40,6 @@ __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_lo
 template <typename T>
 __device__ __forceinline__ void st_nt(T v, T* p) { __builtin_nontemporal_store(v, p); }
 
-// Blocks are independent (any execution order gives the same result), so the
-// launcher may pick the linearisation whose neighbouring workgroups touch
-// neighbouring memory.
-__device__ __forceinline__ void ew_block(const EwArgs& p, int& x, int& y, int& z) {
-  if (p.y_fastest) {
-    y = blockIdx.x % p.gy;
-    const int t = blockIdx.x / p.gy;
-    x = t % p.gx;
-    z = t / p.gx;
-  } else {
-    decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
-  }
-}
-
 // Each thread handles U vectors per step; U is the smallest of 1, 2, 4 that
 // covers the tile in one step (4 when it takes several).  All U loads are
 // issued before any is consumed; indices past the end of the tile (only in a
@@ -64,7 +49,7 @@ __device__ __forceinline__ void ew_block(const EwArgs& p, int& x, int& y, int& z
 template <int OP, int VW, int U, bool POW2>
 __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
   int x, y, z;
-  ew_block(p, x, y, z);
+  p.grid(blockIdx.x, x, y, z);
   const float* A = p.a + p.ta.at(x, y, z);
   const float* B = p.b + p.tb.at(x, y, z);
   float* C = p.c + p.tc.at(x, y, z);
@@ -122,7 +107,7 @@ struct SoftmaxArgs {
   TileOff tx, ty;
   long long ldx, ldy;
   int rows, cols;
-  int gx, gy;
+  BlockDecode grid;
   int tpr;  // threads per row (power of two, <= 256)
 };
 
@@ -164,7 +149,7 @@ template <int NV, int VW, int TPR, bool EXACT>
 __global__ __launch_bounds__(256) void row_softmax_kernel(SoftmaxArgs p) {
   __shared__ float lds[8];
   int x, y, z;
-  decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  p.grid(blockIdx.x, x, y, z);
   const float* X = p.x + p.tx.at(x, y, z);
   float* Y = p.y + p.ty.at(x, y, z);
   constexpr int tpr = TPR;
@@ -241,7 +226,7 @@ __global__ __launch_bounds__(TPB) void row_softmax_wide_kernel(SoftmaxArgs p) {
   constexpr int NW = TPB / 64;
   __shared__ float lds[2][NW];
   int x, y, z;
-  decode_block(blockIdx.x, p.gx, p.gy, x, y, z);
+  p.grid(blockIdx.x, x, y, z);
   const float* X = p.x + p.tx.at(x, y, z);
   float* Y = p.y + p.ty.at(x, y, z);
   const int w = threadIdx.x >> 6;
@@ -308,8 +293,6 @@ hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s,
   a.ldc = p.c.ld;
   a.rows = static_cast<int>(p.c.rows);
   a.cols = static_cast<int>(p.c.cols);
-  a.gx = p.grid[0];
-  a.gy = p.grid[1];
   if (p.a.rows != p.c.rows || p.b.rows != p.c.rows || p.a.cols != p.c.cols ||
       p.b.cols != p.c.cols) {
     why = "elementwise operand tiles differ in shape";
@@ -328,7 +311,7 @@ hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s,
   const int u = nvec <= 256 ? 1 : nvec <= 512 ? 2 : 4;
   const long long sx = p.c.addr.sx < 0 ? -p.c.addr.sx : p.c.addr.sx;
   const long long sy = p.c.addr.sy < 0 ? -p.c.addr.sy : p.c.addr.sy;
-  a.y_fastest = (p.grid[1] > 1 && (sx == 0 || (sy != 0 && sy < sx))) ? 1 : 0;
+  a.grid = block_decode(p.grid[0], p.grid[1], p.grid[1] > 1 && (sx == 0 || (sy != 0 && sy < sx)));
   const long long blocks = grid_blocks(p);
   if (!grid_fits(blocks, 256)) {
     why = "elementwise grid of " + std::to_string(blocks) + " Blocks exceeds one launch (2^24 workgroups of 256)";
@@ -374,8 +357,7 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
   a.ldy = p.c.ld;
   a.rows = static_cast<int>(p.a.rows);
   a.cols = static_cast<int>(p.a.cols);
-  a.gx = p.grid[0];
-  a.gy = p.grid[1];
+  a.grid = block_decode(p.grid[0], p.grid[1], false);
   if (p.c.rows != p.a.rows || p.c.cols != p.a.cols) {
     why = "softmax input and output tiles differ in shape";
     return hipErrorInvalidValue;
