@@ -198,10 +198,10 @@ def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool,
           precondition=None):
     """Average ms per launch of `launch(i)` (i = input set) over `steps`
     launches.  The launches are captured in a HIP graph first (capture runs
-    nothing); then, on `stream` and with no host wait in between: the
-    optional `precondition()` work, `warmup` untimed eager launches,
-    `before_replay()`, and the graph replay between two events.  Without a
-    graph the timed launches are eager."""
+    nothing); then, on `stream`: the optional `precondition()` work, `warmup`
+    untimed eager launches and `before_replay()`; a device synchronisation;
+    the graph replay between two events; a device synchronisation.  Without
+    a graph the timed launches are eager."""
     import torch
 
     graph, mode = None, "eager"
@@ -225,6 +225,8 @@ def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool,
             launch(i % n_sets)
         if before_replay is not None:
             before_replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
         start.record(stream)
         if graph is not None:
             graph.replay()

@@ -38,7 +38,6 @@
 // channel and an f32 result; else the generic kernel (conv_general.hip),
 // which takes every tile shape the planner accepts.
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -454,6 +453,9 @@ __global__ __launch_bounds__(WG, 1) void conv2d_kernel(ConvArgs p) {
 //     M tiles at a time against one N tile and stores them straight from the
 //     accumulators (each store instruction writes two 128-byte pixel runs).
 constexpr int BWG = 512;
+#ifndef XT_BAND_MAX_MI
+#define XT_BAND_MAX_MI 4  // M tiles per pass of a wave (1-4)
+#endif
 
 struct BandArgs {
   const unsigned char* src;
@@ -667,7 +669,7 @@ __device__ __forceinline__ void band_wave(const BandArgs& p, const band_lds_t* F
   int q0 = qbeg + m0 * 32;
   const int tstride = mstep * 32;
   while (n > 0) {
-    const int c = min(n, 4);
+    const int c = min(n, XT_BAND_MAX_MI);
     switch (c) {
       case 1: band_tiles<1, NT, CS, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
       case 2: band_tiles<2, NT, CS, ELEM>(p, Fs, Hs, orc, q0, tstride, qend, j, lane); break;
@@ -742,32 +744,22 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
 
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
 
-// Raises the kernel's dynamic-LDS limit once (a host-side attribute, so later
-// launches - including ones recorded into a HIP graph - only enqueue work).
 template <int NT, bool BF16>
 hipError_t launch_conv_t(const ConvArgs& a, dim3 grid, size_t lds, hipStream_t s) {
-  static std::atomic<int> configured{0};
   auto fn = conv2d_kernel<NT, BF16>;
-  if (static_cast<int>(lds) > configured.load()) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured.store(static_cast<int>(lds));
-  }
+  if (lds > size_t(kMaxLds)) return hipErrorInvalidValue;
+  hipError_t e = allow_full_lds(reinterpret_cast<const void*>(fn));
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(fn, grid, dim3(WG), lds, s, a);
   return hipGetLastError();
 }
 
 template <int NT, int CS, int ELEM>
 hipError_t launch_band_t(const BandArgs& a, int bands, size_t lds, hipStream_t s) {
-  static std::atomic<int> configured{0};
   auto fn = conv2d_band_kernel<NT, CS, ELEM>;
-  if (static_cast<int>(lds) > configured.load()) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured.store(static_cast<int>(lds));
-  }
+  if (lds > size_t(kMaxLds)) return hipErrorInvalidValue;
+  hipError_t e = allow_full_lds(reinterpret_cast<const void*>(fn));
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(fn, dim3(bands), dim3(BWG), lds, s, a);
   return hipGetLastError();
 }

@@ -6,7 +6,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "../plan.h"
 
@@ -17,6 +20,26 @@ namespace xtk {
 // must stay below 2^32; the group count is also passed through int.
 inline bool grid_fits(long long workgroups, int threads) {
   return workgroups >= 1 && workgroups <= 0x7fffffffLL && workgroups * threads < (1LL << 32);
+}
+
+// LDS per workgroup on gfx950.
+constexpr int kMaxLds = 160 * 1024;
+
+// Raises `kernel`'s dynamic-LDS limit to the full 160 KB on the current device,
+// once per (kernel, device) and under a lock, so concurrent first launches
+// cannot leave the limit below what a later launch needs.  A host-side
+// attribute: launches recorded into a HIP graph afterwards only enqueue work.
+inline hipError_t allow_full_lds(const void* kernel) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kernel, dev})) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+  if (e == hipSuccess) done.insert({kernel, dev});
+  return e;
 }
 
 // Blocks of the plan's grid, in 64 bits (three int32 axes).

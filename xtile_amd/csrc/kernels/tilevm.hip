@@ -30,8 +30,6 @@
 #include "common.h"
 #include "launch.h"
 
-#include <mutex>
-#include <set>
 
 namespace xtk {
 namespace {
@@ -39,7 +37,6 @@ namespace {
 constexpr int VM_T = 256;
 constexpr int VM_MAX_INST = 40;
 constexpr int VM_MAX_ACC = 8;
-constexpr size_t kVmMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 enum : int { kLoad = 0, kStore = 1, kUnary = 2, kBinary = 3, kReduce = 4, kPermute = 5, kMatmul = 6 };
 enum : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI8 = 3 };
@@ -337,26 +334,13 @@ hipError_t launch_tilevm(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   a.gx = p.grid[0];
   a.gy = p.grid[1];
   const size_t lds = size_t(vm.lds_floats) * 4;
-  if (lds > kVmMaxLds) {
+  if (lds > size_t(kMaxLds)) {
     why = "tile program needs more than 160 KB of LDS";
     return hipErrorInvalidValue;
   }
-  // The dynamic-LDS limit is raised once per device to the full 160 KB, under
-  // a lock, so concurrent first launches cannot leave it below what a later
-  // launch needs.
   {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    hipError_t e = allow_full_lds(reinterpret_cast<const void*>(tilevm_kernel));
     if (e != hipSuccess) return e;
-    static std::mutex mu;
-    static std::set<int> configured;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!configured.count(dev)) {
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(tilevm_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kVmMaxLds);
-      if (e != hipSuccess) return e;
-      configured.insert(dev);
-    }
   }
   const long long blocks = grid_blocks(p);
   if (!grid_fits(blocks, VM_T)) {
