@@ -1,0 +1,99 @@
+"""Clock and power of the GPU while one benchmark configuration runs back to back.
+
+    python -m xtile_amd.power_sample --config c3 [--seconds 3] > out.json
+
+Runs the configuration's launch (bench.py's inputs, rotating input sets)
+captured in a HIP graph of --per-graph launches and replayed continuously for
+--seconds, while the host samples the driver's GPU metrics table (amdsmi
+gpu_metrics: current graphics clock per XCD, socket power, throttle status)
+every ~20 ms; the first 0.5 s (the clock's ramp) are left out of the medians.
+Prints one JSON line.  Measurement tooling: the tile programs never use it.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", required=True)
+    ap.add_argument("--seconds", type=float, default=3.0)
+    ap.add_argument("--per-graph", type=int, default=100)
+    args = ap.parse_args(argv)
+
+    import amdsmi
+    import torch
+
+    import bench
+    import xtile_amd as xt
+
+    module, host, dtypes, out, meta = bench.make_config(args.config)
+    dev = torch.device("cuda:0")
+    set_bytes = sum(h.nbytes for h in host)
+    nsets = max(1, min(128, math.ceil(bench.ROTATE_BYTES / set_bytes)))
+    first = [bench.to_device(h, d, dev) for h, d in zip(host, dtypes)]
+    sets = [first] + [[t.clone() for t in first] for _ in range(nsets - 1)]
+    stream = torch.cuda.Stream(device=dev)
+    xt.launch(module, *sets[0], stream=stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(args.per_graph):
+            xt.launch(module, *sets[i % nsets], stream=stream)
+    torch.cuda.synchronize()
+
+    amdsmi.amdsmi_init()
+    handle = amdsmi.amdsmi_get_processor_handles()[0]
+    samples = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.time()
+    replays = 0
+    done = torch.cuda.Event()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        while time.time() - t0 < args.seconds:
+            graph.replay()
+            replays += 1
+            done.record(stream)
+            # keep at most a few replays queued, sampling while they run
+            while not done.query() and time.time() - t0 < args.seconds + 1.0:
+                m = amdsmi.amdsmi_get_gpu_metrics_info(handle)
+                samples.append((time.time() - t0, m.get("current_gfxclks"), m.get("current_socket_power"),
+                                m.get("throttle_status")))
+                time.sleep(0.02)
+        end.record(stream)
+    torch.cuda.synchronize()
+    amdsmi.amdsmi_shut_down()
+    us = start.elapsed_time(end) * 1000.0 / (replays * args.per_graph)
+    steady = [s for s in samples if s[0] >= 0.5] or samples
+    clks = [[c for c in (s[1] or []) if isinstance(c, int) and 0 < c < 10000] for s in steady]
+    clks = [c for c in clks if c]
+    per_xcd = [round(statistics.median(col)) for col in zip(*clks)] if clks else None
+    rec = {
+        "config": args.config,
+        "launches": replays * args.per_graph,
+        "us_per_launch": round(us, 3),
+        "gfxclk_MHz_median": round(statistics.median(c for row in clks for c in row)) if clks else None,
+        "gfxclk_MHz_per_xcd": per_xcd,
+        "socket_power_W_median": round(statistics.median(s[2] for s in steady if isinstance(s[2], (int, float))))
+        if steady else None,
+        "throttle_status": sorted({str(s[3]) for s in steady}),
+        "samples": len(steady),
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,8 +1,8 @@
 """Summarise rocprofv3 (rocpd SQLite) output for xtile_amd kernels.
 
     python -m xtile_amd.rocprof_summary --trace T.db [--fetch F.db --write W.db
-        --copy-fetch CF.db --copy-write CW.db --copy-mib 256] [--kernel REGEX]
-        [--command "..."] > profiles/<config>_<kernel>.txt
+        --copy-fetch CF.db --copy-write CW.db --copy-mib 256] [--pmc P.db ...]
+        [--kernel REGEX] [--command "..."] > profiles/<config>_<kernel>.txt
 
 Kernel-trace databases give per-kernel dispatch counts and durations.  The
 FETCH_SIZE / WRITE_SIZE databases (one counter per pass) give KiB per
@@ -10,15 +10,28 @@ dispatch; each counter is scaled by the factor that makes it read the true
 byte count of a plain device copy of --copy-mib MiB (which reads and writes
 exactly that many bytes).  The scaled bytes are printed as `fetch_bytes` /
 `write_bytes` lines, which bench.py reads as roofline.traffic.
+
+Each --pmc database (any other counters, one pass each) is reduced per
+dispatch of the selected kernel - SQ_* counters summed over their instances
+(shader engines), GRBM_* counters as the maximum over theirs (XCDs) - and
+averaged over the dispatches.  With SQ_VALU_MFMA_BUSY_CYCLES and
+GRBM_GUI_ACTIVE it also prints the matrix-core busy fraction,
+busy / (GUI-active cycles x 1024 SIMDs), and the clock the GUI-active count
+implies over the dispatch's duration; under counter collection dispatches
+run one at a time, so that clock is the one of a serialised launch, not of a
+back-to-back stream.
 """
 
 from __future__ import annotations
 
 import argparse
+import collections
 import json
 import re
 import sqlite3
 import statistics
+
+SIMDS = 1024  # 256 CUs x 4 SIMDs on MI355X
 
 
 def _kernels(db_path: str, pattern: str | None):
@@ -29,16 +42,26 @@ def _kernels(db_path: str, pattern: str | None):
     return rows
 
 
-def _counter(db_path: str, counter: str, pattern: str | None):
+def _per_dispatch(db_path: str, pattern: str | None):
+    """{dispatch_id: ({counter: reduced value}, duration_ns)} for the selected kernel."""
     db = sqlite3.connect(db_path)
-    rows = db.execute(
-        "select k.name, p.counter_value from pmc_events p join kernels k "
-        "on p.dispatch_id = k.dispatch_id where p.counter_name = ?",
-        (counter,),
-    ).fetchall()
-    if pattern:
-        rows = [r for r in rows if re.search(pattern, r[0])]
-    return [float(v) for _, v in rows]
+    rows = db.execute("select dispatch_id, name, counter_name, counter_value, duration from pmc_events").fetchall()
+    vals: dict = collections.defaultdict(lambda: collections.defaultdict(list))
+    dur = {}
+    for d, name, cn, v, du in rows:
+        if pattern and not re.search(pattern, name):
+            continue
+        vals[d][cn].append(float(v))
+        dur[d] = du
+    out = {}
+    for d, cs in vals.items():
+        out[d] = ({cn: (max(v) if cn.startswith("GRBM_") else sum(v)) for cn, v in cs.items()}, dur[d])
+    return out
+
+
+def _counter(db_path: str, counter: str, pattern: str | None):
+    per = _per_dispatch(db_path, pattern)
+    return [cs[counter] for cs, _ in per.values() if counter in cs]
 
 
 def main(argv=None) -> int:
@@ -49,9 +72,11 @@ def main(argv=None) -> int:
     ap.add_argument("--copy-fetch")
     ap.add_argument("--copy-write")
     ap.add_argument("--copy-mib", type=float, default=256.0)
+    ap.add_argument("--pmc", action="append", default=[], help="a counter-collection database (repeatable)")
     ap.add_argument("--kernel", default=None, help="regex selecting the kernel of interest")
     ap.add_argument("--command", action="append", default=[], help="command lines to record")
     ap.add_argument("--bench-log", default=None, help="stdout of the traced bench.py run")
+    ap.add_argument("--power", default=None, help="JSON line written by xtile_amd.power_sample for this config")
     args = ap.parse_args(argv)
 
     out = []
@@ -106,6 +131,33 @@ def main(argv=None) -> int:
             out.append(f"write_kib_per_dispatch: {wk:.1f}  (raw, {len(write)} dispatches)")
             out.append(f"fetch_bytes: {fk * 1024.0 * f_scale:.0f}")
             out.append(f"write_bytes: {wk * 1024.0 * w_scale:.0f}")
+    for db in args.pmc:
+        per = _per_dispatch(db, args.kernel)
+        if not per:
+            continue
+        names = sorted({cn for cs, _ in per.values() for cn in cs})
+        out.append(f"# counters per dispatch of the selected kernel ({len(per)} dispatches, {db.split('/')[-2]})")
+        for cn in names:
+            vals = [cs[cn] for cs, _ in per.values() if cn in cs]
+            out.append(f"{cn}: {statistics.mean(vals):.0f}")
+        busy = [cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (cs["GRBM_GUI_ACTIVE"] * SIMDS)
+                for cs, _ in per.values() if "SQ_VALU_MFMA_BUSY_CYCLES" in cs and cs.get("GRBM_GUI_ACTIVE")]
+        clk = [cs["GRBM_GUI_ACTIVE"] / d for cs, d in per.values() if cs.get("GRBM_GUI_ACTIVE") and d]
+        durs = [d / 1000.0 for _, d in per.values()]
+        out.append(f"pmc_dispatch_avg_us: {statistics.mean(durs):.3f}")
+        if busy:
+            out.append(f"mfma_busy_fraction: {statistics.mean(busy):.3f}  "
+                       "(SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs))")
+        if clk:
+            out.append(f"gui_active_clock_GHz: {statistics.mean(clk):.3f}  (GRBM_GUI_ACTIVE / dispatch duration, "
+                       "serialised dispatches)")
+    if args.power:
+        rec = json.loads(open(args.power).read().strip().splitlines()[-1])
+        out.append("# clock and power while the kernel runs back to back (xtile_amd.power_sample)")
+        for k in ("launches", "us_per_launch", "gfxclk_MHz_median", "gfxclk_MHz_per_xcd", "socket_power_W_median",
+                  "throttle_status", "samples"):
+            if k in rec:
+                out.append(f"{k}: {rec[k]}")
     print("\n".join(out))
     return 0
 
