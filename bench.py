@@ -14,10 +14,12 @@ loop, a streaming copy, an empty kernel), then each configuration, then the
 vendor GEMM - and only then the CPU legs (the oracle), so the GPU is never
 left idle between timed regions.
 
-Timing of a configuration: W untimed warm-up launches, one more eager launch
-whose output is kept as the reference, then K launches captured in a HIP
-graph and replayed once between two HIP events on the launch stream, with
-device synchronisation on both sides; per-step time = elapsed / K.  Every step
+Timing of a configuration: one eager launch whose output is kept as the
+reference; K launches captured in a HIP graph, instantiated and uploaded to
+the device; ~100 ms of pre-conditioning work (a ceiling kernel, never the
+configuration's own); W untimed warm-up launches; then the graph launched once
+between two HIP events on the launch stream, with device synchronisation on
+both sides; per-step time = elapsed / K.  Every step
 reads a different input set (buffer rotation over >= 1 GiB) so inputs are not
 left resident in the 256 MB Infinity Cache between steps.  Inputs are in HBM
 before the timed region starts; no host transfer is timed.
@@ -194,24 +196,84 @@ def to_host(t, dtype: str) -> np.ndarray:
     return t.numpy()
 
 
+def torch_uint8():
+    import torch
+
+    return torch.uint8
+
+
+_HIP = None
+
+
+def _hip():
+    """The HIP runtime torch loaded (one runtime per process)."""
+    global _HIP
+    if _HIP is None:
+        import torch
+
+        _HIP = ctypes.CDLL(str(Path(torch.__file__).resolve().parent / "lib" / "libamdhip64.so"))
+        vp, pp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        for name, args in {"hipStreamBeginCapture": [vp, ctypes.c_int], "hipStreamEndCapture": [vp, pp],
+                           "hipGraphInstantiate": [pp, vp, vp, vp, ctypes.c_size_t],
+                           "hipGraphUpload": [vp, vp], "hipGraphLaunch": [vp, vp],
+                           "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp]}.items():
+            getattr(_HIP, name).argtypes = args
+            getattr(_HIP, name).restype = ctypes.c_int
+    return _HIP
+
+
+class HipGraph:
+    """`steps` launches captured from `stream` into a HIP graph, instantiated
+    and uploaded to the device before anything is timed.  A graph that is not
+    uploaded pays a one-time setup on its first launch (20-60 us per 20-launch
+    graph on MI355X), which would otherwise land in a short timed region."""
+
+    def __init__(self, launch, n_sets: int, steps: int, stream):
+        hip = _hip()
+        self.stream = ctypes.c_void_p(stream.cuda_stream)
+        self.graph, self.exe = ctypes.c_void_p(), ctypes.c_void_p()
+        self._ok(hip.hipStreamBeginCapture(self.stream, 2), "hipStreamBeginCapture")  # relaxed mode
+        try:
+            for i in range(steps):
+                launch(i % n_sets)
+        finally:
+            rc = hip.hipStreamEndCapture(self.stream, ctypes.byref(self.graph))
+        self._ok(rc, "hipStreamEndCapture")
+        self._ok(hip.hipGraphInstantiate(ctypes.byref(self.exe), self.graph, None, None, 0), "hipGraphInstantiate")
+        self._ok(hip.hipGraphUpload(self.exe, self.stream), "hipGraphUpload")
+
+    @staticmethod
+    def _ok(rc, what):
+        if rc:
+            raise RuntimeError(f"{what} failed (hipError {rc})")
+
+    def replay(self):
+        self._ok(_hip().hipGraphLaunch(self.exe, self.stream), "hipGraphLaunch")
+
+    def __del__(self):
+        hip = _HIP
+        if hip is not None:
+            if getattr(self, "exe", None) and self.exe.value:
+                hip.hipGraphExecDestroy(self.exe)
+            if getattr(self, "graph", None) and self.graph.value:
+                hip.hipGraphDestroy(self.graph)
+
+
 def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool, before_replay=None,
           precondition=None):
     """Average ms per launch of `launch(i)` (i = input set) over `steps`
-    launches.  The launches are captured in a HIP graph first (capture runs
-    nothing); then, on `stream`: the optional `precondition()` work, `warmup`
-    untimed eager launches and `before_replay()`; a device synchronisation;
-    the graph replay between two events; a device synchronisation.  Without
-    a graph the timed launches are eager."""
+    launches.  The launches are captured in a HIP graph and uploaded first
+    (capture runs nothing); then, on `stream`: the optional `precondition()`
+    work, `warmup` untimed eager launches and `before_replay()`; a device
+    synchronisation; the graph launch between two events; a device
+    synchronisation.  Without a graph the timed launches are eager."""
     import torch
 
     graph, mode = None, "eager"
     if use_graph:
         try:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(steps):
-                    launch(i % n_sets)
-            mode = "hip_graph"
+            graph = HipGraph(launch, n_sets, steps, stream)
+            mode = "hip_graph (uploaded before timing)"
         except Exception as exc:  # capture unsupported: time eager launches
             print(f"[bench] graph capture failed ({exc}); timing eager launches", file=sys.stderr)
             graph = None
@@ -290,6 +352,17 @@ class Preconditioner:
         if rc:
             raise RuntimeError(f"ceiling copy launch failed (hipError {rc})")
 
+    @staticmethod
+    def touch(sets) -> None:
+        """Reads one byte of every 64 KB of every rotating input set, in the
+        order the timed launches use them, so that their page translations
+        are warm (a short timed run otherwise pays a TLB miss on each page it
+        is the first to touch since the sets were written) while almost none
+        of their data enters the 256 MB Infinity Cache."""
+        for st in sets:
+            for t in st:
+                t.view(-1).view(torch_uint8())[::65536].sum()
+
     def run(self, bound: str, dtype: str, stream) -> None:
         """About MS milliseconds of MFMA loop (matrix-bound configurations) or
         streaming copy (bandwidth-bound ones) on `stream`."""
@@ -333,6 +406,7 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool, pre: "Prec
 
     def precondition():
         pre.run(meta["bound"], meta["dtype"], stream)
+        pre.touch(sets)
 
     ms, mode = timed(launch, nsets, steps, warmup, stream, use_graph, before_replay=clear,
                      precondition=precondition if pre is not None else None)
@@ -368,7 +442,7 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool, pre: "Prec
         "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets"
                   + (f", after {Preconditioner.MS:.0f} ms of device pre-conditioning ("
                      + ("MFMA loop" if meta["bound"] == "mfma" else "streaming copy")
-                     + ", include/xt_ceiling.h)" if pre is not None else ""),
+                     + ", include/xt_ceiling.h) and a page-touch of every input set" if pre is not None else ""),
         "roofline": roof,
         "algo_bytes": plan["bytes"],
         "algo_flops": plan["flops"],
