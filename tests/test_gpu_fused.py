@@ -181,3 +181,27 @@ def test_misaligned_buffer_runs_on_the_interpreter(cuda):
     xt.launch(m, torch.from_numpy(a).to(cuda), torch.from_numpy(v).to(cuda), out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), a + v)
+
+
+def test_misaligned_softmax_rows_above_2048_run_on_the_interpreter(cuda):
+    """Rows of 4096 floats are planned onto the float4 softmax kernel; a view
+    with a 4-byte storage offset cannot be read as float4, so that launch
+    runs on the interpreter lowering the plan keeps beside it (before, the
+    launch was refused as 'row too long')."""
+    import torch
+
+    m = K.softmax(64, 4096, 1)
+    assert xt.plan(m)["kernel"].startswith("row_softmax")
+    rng = np.random.default_rng(47)
+    x = rng.normal(0, 2, (64, 4096)).astype(np.float32)
+    print("[gpu] misaligned softmax 64x4096", flush=True)
+    store = torch.zeros(64 * 4096 + 1, dtype=torch.float32, device=cuda)
+    inp = store[1:].view(64, 4096)
+    assert inp.data_ptr() % 16 == 4
+    inp.copy_(torch.from_numpy(x).to(cuda))
+    out = torch.zeros(64, 4096, dtype=torch.float32, device=cuda)
+    xt.launch(m, inp, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = run_oracle(m, [x, np.zeros_like(x)], 4)[1]
+    assert np.max(np.abs(got - want) / np.abs(want)) <= 1e-5
