@@ -550,9 +550,17 @@ def vendor() -> dict:
         out["hipblaslt_bf16_c5_f32out_TFLOPs"] = rate(lambda: torch.mm(a, b, out_dtype=torch.float32), f)
     except Exception:
         out["hipblaslt_bf16_c5_f32out_TFLOPs"] = None
+    a = torch.randint(-128, 128, (4096, 4096), dtype=torch.int8, device=dev)
+    b = torch.randint(-128, 128, (4096, 4096), dtype=torch.int8, device=dev)
+    try:
+        out["hipblaslt_i8_4096_i32out_TOPs"] = rate(lambda: torch._int_mm(a, b), 2 * 4096**3)
+    except Exception as exc:
+        out["hipblaslt_i8_4096_i32out_TOPs"] = None
+        out["i8_error"] = str(exc)[:200]
     del a, b
     torch.cuda.empty_cache()
-    out["note"] = "torch.mm (hipBLASLt); f32out = torch.mm(..., out_dtype=torch.float32), the configurations' own types"
+    out["note"] = ("torch.mm (hipBLASLt); f32out = torch.mm(..., out_dtype=torch.float32), the configurations' own "
+                   "types; i8 = torch._int_mm (i32 out, no epilogue)")
     return out
 
 
@@ -692,7 +700,7 @@ def main(argv=None) -> int:
     ceil = None if args.no_ceilings or pre is None else ceilings(pre)
     results = {n: gpu_leg(n, cfgs[n], args.steps, args.warmup, not args.no_graph, pre) for n in names}
     del pre
-    vend = None if args.no_ceilings or not ({"c3", "c5"} & set(names)) else vendor()
+    vend = None if args.no_ceilings or not ({"c3", "c5", "c6"} & set(names)) else vendor()
     if args.cpu_seconds > 0:
         for n in names:
             cpu_leg(n, cfgs[n], results[n], args.cpu_seconds)

@@ -271,6 +271,53 @@ __global__ __launch_bounds__(TPB) void row_softmax_wide_kernel(SoftmaxArgs p) {
   }
 }
 
+// The same full-row softmax for the common case of one row per Block on a
+// 1-D grid: Block x's row starts x * step float4 vectors past the row of
+// Block 0, so the prologue is one multiply-add (no Block decode, no row loop,
+// a four-argument kernarg segment).
+template <int TPB, int NV>
+__global__ __launch_bounds__(TPB) void row_softmax_1d_kernel(const float4v* __restrict__ x, float4v* __restrict__ y,
+                                                             long long xstep, long long ystep) {
+  constexpr int NW = TPB / 64;
+  __shared__ float lds[2][NW];
+  const int w = threadIdx.x >> 6;
+  const float4v* xr = x + blockIdx.x * xstep + threadIdx.x;
+  float4v* yr = y + blockIdx.x * ystep + threadIdx.x;
+  float4v v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) v[j] = ld_nt(xr + j * TPB);
+  issue_fence();
+  float m = fmaxf(fmaxf(v[0].x, v[0].y), fmaxf(v[0].z, v[0].w));
+#pragma unroll
+  for (int j = 1; j < NV; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((threadIdx.x & 63) == 0) lds[0][w] = m;
+  __syncthreads();
+  m = lds[0][0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) m = fmaxf(m, lds[0][k]);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    v[j].x = expf(v[j].x - m);
+    v[j].y = expf(v[j].y - m);
+    v[j].z = expf(v[j].z - m);
+    v[j].w = expf(v[j].w - m);
+    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  if ((threadIdx.x & 63) == 0) lds[1][w] = s;
+  __syncthreads();
+  s = lds[1][0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) s += lds[1][k];
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) st_nt(v[j] * inv, yr + j * TPB);
+}
+
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
 
 bool aligned4(const xt::Access2D& a, const void* base) {
@@ -370,6 +417,19 @@ hipError_t launch_row_softmax(const xt::Plan& p, void* const* bufs, hipStream_t 
     return hipErrorInvalidValue;
   }
   dim3 grid(static_cast<unsigned>(blocks));
+  if (wide && a.rows == 1 && p.grid[1] == 1 && p.grid[2] == 1) {
+    // one row per Block on a 1-D grid (aligned4 makes every offset a float4 multiple)
+    const float4v* x4 = reinterpret_cast<const float4v*>(a.x + p.a.addr.c0);
+    float4v* y4 = reinterpret_cast<float4v*>(a.y + p.c.addr.c0);
+    const long long xs = p.a.addr.sx / 4, ys = p.c.addr.sx / 4;
+    switch (a.cols / 2048) {
+#define XT_SM1(NVV) \
+  case NVV: hipLaunchKernelGGL((row_softmax_1d_kernel<512, NVV>), grid, dim3(512), 0, s, x4, y4, xs, ys); break
+      XT_SM1(1); XT_SM1(2); XT_SM1(3); XT_SM1(4); XT_SM1(5); XT_SM1(6); XT_SM1(7); XT_SM1(8);
+#undef XT_SM1
+    }
+    return hipGetLastError();
+  }
   if (wide) {
     a.tpr = 512;
     switch (a.cols / 2048) {
