@@ -18,7 +18,12 @@ from __future__ import annotations
 import os
 from typing import Any
 
-from . import _xtile as _native
+if os.environ.get("XTILE_AMD_BINDING", "ctypes") == "compiled":
+    from ._compiled import load as _load_compiled
+
+    _native = _load_compiled()  # csrc/XTModule.cpp, the compiled _xtile
+else:
+    from . import _xtile as _native  # ctypes over the same C ABI
 from .dsl import (
     Array,
     DType,

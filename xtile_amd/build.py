@@ -4,6 +4,9 @@ Produces, under ``xtile_amd/lib/``:
   * ``libxtile_amd.so`` - the C ABI of ``include/xtile_amd.h``: xt parser,
     verifier, passes, launch planner and the gfx950 HIP kernels;
   * ``xt-opt``          - the command-line driver (host code only);
+  * ``_xtile<ext>.so``   - the compiled Python module ``_xtile``
+    (``csrc/XTModule.cpp``, pybind11) over the C ABI, with the reference
+    module's function names;
   * ``libxt_ceiling.so`` - the measurement kernels of ``include/xt_ceiling.h``
     (a copy, an empty kernel and an MFMA loop) that bench.py times for its
     ceilings; the tile programs never use it.
@@ -19,6 +22,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -118,7 +122,41 @@ def build(verbose: bool = False) -> Path:
     _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", str(ceil_obj), "-o", str(ceil_tmp)])
     os.replace(ceil_tmp, LIB / "libxt_ceiling.so")
     _run([CXX, *map(str, host_objs), str(xt_opt_obj), "-o", str(LIB / "xt-opt")])
+    build_module()
     return lib
+
+
+def module_path() -> Path:
+    """Where build_module() puts the compiled ``_xtile`` module."""
+    return LIB / ("_xtile" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def build_module() -> Path:
+    """Compile csrc/XTModule.cpp against the freshly linked libxtile_amd.so
+    (found beside it at run time through an $ORIGIN rpath)."""
+    import pybind11
+
+    out = module_path()
+    tmp = out.with_name(out.name + ".tmp")
+    _run(
+        [
+            CXX,
+            *HOST_FLAGS,
+            "-shared",
+            "-fvisibility=hidden",
+            f"-I{pybind11.get_include()}",
+            f"-I{sysconfig.get_paths()['include']}",
+            f"-I{ROOT / 'include'}",
+            str(CSRC / "XTModule.cpp"),
+            f"-L{LIB}",
+            "-lxtile_amd",
+            "-Wl,-rpath,$ORIGIN",
+            "-o",
+            str(tmp),
+        ]
+    )
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
