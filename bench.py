@@ -17,9 +17,11 @@ left idle between timed regions.
 Timing of a configuration: one eager launch whose output is kept as the
 reference; K launches captured in a HIP graph, instantiated and uploaded to
 the device; ~100 ms of pre-conditioning work (a ceiling kernel, never the
-configuration's own); W untimed warm-up launches; then the graph launched once
-between two HIP events on the launch stream, with device synchronisation on
-both sides; per-step time = elapsed / K.  Every step
+configuration's own); W untimed warm-up launches; device synchronisation; a
+hold kernel (one wave waiting 500 + K us of wall clock) that keeps the stream
+busy while the host enqueues the graph; then the graph launched once between
+two HIP events on the launch stream, and device synchronisation; per-step
+time = elapsed / K, the events bracketing exactly the K launches.  Every step
 reads a different input set (buffer rotation over >= 1 GiB) so inputs are not
 left resident in the 256 MB Infinity Cache between steps.  Inputs are in HBM
 before the timed region starts; no host transfer is timed.
@@ -259,14 +261,32 @@ class HipGraph:
                 hip.hipGraphDestroy(self.graph)
 
 
+def hold_us(steps: int) -> int:
+    """Length of the hold kernel ahead of a timed run of `steps` launches:
+    longer than the host takes to enqueue them (a 20-launch graph takes
+    40-170 us to submit on the MI355X boxes, a 2000-launch one ~1.1 ms)."""
+    return min(10**6, 500 + steps)
+
+
+def hold(stream, steps: int) -> None:
+    rc = _ceiling_lib().xt_ceiling_hold(hold_us(steps), stream.cuda_stream)
+    if rc:
+        raise RuntimeError(f"hold kernel launch failed (hipError {rc})")
+
+
 def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool, before_replay=None,
           precondition=None):
     """Average ms per launch of `launch(i)` (i = input set) over `steps`
     launches.  The launches are captured in a HIP graph and uploaded first
     (capture runs nothing); then, on `stream`: the optional `precondition()`
     work, `warmup` untimed eager launches and `before_replay()`; a device
-    synchronisation; the graph launch between two events; a device
-    synchronisation.  Without a graph the timed launches are eager."""
+    synchronisation; the hold kernel (xt_ceiling_hold), then the graph launch
+    between two events; a device synchronisation.  The hold keeps the stream
+    busy while the host enqueues the graph, so the start event fires when the
+    timed launches are already queued and the events time the kernels, not the
+    host's submission (without it a 20-launch C1 run measured 6.4-9.2 us per
+    launch against 4.1-4.5 with it and 3.7-4.1 over 2000 launches).  Without
+    a graph the timed launches are eager."""
     import torch
 
     graph, mode = None, "eager"
@@ -289,6 +309,7 @@ def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool,
             before_replay()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
+        hold(stream, steps)
         start.record(stream)
         if graph is not None:
             graph.replay()
@@ -439,7 +460,8 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool, pre: "Prec
         "ms_per_step": ms,
         "dtype": meta["dtype"],
         "data": meta["data"],
-        "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets"
+        "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets, "
+                  f"a {hold_us(steps)} us hold kernel ahead of the start event (covers the host's enqueue)"
                   + (f", after {Preconditioner.MS:.0f} ms of device pre-conditioning ("
                      + ("MFMA loop" if meta["bound"] == "mfma" else "streaming copy")
                      + ", include/xt_ceiling.h) and a page-touch of every input set" if pre is not None else ""),
@@ -451,15 +473,22 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool, pre: "Prec
     }
 
 
+_CEILING_LIB = None
+
+
 def _ceiling_lib():
-    lib = ctypes.CDLL(str(ROOT / "xtile_amd" / "lib" / "libxt_ceiling.so"))
-    lib.xt_ceiling_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-    lib.xt_ceiling_noop.argtypes = [ctypes.c_int, ctypes.c_void_p]
-    lib.xt_ceiling_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                    ctypes.c_void_p]
-    for f in (lib.xt_ceiling_copy, lib.xt_ceiling_noop, lib.xt_ceiling_mfma):
-        f.restype = ctypes.c_int
-    return lib
+    global _CEILING_LIB
+    if _CEILING_LIB is None:
+        lib = ctypes.CDLL(str(ROOT / "xtile_amd" / "lib" / "libxt_ceiling.so"))
+        lib.xt_ceiling_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.xt_ceiling_noop.argtypes = [ctypes.c_int, ctypes.c_void_p]
+        lib.xt_ceiling_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_void_p]
+        lib.xt_ceiling_hold.argtypes = [ctypes.c_uint, ctypes.c_void_p]
+        for f in (lib.xt_ceiling_copy, lib.xt_ceiling_noop, lib.xt_ceiling_mfma, lib.xt_ceiling_hold):
+            f.restype = ctypes.c_int
+        _CEILING_LIB = lib
+    return _CEILING_LIB
 
 
 def ceilings(pre: Preconditioner) -> dict:

@@ -27,6 +27,14 @@ int xt_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream);
  * per-launch floor of a graph replay at a given grid size. */
 int xt_ceiling_noop(int workgroups, void* stream);
 
+/* One wave that occupies `stream` for `microseconds` (1 to 10^6) of the
+ * device's constant-rate wall clock and does nothing else.  Enqueued ahead
+ * of a timed run, it lets the host finish enqueuing the run (tens to
+ * hundreds of microseconds for a graph of launches) before the first timed
+ * kernel starts, so that a short run's events time the kernels and not the
+ * host's submission. */
+int xt_ceiling_hold(unsigned microseconds, void* stream);
+
 /* Back-to-back MFMAs: `workgroups` workgroups of 4 waves, each wave running
  * `iters` rounds of 8 independent 32x32 MFMAs on fragments it reads once from
  * `operands` (16 bytes per lane per fragment; at least

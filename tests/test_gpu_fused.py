@@ -45,6 +45,8 @@ def _ln_inputs(rows, cols, seed):
         (96, 48, 16, "tile=16x48 threads=16x4"),       # 48 columns: 12 vectors, 4 threads a row
         # more Blocks than the chip holds: 2048 workgroups walk 8192 Blocks with gamma / beta in registers
         (8192, 1024, 1, "tile=1x1024 threads=1x256 vw=4 workgroups=2048"),
+        # 512 workgroups walk 5000 Blocks: the last pass leaves most workgroups without a Block
+        (5000, 4096, 1, "tile=1x4096 threads=1x512 vw=4 workgroups=512"),
     ],
 )
 def test_fused_layernorm(cuda, rows, cols, trow, layout):
@@ -127,12 +129,12 @@ func.func @center(%x: memref<8192x4096xf32>, %b: memref<1x4096xf32>, %y: memref<
 
 
 def test_fused_block_loop_with_one_lds_reduction_is_bit_exact(cuda):
-    """x - rowmax(x) + b over 8192 rows: 1024 workgroups walk the Blocks with
+    """x - rowmax(x) + b over 8192 rows: 512 workgroups walk the Blocks with
     b in registers, and the one LDS reduction region is reused Block after
     Block (a barrier closes each Block).  max, sub and add are exact in any
     order, so the result is bit-exact."""
     m = xt.parse(_CENTER)
-    assert xt.plan(m)["kernel"].startswith("fused f32 tile=1x4096 threads=1x512 vw=4 workgroups=1024")
+    assert xt.plan(m)["kernel"].startswith("fused f32 tile=1x4096 threads=1x512 vw=4 workgroups=512")
     rng = np.random.default_rng(47)
     x = rng.normal(0, 1, (8192, 4096)).astype(np.float32)
     b = rng.normal(0, 1, (1, 4096)).astype(np.float32)

@@ -247,7 +247,7 @@ def test_ceiling_library_exports_every_declared_symbol():
     include/xt_ceiling.h declares, and refuses bad arguments on the host."""
     header = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "xt_ceiling.h").read_text(), flags=re.S)
     declared = sorted(set(re.findall(r"\b(xt_[a-z_]+)\s*\(", header)))
-    assert declared == ["xt_ceiling_copy", "xt_ceiling_mfma", "xt_ceiling_noop"]
+    assert declared == ["xt_ceiling_copy", "xt_ceiling_hold", "xt_ceiling_mfma", "xt_ceiling_noop"]
     import bench
 
     lib = bench._ceiling_lib()
@@ -256,6 +256,8 @@ def test_ceiling_library_exports_every_declared_symbol():
     # misaligned sizes, empty grids and unknown kinds are refused before any launch
     assert lib.xt_ceiling_copy(0x1000, 0x2000, 15, None) != 0
     assert lib.xt_ceiling_noop(0, None) != 0
+    assert lib.xt_ceiling_hold(0, None) != 0 and lib.xt_ceiling_hold(1000001, None) != 0
+    assert bench.hold_us(20) == 520 and bench.hold_us(10**7) == 10**6
     assert lib.xt_ceiling_mfma(0x1000, 0x2000, 1, 1, 7, None) != 0
 
 

@@ -1,7 +1,9 @@
 // Measurement kernels for the benchmark's ceilings (include/xt_ceiling.h):
-// a streaming copy, an empty kernel and an MFMA issue loop.  They compute
-// nothing a tile program needs; bench.py times them beside the tile programs
-// so that each roofline fraction can be read against what this GPU attains.
+// a streaming copy, an empty kernel and an MFMA issue loop, and the hold
+// kernel that keeps a stream busy while the host enqueues a timed run.  They
+// compute nothing a tile program needs; bench.py times them beside the tile
+// programs so that each roofline fraction can be read against what this GPU
+// attains.
 #include <hip/hip_runtime.h>
 
 #include "../../include/xt_ceiling.h"
@@ -40,6 +42,14 @@ __global__ __launch_bounds__(256) void copy_kernel(const float4v* __restrict__ s
 }
 
 __global__ __launch_bounds__(256) void noop_kernel() {}
+
+// One wave that returns once `ticks` of the constant-rate wall clock have
+// passed since it started; sleeping between reads keeps it off the issue
+// ports.  The host bounds `ticks`, so every launch ends.
+__global__ __launch_bounds__(64) void hold_kernel(unsigned long long ticks) {
+  const unsigned long long t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
 
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef int int16v __attribute__((ext_vector_type(16)));
@@ -103,6 +113,18 @@ int xt_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream) {
 int xt_ceiling_noop(int workgroups, void* stream) {
   if (workgroups < 1 || (long long)workgroups * 256 >= (1LL << 32)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(noop_kernel, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream));
+  return hipGetLastError();
+}
+
+int xt_ceiling_hold(unsigned microseconds, void* stream) {
+  if (microseconds < 1 || microseconds > 1000000) return hipErrorInvalidValue;
+  int dev = 0, khz = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+  if (e != hipSuccess) return e;
+  if (khz <= 0) return hipErrorInvalidValue;
+  const unsigned long long ticks = static_cast<unsigned long long>(microseconds) * static_cast<unsigned>(khz) / 1000u;
+  hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), ticks);
   return hipGetLastError();
 }
 

@@ -19,6 +19,7 @@
 // shuffles (and LDS when a row spans waves), or across the TR threads of a
 // column through LDS.
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <sstream>
 
@@ -113,9 +114,14 @@ class Gen {
     const long long blocks = (long long)grid_[0] * grid_[1] * grid_[2];
     const long long resident = 256LL * std::max(1, std::min(32, 2048 / L.threads()));
     bool invariant = false;
-    for (const VmInst& in : vm_.inst) invariant |= in.op == VmOp::Load && !streamed(in.kind);
+    long long stream_bytes = 0;  // streamed tile bytes one Block reads
+    for (const VmInst& in : vm_.inst)
+      if (in.op == VmOp::Load) {
+        invariant |= !streamed(in.kind);
+        if (streamed(in.kind)) stream_bytes += (long long)in.dims[1] * in.dims[2] * elem_bytes(vm_.access[in.kind].elem);
+      }
     hoist_ = invariant && blocks > 2 * resident && blocks < (1LL << 30);
-    const long long wgs = hoist_ ? resident : blocks;
+    const long long wgs = hoist_ ? walkers(blocks, resident, stream_bytes) : blocks;
     pre_.str("");
     body_.str("");
     for (size_t i = 0; i < vm_.inst.size(); ++i)
@@ -160,6 +166,33 @@ class Gen {
   bool hoist_ = false;
   int red_floats_ = 0;
   int n_red_ = 0;                   // reductions that go through LDS
+
+  // Workgroups of a kernel that walks the Blocks: each holds its Block's
+  // streamed tiles and the next Block's prefetch, so the grid keeps about
+  // 2 * wgs * stream_bytes of reads in flight.  About 16 MB is best: on an
+  // 8192 x 4096 f32 layernorm (16 KB rows) 512 workgroups, two per CU with 16
+  // rows each, ran 44.5 us per launch against 47.0 with 1024 (full occupancy,
+  // 32 MB in flight) and 60.7 with 256.  A multiple of the 256 CUs, within
+  // [256, resident], and among those near the target the one that deals the
+  // Blocks most evenly (384 workgroups over 8192 rows, 21.3 rows each, ran
+  // 47.7 us).
+  static long long walkers(long long blocks, long long resident, long long stream_bytes) {
+    constexpr long long kInFlight = 16LL << 20;
+    long long target = stream_bytes > 0 ? kInFlight / (2 * stream_bytes) : resident;
+    target = std::max(256LL, std::min(resident, target / 256 * 256));
+    long long best = target;
+    double best_cost = 1e300;
+    for (long long w = std::max(256LL, target / 2 / 256 * 256); w <= std::min(resident, target * 2); w += 256) {
+      const double per = (double)blocks / w, imbalance = std::ceil(per) / per;
+      // prefer the target; a workgroup count off it by 2x costs as much as 10% imbalance
+      const double cost = imbalance * (1.0 + 0.1 * std::fabs(std::log2((double)w / target)));
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = w;
+      }
+    }
+    return best;
+  }
 
   static void dims2(const int d[3], int& a, int& b) {
     a = d[1];
