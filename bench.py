@@ -15,22 +15,24 @@ vendor GEMM - and only then the CPU legs (the oracle), so the GPU is never
 left idle between timed regions.
 
 Timing of a configuration: one eager launch whose output is kept as the
-reference; K launches captured in a HIP graph, instantiated and uploaded to
-the device; ~100 ms of pre-conditioning work (a ceiling kernel, never the
-configuration's own); W untimed warm-up launches; device synchronisation; a
-hold kernel (one wave waiting 500 + K us of wall clock) that keeps the stream
-busy while the host enqueues the graph; then the graph launched once between
-two HIP events on the launch stream, and device synchronisation; per-step
-time = elapsed / K, the events bracketing exactly the K launches.  Every step
-reads a different input set (buffer rotation over >= 1 GiB) so inputs are not
-left resident in the 256 MB Infinity Cache between steps.  Inputs are in HBM
-before the timed region starts; no host transfer is timed.
+reference; for runs of more than 64 launches, K launches captured in a HIP
+graph, instantiated and uploaded to the device; ~100 ms of pre-conditioning
+work (a ceiling kernel, never the configuration's own); W untimed warm-up
+launches; device synchronisation; a hold kernel (one wave waiting a few
+hundred microseconds of wall clock) that keeps the stream busy while the host
+enqueues the timed launches; then the K launches (the graph's one replay, or
+K eager launches for K <= 64) between two HIP events on the launch stream,
+and device synchronisation; per-step time = elapsed / K, the events
+bracketing exactly the K launches.  Every step reads a different input set
+(buffer rotation over >= 1 GiB) so inputs are not left resident in the
+256 MB Infinity Cache between steps.  Inputs are in HBM before the timed
+region starts; no host transfer is timed.
 
-Checks: the output of input set 0 is cleared after the warm-up and the
-capture, just before the timed replay; after the replay it must equal the eager reference bit for bit, and the
-reference must match the oracle (the CPU leg's own output on the same inputs)
-to the configuration's bar.  A failed check fails the run: no JSON line is
-printed and the exit status is 1.
+Checks: the output of input set 0 is cleared after the warm-up, just before
+the timed launches; afterwards it must equal the eager reference bit for bit
+("replay_equals_eager"), and the reference must match the oracle (the CPU
+leg's own output on the same inputs) to the configuration's bar.  A failed
+check fails the run: no JSON line is printed and the exit status is 1.
 
 roofline.achieved = algorithmic bytes (or FLOPs) of one launch / per-step
 time; roofline.traffic = measured HBM bytes per launch from the rocprofv3
@@ -261,42 +263,61 @@ class HipGraph:
                 hip.hipGraphDestroy(self.graph)
 
 
-def hold_us(steps: int) -> int:
+# Runs of at most this many launches are timed as eager launches queued
+# behind the hold kernel; longer runs as one replay of an uploaded HIP graph.
+EAGER_MAX_STEPS = 64
+
+
+def hold_us(steps: int, eager: bool) -> int:
     """Length of the hold kernel ahead of a timed run of `steps` launches:
-    longer than the host takes to enqueue them (a 20-launch graph takes
-    40-170 us to submit on the MI355X boxes, a 2000-launch one ~1.1 ms)."""
-    return min(10**6, 500 + steps)
+    longer than the host takes to enqueue them.  On the MI355X boxes a
+    20-launch graph takes 40-170 us to submit and a 2000-launch one ~1.1 ms;
+    an eager launch through xt.launch ~17 us."""
+    return min(5000, 500 + 40 * steps) if eager else min(10**6, 500 + steps)
 
 
-def hold(stream, steps: int) -> None:
-    rc = _ceiling_lib().xt_ceiling_hold(hold_us(steps), stream.cuda_stream)
+def hold(stream, us: int) -> None:
+    rc = _ceiling_lib().xt_ceiling_hold(us, stream.cuda_stream)
     if rc:
         raise RuntimeError(f"hold kernel launch failed (hipError {rc})")
 
 
 def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool, before_replay=None,
           precondition=None):
-    """Average ms per launch of `launch(i)` (i = input set) over `steps`
-    launches.  The launches are captured in a HIP graph and uploaded first
-    (capture runs nothing); then, on `stream`: the optional `precondition()`
-    work, `warmup` untimed eager launches and `before_replay()`; a device
-    synchronisation; the hold kernel (xt_ceiling_hold), then the graph launch
-    between two events; a device synchronisation.  The hold keeps the stream
-    busy while the host enqueues the graph, so the start event fires when the
-    timed launches are already queued and the events time the kernels, not the
-    host's submission (without it a 20-launch C1 run measured 6.4-9.2 us per
-    launch against 4.1-4.5 with it and 3.7-4.1 over 2000 launches).  Without
-    a graph the timed launches are eager."""
+    """(average ms per launch of `launch(i)` over `steps` launches, i = input
+    set; description of how they were timed).
+
+    Runs of more than EAGER_MAX_STEPS launches are captured in a HIP graph and
+    uploaded first (capture runs nothing).  Then, on `stream`: the optional
+    `precondition()` work, `warmup` untimed eager launches and
+    `before_replay()`; a device synchronisation; the hold kernel
+    (xt_ceiling_hold); the start event, the timed launches (the graph's one
+    replay, or the eager launches), the end event; a device synchronisation.
+
+    The hold keeps the stream busy while the host enqueues the timed launches,
+    so the start event fires when they are already queued and the events time
+    the kernels, not the host's submission: without it a 20-launch C1 run
+    measured 6.4-9.2 us per launch, against 4.1-4.5 us with it and 3.7-4.1 over
+    2000 launches.  Short runs use eager launches because a graph's first
+    replay costs each short launch about 0.3-0.4 us more than its later
+    replays (C1, 20 launches: 4.55-4.65 us per launch on the first replay,
+    4.13-4.17 eager behind the hold, 4.20-4.24 on a second replay; C2 and C4
+    by 0.2-0.6 us), and a timed run replays its graph once; long runs use the
+    graph, because a long queue of eager launches runs slower than a replay
+    (C2, 200 launches: 44.9-45.7 us eager, 43.6-44.2 replayed)."""
+    import time
+
     import torch
 
-    graph, mode = None, "eager"
-    if use_graph:
+    eager = not use_graph or steps <= EAGER_MAX_STEPS
+    graph, mode = None, "eager launches"
+    if not eager:
         try:
             graph = HipGraph(launch, n_sets, steps, stream)
-            mode = "hip_graph (uploaded before timing)"
+            mode = "one replay of a HIP graph uploaded before timing"
         except Exception as exc:  # capture unsupported: time eager launches
             print(f"[bench] graph capture failed ({exc}); timing eager launches", file=sys.stderr)
-            graph = None
+            eager = True
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -308,16 +329,24 @@ def timed(launch, n_sets: int, steps: int, warmup: int, stream, use_graph: bool,
         if before_replay is not None:
             before_replay()
     torch.cuda.synchronize()
+    us = hold_us(steps, eager)
     with torch.cuda.stream(stream):
-        hold(stream, steps)
+        hold(stream, us)
         start.record(stream)
+        t0 = time.perf_counter()
         if graph is not None:
             graph.replay()
         else:
             for i in range(steps):
                 launch(i % n_sets)
+        t1 = time.perf_counter()
         end.record(stream)
     torch.cuda.synchronize()
+    enq = (t1 - t0) * 1e6
+    if enq > us:
+        print(f"[bench] the host took {enq:.0f} us to enqueue {steps} launches, longer than the {us} us hold: "
+              "the timed region includes host submission", file=sys.stderr)
+    mode += f" behind a {us} us hold kernel (host enqueue {enq:.0f} us)"
     return start.elapsed_time(end) / steps, mode
 
 
@@ -460,8 +489,7 @@ def gpu_leg(name: str, cfg, steps: int, warmup: int, use_graph: bool, pre: "Prec
         "ms_per_step": ms,
         "dtype": meta["dtype"],
         "data": meta["data"],
-        "timing": f"{mode}, {steps} launches after {warmup} warm-up, {nsets} rotating input sets, "
-                  f"a {hold_us(steps)} us hold kernel ahead of the start event (covers the host's enqueue)"
+        "timing": f"{steps} {mode}, after {warmup} warm-up, {nsets} rotating input sets"
                   + (f", after {Preconditioner.MS:.0f} ms of device pre-conditioning ("
                      + ("MFMA loop" if meta["bound"] == "mfma" else "streaming copy")
                      + ", include/xt_ceiling.h) and a page-touch of every input set" if pre is not None else ""),
@@ -542,25 +570,21 @@ def ceilings(pre: Preconditioner) -> dict:
     return out
 
 
-def vendor() -> dict:
+def vendor(pre: "Preconditioner | None") -> dict:
     """hipBLASLt through torch on the GEMM configurations' shapes and types,
-    in the same process (eager launches between events, after warm-up)."""
+    in the same process and the same protocol as the configurations: the MFMA
+    pre-conditioning loop, 10 warm-up calls, then 50 calls queued behind the
+    hold kernel between two events (on a side stream)."""
     import torch
 
     dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
     out = {}
 
-    def rate(fn, flops, n=50):
-        for _ in range(10):
-            fn()
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(n):
-            fn()
-        e.record()
-        torch.cuda.synchronize()
-        return flops / (s.elapsed_time(e) / n * 1e-3) / 1e12
+    def rate(fn, flops, n=50, kind="f16"):
+        precondition = (lambda: pre.run("mfma", kind, stream)) if pre is not None else None
+        ms, _ = timed(lambda i: fn(), 1, n, 10, stream, True, precondition=precondition)
+        return flops / (ms * 1e-3) / 1e12
 
     a = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
     b = (torch.rand(4096, 4096, device=dev) * 2 - 1).half()
@@ -574,22 +598,23 @@ def vendor() -> dict:
     a = (torch.randn(4096, 4096, device=dev) * 0.02).bfloat16()
     b = (torch.randn(4096, 11008, device=dev) * 0.02).bfloat16()
     f = 2 * 4096 * 4096 * 11008
-    out["hipblaslt_bf16_c5_bf16out_TFLOPs"] = rate(lambda: torch.mm(a, b), f)
+    out["hipblaslt_bf16_c5_bf16out_TFLOPs"] = rate(lambda: torch.mm(a, b), f, kind="bf16")
     try:
-        out["hipblaslt_bf16_c5_f32out_TFLOPs"] = rate(lambda: torch.mm(a, b, out_dtype=torch.float32), f)
+        out["hipblaslt_bf16_c5_f32out_TFLOPs"] = rate(lambda: torch.mm(a, b, out_dtype=torch.float32), f, kind="bf16")
     except Exception:
         out["hipblaslt_bf16_c5_f32out_TFLOPs"] = None
     a = torch.randint(-128, 128, (4096, 4096), dtype=torch.int8, device=dev)
     b = torch.randint(-128, 128, (4096, 4096), dtype=torch.int8, device=dev)
     try:
-        out["hipblaslt_i8_4096_i32out_TOPs"] = rate(lambda: torch._int_mm(a, b), 2 * 4096**3)
+        out["hipblaslt_i8_4096_i32out_TOPs"] = rate(lambda: torch._int_mm(a, b), 2 * 4096**3, kind="i8")
     except Exception as exc:
         out["hipblaslt_i8_4096_i32out_TOPs"] = None
         out["i8_error"] = str(exc)[:200]
     del a, b
     torch.cuda.empty_cache()
     out["note"] = ("torch.mm (hipBLASLt); f32out = torch.mm(..., out_dtype=torch.float32), the configurations' own "
-                   "types; i8 = torch._int_mm (i32 out, no epilogue)")
+                   "types; i8 = torch._int_mm (i32 out, no epilogue); the same operands every call (no rotation); "
+                   "MFMA pre-conditioning, 10 warm-up calls, 50 timed calls queued behind the hold kernel")
     return out
 
 
@@ -728,8 +753,8 @@ def main(argv=None) -> int:
     pre = None if args.no_precondition else Preconditioner()
     ceil = None if args.no_ceilings or pre is None else ceilings(pre)
     results = {n: gpu_leg(n, cfgs[n], args.steps, args.warmup, not args.no_graph, pre) for n in names}
+    vend = None if args.no_ceilings or not ({"c3", "c5", "c6"} & set(names)) else vendor(pre)
     del pre
-    vend = None if args.no_ceilings or not ({"c3", "c5", "c6"} & set(names)) else vendor()
     if args.cpu_seconds > 0:
         for n in names:
             cpu_leg(n, cfgs[n], results[n], args.cpu_seconds)

@@ -257,7 +257,8 @@ def test_ceiling_library_exports_every_declared_symbol():
     assert lib.xt_ceiling_copy(0x1000, 0x2000, 15, None) != 0
     assert lib.xt_ceiling_noop(0, None) != 0
     assert lib.xt_ceiling_hold(0, None) != 0 and lib.xt_ceiling_hold(1000001, None) != 0
-    assert bench.hold_us(20) == 520 and bench.hold_us(10**7) == 10**6
+    assert bench.hold_us(20, eager=True) == 1300 and bench.hold_us(10**4, eager=True) == 5000
+    assert bench.hold_us(2000, eager=False) == 2500 and bench.hold_us(10**7, eager=False) == 10**6
     assert lib.xt_ceiling_mfma(0x1000, 0x2000, 1, 1, 7, None) != 0
 
 
