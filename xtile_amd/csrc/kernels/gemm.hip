@@ -49,6 +49,9 @@ namespace xtk {
 namespace {
 
 constexpr int SLICE = 128;  // bytes of K per LDS row and K slice
+#ifndef XT_GEMM_NS
+#define XT_GEMM_NS 4
+#endif
 
 enum { kF16 = 0, kBF16 = 1, kI8 = 2 };
 
@@ -380,6 +383,236 @@ __global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(Gem
   }
 }
 
+// ---------------------------------------------------------------------------
+// 256 x 256 f16 / bf16 GEMM with an f32 result whose operands reach LDS by
+// DMA (buffer_load ... lds): no VGPR staging, no register transposes, no LDS
+// stores.
+//   * Four waves of 128 x 128 (4 x 4 tiles of v_mfma_f32_32x32x16), one per
+//     SIMD.  A stage is 32 K values: A [256 rows][64 B] and B [32 k][512 B],
+//     16 KB each, in one of NS LDS buffers (each its own LDS variable, so
+//     that reading one while DMA into others is in flight needs no wait).
+//   * A DMA instruction fills 1 KB of LDS, lane L at byte 16 L.  The layouts
+//     are swizzled by choosing which global chunk each lane fetches: A row r
+//     keeps its 16-byte chunk c at position c ^ ((r >> 2) & 3), so a
+//     16-lane phase of fragment reads (16 consecutive rows) hits 16 distinct
+//     16-byte bank groups; B row k keeps chunk c at c ^ 4 (k & 3), so the four
+//     rows a half-wave reads with ds_read_b64_tr_b16 fall in four different
+//     64-byte bank groups.
+//   * B fragments come straight from the [k][n] layout through
+//     ds_read_b64_tr_b16: lane l receives column l % 32 and k values
+//     8 (l / 32) + 4 h .. + 3 from read h, the operand layout of the MFMA.
+//   * Barrier B_s opens stage s.  Before it each wave waits for its own DMA
+//     of stages s and s + 1 and for its LDS reads; so after it every wave's
+//     DMA of both stages has landed and every wave is done with stage s - 1.
+//     Then the DMA of stage s + NS - 1 goes into stage s - 1's buffer, the
+//     stage's two K steps run (32 MFMAs a wave), and the first fragments of
+//     stage s + 1 are read before B_{s+1}, so no barrier is followed by an
+//     LDS round trip.  A stage's DMA has NS - 2 stages of compute to land.
+//     The barrier is a bare s_barrier: __syncthreads' release fence would
+//     also wait for the DMA that should stay in flight.
+// One 16-byte-per-lane LDS DMA: lane L's 16 bytes from rsrc at voff + soff
+// land at LDS byte lds + 16 L.  Issued as inline assembly so that the
+// compiler does not track it: the kernel accounts for these loads itself
+// (explicit vmcnt waits before every barrier), and the compiler, which cannot
+// tell the kernel's LDS buffers apart reliably, would otherwise wait for every
+// DMA in flight before the next LDS read.  M0 carries the LDS address and is
+// restored afterwards.
+__device__ __forceinline__ void dma16(int4v rsrc, unsigned lds, unsigned voff, unsigned soff) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory");
+}
+
+__device__ __forceinline__ int4v raw_rsrc(const void* base) {
+  const unsigned long long b = reinterpret_cast<unsigned long long>(base);
+  return int4v{(int)(unsigned)b, (int)(unsigned)(b >> 32) & 0xFFFF, (int)0xFFFFFFFF, 0x00020000};
+}
+
+template <int ELEM, int NS>
+__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
+  static_assert(NS >= 3 && NS <= 5, "stages");
+  constexpr int BM = 256, BN = 256, WM = 128, WN = 128, MI = 4, NI = 4;
+  constexpr int KB = 64;            // K bytes per A row and stage
+  constexpr int AB = BM * KB;       // A bytes per stage
+  constexpr int BR = BN * 2;        // B bytes per k row
+  constexpr int STAGE = AB + 32 * BR;
+  constexpr int PER = 8;            // DMA instructions per wave and stage
+  typedef __attribute__((address_space(3))) unsigned char lds_t;
+  __shared__ __attribute__((aligned(1024))) unsigned char S0[STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char S1[STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char S2[STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char S3[NS > 3 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char S4[NS > 4 ? STAGE : 16];
+  unsigned char* const buf[5] = {S0, S1, S2, S3, S4};
+  auto lds_addr = [](const unsigned char* q) {
+    return (unsigned)reinterpret_cast<uintptr_t>((const lds_t*)q);
+  };
+
+  const TilePtrs t = gemm_tile_of<ELEM, BM, BN>(p);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int4v ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
+  const unsigned lda = (unsigned)(p.lda * 2), ldb = (unsigned)(p.ldb * 2);
+  const int nk = p.nk * 2;  // stages of 32 K values (>= 2)
+
+  // DMA lane offsets.  A instruction i (rows 16i .. 16i+15): lane L holds
+  // row 16i + L/4 at position L%4, i.e. chunk (L%4) ^ ((L/16) & 3).  B
+  // instruction i (k rows 2i, 2i+1): lane (h, pc) = (L/32, L%32) holds
+  // chunk pc ^ 4 ((2i + h) & 3).
+  const unsigned va = (unsigned)(lane >> 2) * lda + (unsigned)(((lane & 3) ^ ((lane >> 4) & 3)) << 4);
+  unsigned vb[2];
+  {
+    const int h = lane >> 5, pc = lane & 31;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) vb[q] = (unsigned)h * ldb + (unsigned)((pc ^ (4 * ((2 * q + h) & 3))) << 4);
+  }
+  // this wave's share of stage kt: A instructions 4w .. 4w+3, B the same
+  auto dma = [&](int kt, unsigned char* S) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = wave * 4 + q;
+      dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kt * KB);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = wave * 4 + q;
+      dma16(rb, lds_addr(S + AB + i * 1024), vb[q & 1], (unsigned)(kt * 32 + 2 * i) * ldb);
+    }
+  };
+
+  // fragment offsets: A row r at r * 64, chunk c at c ^ ((r >> 2) & 3); B per
+  // (tile j, read h) an offset in the stage's first K step, plus 16 rows for
+  // the second
+  const int lrow = lane & 31, hi = lane >> 5;
+  int arow[MI], asw[MI], boff[NI][2];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int r = wm * WM + i * 32 + lrow;
+    arow[i] = r * KB;
+    asw[i] = (r >> 2) & 3;
+  }
+  {
+    const int g = lane >> 4, li = lane & 15;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
+        const int cb = (wn * WN + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
+        boff[j][h] = AB + k * BR + (((cb >> 4) ^ (4 * (k & 3))) << 4) + (cb & 15);
+      }
+  }
+  uint4v af[2][MI], bfr[2][NI];
+  auto read_frags = [&](const unsigned char* S, int ks, int set) {
+    const int c = ks * 2 + hi;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+      af[set][i] = *reinterpret_cast<const uint4v*>(S + arow[i] + ((c ^ asw[i]) << 4));
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          reinterpret_cast<short4v __attribute__((address_space(3)))*>((lds_t*)(S + ks * 16 * BR + boff[j][0])));
+      const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          reinterpret_cast<short4v __attribute__((address_space(3)))*>((lds_t*)(S + ks * 16 * BR + boff[j][1])));
+      const uint2v l2 = __builtin_bit_cast(uint2v, lo), h2 = __builtin_bit_cast(uint2v, h4);
+      bfr[set][j] = uint4v{l2[0], l2[1], h2[0], h2[1]};
+    }
+  };
+
+  float16v acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+  // vmcnt(n) alone (gfx9 encoding: expcnt and lgkmcnt fields at their
+  // maxima).  The LDS reads need no wait before a barrier: those of the
+  // stage whose buffer the next DMA overwrites were consumed by its MFMAs,
+  // and the prefetched reads target a buffer no DMA touches until later.
+#define XT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
+  // prologue: stages 0 .. NS-2 in flight; 0 and 1 landed before B_0
+#pragma unroll
+  for (int q = 0; q < NS - 1; ++q)
+    if (q < nk) dma(q, buf[q]);
+  if (nk >= NS - 1) XT_WAIT_VM(PER * (NS - 3));
+  else XT_WAIT_VM(0);
+  asm volatile("s_barrier" ::: "memory");
+  read_frags(buf[0], 0, 0);
+
+  auto stage = [&](int s, unsigned char* S, const unsigned char* Snext, unsigned char* Sfree) {
+    // the first MFMAs go out before the DMA instructions, so the matrix pipe
+    // is busy while they issue
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[0][j] = mfma<ELEM>(af[0][0], bfr[0][j], acc[0][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + NS - 1 < nk) dma(s + NS - 1, Sfree);
+    read_frags(S, 1, 1);
+#pragma unroll
+    for (int i = 1; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] = mfma<ELEM>(af[0][i], bfr[0][j], acc[i][j]);
+    // unconditional (the last stage reads a buffer it never uses), so that
+    // the waits for this step's fragments do not cover these reads
+    read_frags(Snext, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) acc[i][j] = mfma<ELEM>(af[1][i], bfr[1][j], acc[i][j]);
+    // each K step's 12 fragment reads (4 A, 8 B) ride behind the previous
+    // step's MFMAs, one read per MFMA
+#pragma unroll
+    for (int g = 0; g < 12; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+    }
+#pragma unroll
+    for (int g = 0; g < 12; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    // B_{s+1}: this wave's DMA of stage s + 2 landed (stages s+3 .. s+NS-1
+    // may stay in flight), its reads done
+    if (s + NS - 1 < nk) XT_WAIT_VM(PER * (NS - 3));
+    else XT_WAIT_VM(0);
+    asm volatile("s_barrier" ::: "memory");
+  };
+  for (int s0 = 0; s0 < nk; s0 += NS) {
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+      if (s0 + q < nk) stage(s0 + q, buf[q], buf[(q + 1) % NS], buf[(q + NS - 1) % NS]);
+  }
+#undef XT_WAIT_VM
+
+  const bool hs = p.has_scale, hb = p.has_bias;
+  // D = A x B per 32x32 tile: lane l holds output column l%32 of tile j and
+  // register v row 8*(v/4) + 4*(l/32) + v%4 of tile i; a half-wave writes one
+  // whole 128-byte line per register.
+  const int orow = hi * 4;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int n = wn * WN + j * 32 + lrow;
+    const float sv = hs ? t.S[n] : 1.f, bv = hb ? t.Bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const long long off = t.c_off + (long long)(wm * WM + i * 32 + (v >> 2) * 8 + orow + (v & 3)) * p.ldc + n;
+        static_cast<float*>(p.c)[off] = scale_bias(acc[i][j][v], sv, bv, hs, hb);
+      }
+  }
+}
+
 TileOff to_off(const xt::TileAddr& a) { return TileOff{a.c0, a.sx, a.sy, a.sz}; }
 
 bool offs_multiple(const xt::TileAddr& a, long long m) {
@@ -437,6 +670,11 @@ Cover cover_dim(const xt::Plan& p, long long w, bool is_m) {
 template <int ELEM, bool OUT_I8>
 void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
   const dim3 grid(a.nwg), block(256);
+  if constexpr (ELEM != kI8 && !OUT_I8)
+    if (bm == 256) {
+      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, XT_GEMM_NS>), grid, block, 0, s, a);
+      return;
+    }
   if (bm == 256) hipLaunchKernelGGL((gemm_kernel<ELEM, 256, 256, OUT_I8>), grid, block, 0, s, a);
   else if (bm == 128) hipLaunchKernelGGL((gemm_kernel<ELEM, 128, 128, OUT_I8>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((gemm_kernel<ELEM, 64, 64, OUT_I8>), grid, block, 0, s, a);
