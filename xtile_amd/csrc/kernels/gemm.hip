@@ -52,6 +52,15 @@ constexpr int SLICE = 128;  // bytes of K per LDS row and K slice
 #ifndef XT_GEMM_NS
 #define XT_GEMM_NS 4
 #endif
+#ifndef XT_GEMM_RORD
+#define XT_GEMM_RORD 0
+#endif
+#ifndef XT_GEMM_NT
+#define XT_GEMM_NT 1
+#endif
+#ifndef XT_GEMM_GROUP
+#define XT_GEMM_GROUP 8
+#endif
 
 enum { kF16 = 0, kBF16 = 1, kI8 = 2 };
 
@@ -511,20 +520,31 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
       }
   }
   uint4v af[2][MI], bfr[2][NI];
+  auto read_a = [&](const unsigned char* S, int ks, int set, int i) {
+    af[set][i] = *reinterpret_cast<const uint4v*>(S + arow[i] + (((ks * 2 + hi) ^ asw[i]) << 4));
+  };
+  auto read_b = [&](const unsigned char* S, int ks, int set, int j) {
+    const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<short4v __attribute__((address_space(3)))*>((lds_t*)(S + ks * 16 * BR + boff[j][0])));
+    const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<short4v __attribute__((address_space(3)))*>((lds_t*)(S + ks * 16 * BR + boff[j][1])));
+    const uint2v l2 = __builtin_bit_cast(uint2v, lo), h2 = __builtin_bit_cast(uint2v, h4);
+    bfr[set][j] = uint4v{l2[0], l2[1], h2[0], h2[1]};
+  };
   auto read_frags = [&](const unsigned char* S, int ks, int set) {
-    const int c = ks * 2 + hi;
+#if XT_GEMM_RORD
+    // in the order the MFMAs consume them: B0 A0 B1 A1 ...
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
-      af[set][i] = *reinterpret_cast<const uint4v*>(S + arow[i] + ((c ^ asw[i]) << 4));
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          reinterpret_cast<short4v __attribute__((address_space(3)))*>((lds_t*)(S + ks * 16 * BR + boff[j][0])));
-      const short4v h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          reinterpret_cast<short4v __attribute__((address_space(3)))*>((lds_t*)(S + ks * 16 * BR + boff[j][1])));
-      const uint2v l2 = __builtin_bit_cast(uint2v, lo), h2 = __builtin_bit_cast(uint2v, h4);
-      bfr[set][j] = uint4v{l2[0], l2[1], h2[0], h2[1]};
+    for (int q = 0; q < 4; ++q) {
+      read_b(S, ks, set, q);
+      read_a(S, ks, set, q);
     }
+#else
+#pragma unroll
+    for (int i = 0; i < MI; ++i) read_a(S, ks, set, i);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) read_b(S, ks, set, j);
+#endif
   };
 
   float16v acc[MI][NI];
@@ -608,7 +628,11 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const long long off = t.c_off + (long long)(wm * WM + i * 32 + (v >> 2) * 8 + orow + (v & 3)) * p.ldc + n;
+#if XT_GEMM_NT
+        __builtin_nontemporal_store(scale_bias(acc[i][j][v], sv, bv, hs, hb), static_cast<float*>(p.c) + off);
+#else
         static_cast<float*>(p.c)[off] = scale_bias(acc[i][j][v], sv, bv, hs, hb);
+#endif
       }
   }
 }
@@ -771,7 +795,7 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
     return hipErrorInvalidValue;
   }
   a.nwg = static_cast<int>(nwg);
-  a.group = 8;
+  a.group = XT_GEMM_GROUP;
   const bool out_i8 = p.c.elem == xt::Elem::I8;
   switch (p.a.elem) {
     case xt::Elem::I8: out_i8 ? launch_t<kI8, true>(bm, a, s) : launch_t<kI8, false>(bm, a, s); break;
