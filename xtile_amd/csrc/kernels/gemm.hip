@@ -17,7 +17,11 @@
 // and bias columns).  Blocks are independent (README.md:85-89), so both are
 // pure scheduling choices.
 //
-// One kernel template for BM x BN in {256 x 256, 128 x 128, 64 x 64}:
+// f16 / bf16 programs with an f32 result and 256 x 256 workgroup tiles run on
+// gemm_dma_kernel (operands landed in LDS by DMA; described where it is
+// defined).  The
+// rest (i8, i8 results, smaller tiles) run on gemm_kernel, one template for
+// BM x BN in {256 x 256, 128 x 128, 64 x 64}:
 //   * 4 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_{f16,bf16} or
 //     v_mfma_i32_32x32x32_i8.  Every fragment is 16 bytes per lane, so one
 //     K slice is 128 bytes of every row whatever the element type (64 f16/bf16
@@ -49,18 +53,8 @@ namespace xtk {
 namespace {
 
 constexpr int SLICE = 128;  // bytes of K per LDS row and K slice
-#ifndef XT_GEMM_NS
-#define XT_GEMM_NS 4
-#endif
-#ifndef XT_GEMM_RORD
-#define XT_GEMM_RORD 0
-#endif
-#ifndef XT_GEMM_NT
-#define XT_GEMM_NT 1
-#endif
-#ifndef XT_GEMM_GROUP
-#define XT_GEMM_GROUP 8
-#endif
+constexpr int kDmaStages = 4;  // K stages of gemm_dma_kernel in LDS (3: 168 us on C3, 5: 135-137, 4: 131)
+constexpr int kTileGroup = 8;  // tile columns per group of the workgroup order
 
 enum { kF16 = 0, kBF16 = 1, kI8 = 2 };
 
@@ -532,19 +526,10 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
     bfr[set][j] = uint4v{l2[0], l2[1], h2[0], h2[1]};
   };
   auto read_frags = [&](const unsigned char* S, int ks, int set) {
-#if XT_GEMM_RORD
-    // in the order the MFMAs consume them: B0 A0 B1 A1 ...
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      read_b(S, ks, set, q);
-      read_a(S, ks, set, q);
-    }
-#else
 #pragma unroll
     for (int i = 0; i < MI; ++i) read_a(S, ks, set, i);
 #pragma unroll
     for (int j = 0; j < NI; ++j) read_b(S, ks, set, j);
-#endif
   };
 
   float16v acc[MI][NI];
@@ -628,11 +613,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const long long off = t.c_off + (long long)(wm * WM + i * 32 + (v >> 2) * 8 + orow + (v & 3)) * p.ldc + n;
-#if XT_GEMM_NT
         __builtin_nontemporal_store(scale_bias(acc[i][j][v], sv, bv, hs, hb), static_cast<float*>(p.c) + off);
-#else
-        static_cast<float*>(p.c)[off] = scale_bias(acc[i][j][v], sv, bv, hs, hb);
-#endif
       }
   }
 }
@@ -696,7 +677,7 @@ void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
   const dim3 grid(a.nwg), block(256);
   if constexpr (ELEM != kI8 && !OUT_I8)
     if (bm == 256) {
-      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, XT_GEMM_NS>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages>), grid, block, 0, s, a);
       return;
     }
   if (bm == 256) hipLaunchKernelGGL((gemm_kernel<ELEM, 256, 256, OUT_I8>), grid, block, 0, s, a);
@@ -795,7 +776,7 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
     return hipErrorInvalidValue;
   }
   a.nwg = static_cast<int>(nwg);
-  a.group = XT_GEMM_GROUP;
+  a.group = kTileGroup;
   const bool out_i8 = p.c.elem == xt::Elem::I8;
   switch (p.a.elem) {
     case xt::Elem::I8: out_i8 ? launch_t<kI8, true>(bm, a, s) : launch_t<kI8, false>(bm, a, s); break;
