@@ -19,9 +19,8 @@
 //
 // f16 / bf16 programs with an f32 result and 256 x 256 workgroup tiles run on
 // gemm_dma_kernel (operands landed in LDS by DMA; described where it is
-// defined).  The
-// rest (i8, i8 results, smaller tiles) run on gemm_kernel, one template for
-// BM x BN in {256 x 256, 128 x 128, 64 x 64}:
+// defined).  The rest (i8, i8 results, smaller tiles) run on gemm_kernel, one
+// template for BM x BN in {256 x 256, 128 x 128, 64 x 64}:
 //   * 4 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_{f16,bf16} or
 //     v_mfma_i32_32x32x32_i8.  Every fragment is 16 bytes per lane, so one
 //     K slice is 128 bytes of every row whatever the element type (64 f16/bf16
