@@ -15,6 +15,43 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 typedef unsigned int uint4v __attribute__((ext_vector_type(4)));
 typedef unsigned int uint2v __attribute__((ext_vector_type(2)));
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer descriptor (stride 0, `bytes` records): offsets at or past
+// `bytes` read as zero.
+__device__ __forceinline__ i32x4 raw_rsrc(const void* base, unsigned bytes = 0xFFFFFFFFu) {
+  const unsigned long long b = reinterpret_cast<unsigned long long>(base);
+  return i32x4{(int)(unsigned)b, (int)(unsigned)(b >> 32) & 0xFFFF, (int)bytes, 0x00020000};
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) unsigned char*)p);
+}
+
+// One 16-byte-per-lane LDS DMA: lane L's 16 bytes from rsrc at voff + soff
+// land at LDS byte lds + 16 L (lanes off in exec write nothing).  Issued as
+// inline assembly so that the compiler does not track it: kernels using it
+// account for these loads themselves (explicit vmcnt waits before their
+// barriers), where the compiler, which cannot tell LDS buffers apart
+// reliably, would wait for every DMA in flight before the next LDS read.
+// M0 carries the LDS address and is restored afterwards.
+__device__ __forceinline__ void dma16(i32x4 rsrc, unsigned lds, unsigned voff, unsigned soff) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory");
+}
+
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: expcnt and lgkmcnt fields at
+// their maxima), n < 64.
+#define XTK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
+
 // Affine element offset of a tile origin: c0 + x*sx + y*sy + z*sz
 // (the host folds tile coordinates, tile shape and memref strides into it).
 struct TileOff {

@@ -412,30 +412,6 @@ __global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(Gem
 //     LDS round trip.  A stage's DMA has NS - 2 stages of compute to land.
 //     The barrier is a bare s_barrier: __syncthreads' release fence would
 //     also wait for the DMA that should stay in flight.
-// One 16-byte-per-lane LDS DMA: lane L's 16 bytes from rsrc at voff + soff
-// land at LDS byte lds + 16 L.  Issued as inline assembly so that the
-// compiler does not track it: the kernel accounts for these loads itself
-// (explicit vmcnt waits before every barrier), and the compiler, which cannot
-// tell the kernel's LDS buffers apart reliably, would otherwise wait for every
-// DMA in flight before the next LDS read.  M0 carries the LDS address and is
-// restored afterwards.
-__device__ __forceinline__ void dma16(int4v rsrc, unsigned lds, unsigned voff, unsigned soff) {
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-      : "memory");
-}
-
-__device__ __forceinline__ int4v raw_rsrc(const void* base) {
-  const unsigned long long b = reinterpret_cast<unsigned long long>(base);
-  return int4v{(int)(unsigned)b, (int)(unsigned)(b >> 32) & 0xFFFF, (int)0xFFFFFFFF, 0x00020000};
-}
-
 template <int ELEM, int NS>
 __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   static_assert(NS >= 3 && NS <= 5, "stages");
@@ -452,16 +428,13 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) unsigned char S3[NS > 3 ? STAGE : 16];
   __shared__ __attribute__((aligned(1024))) unsigned char S4[NS > 4 ? STAGE : 16];
   unsigned char* const buf[5] = {S0, S1, S2, S3, S4};
-  auto lds_addr = [](const unsigned char* q) {
-    return (unsigned)reinterpret_cast<uintptr_t>((const lds_t*)q);
-  };
 
   const TilePtrs t = gemm_tile_of<ELEM, BM, BN>(p);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int4v ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
+  const i32x4 ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
   const unsigned lda = (unsigned)(p.lda * 2), ldb = (unsigned)(p.ldb * 2);
   const int nk = p.nk * 2;  // stages of 32 K values (>= 2)
 
@@ -539,11 +512,10 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-  // vmcnt(n) alone (gfx9 encoding: expcnt and lgkmcnt fields at their
-  // maxima).  The LDS reads need no wait before a barrier: those of the
-  // stage whose buffer the next DMA overwrites were consumed by its MFMAs,
-  // and the prefetched reads target a buffer no DMA touches until later.
-#define XT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
+  // The LDS reads need no wait before a barrier: those of the stage whose
+  // buffer the next DMA overwrites were consumed by its MFMAs, and the
+  // prefetched reads target a buffer no DMA touches until later.
+#define XT_WAIT_VM(n) XTK_WAIT_VM(n)
   // prologue: stages 0 .. NS-2 in flight; 0 and 1 landed before B_0
 #pragma unroll
   for (int q = 0; q < NS - 1; ++q)
