@@ -163,3 +163,55 @@ def test_softmax_special_rows_c2_shape(cuda):
     for rs in where.values():
         plain[rs] = False
     np.testing.assert_allclose(got[plain].sum(axis=1), 1.0, rtol=0, atol=1e-5)
+
+
+def _ftoi_reference(y: np.ndarray) -> np.ndarray:
+    """astype(int8) as xt.ftoi defines it: NaN -> 0, round half to even,
+    saturate to [-128, 127]."""
+    with np.errstate(invalid="ignore"):
+        r = np.rint(np.nan_to_num(y.astype(np.float64), nan=0.0, posinf=1e300, neginf=-1e300))
+    return np.clip(r, -128, 127).astype(np.int8)
+
+
+@pytest.mark.parametrize("mn", [512, 384])
+def test_matmul_i8_epilogue_special_values(cuda, mn):
+    """kernels/matmul.py's epilogue t * scale + bias -> astype(int8) at the
+    values that decide a float -> i8 conversion: scale or bias NaN, +-inf, -0,
+    huge (past the i32 range), and exact halves (A, B in {-1, 0, 1} and scale
+    0.5 make most outputs k + 0.5, which must round to even).  512 x 512 runs
+    on the 256 x 256 DMA kernel, 384 x 384 on the 128 x 128 staged kernel.
+    Checked bit for bit against the oracle and against the closed form above
+    (the products are exact small integers, so t * s + b is one f32 multiply
+    and one f32 add)."""
+    m_ = n_ = mn
+    k_ = 256
+    rng = np.random.default_rng(11)
+    a = rng.integers(-1, 2, (m_, k_), dtype=np.int8)
+    b = rng.integers(-1, 2, (k_, n_), dtype=np.int8)
+    s = np.full((1, n_), 0.5, np.float32)
+    bias = np.zeros((1, n_), np.float32)
+    special = [
+        (np.nan, 0.0), (np.inf, 0.0), (-np.inf, 0.0), (0.0, np.inf), (0.0, -np.inf), (1.0, np.nan),
+        (1.0, 3e38), (1.0, -3e38), (1e30, 0.0), (-1e30, 0.0), (-0.0, -0.0), (0.5, 0.5), (0.5, -0.5),
+        (-0.5, 0.0), (0.25, 0.0), (1.5, 0.25), (3.0, 0.5), (1e-45, 0.0), (0.5, 127.5), (0.5, -128.5),
+    ]
+    for c0 in range(0, n_, 32):  # every 32 columns: every wave, tile and lane group
+        for i, (sv, bv) in enumerate(special):
+            s[0, c0 + i] = sv
+            bias[0, c0 + i] = bv
+    mod = K.matmul_i8(m_, n_, k_, 64, 64)
+    c = np.zeros((m_, n_), np.int8)
+    got = run_gpu(mod, [a, b, c, s, bias], ["i8", "i8", "i8", "f32", "f32"], cuda,
+                  case=f"mm i8 epilogue special values {m_}x{n_}x{k_}")[2]
+    want = run_oracle(mod, [a, b, c, s, bias], oracle_threads())[2]
+    assert np.array_equal(want, got)
+    acc = a.astype(np.int64) @ b.astype(np.int64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        t = acc.astype(np.float32) * s
+        y = (t + bias).astype(np.float32)
+    assert np.array_equal(_ftoi_reference(y), got)
+    # the ties really occur, and NaN columns give 0
+    with np.errstate(invalid="ignore"):
+        ties = (np.abs(y - np.floor(y)) == 0.5) & (np.abs(y) < 128)
+    assert np.count_nonzero(ties) > m_ * n_ // 4
+    assert np.all(got[:, 0] == 0) and np.all(got[:, 5] == 0)

@@ -16,6 +16,7 @@ typedef unsigned int uint4v __attribute__((ext_vector_type(4)));
 typedef unsigned int uint2v __attribute__((ext_vector_type(2)));
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int int2v __attribute__((ext_vector_type(2)));
 
 // A raw buffer descriptor (stride 0, `bytes` records): offsets at or past
 // `bytes` read as zero.

@@ -484,7 +484,6 @@ struct BandArgs {
 enum { kBandF16 = 0, kBandBF16 = 1, kBandI8 = 2 };
 typedef int int4v __attribute__((ext_vector_type(4)));
 typedef int int16v __attribute__((ext_vector_type(16)));
-typedef int int2v __attribute__((ext_vector_type(2)));
 
 // f16 / bf16 accumulate in f32; i8 in i32 (exact), converted to f32 when stored.
 template <int ELEM>
