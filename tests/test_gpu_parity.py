@@ -52,6 +52,35 @@ def test_add_rows_reference_program(cuda):
     assert np.array_equal(got, a + b)
 
 
+@pytest.mark.parametrize("swap_b", [False, True])
+@pytest.mark.parametrize("rows,cols,th,tw,grid", [(1024, 1024, 32, 64, (32, 16)), (96, 100, 24, 100, (4, 1)),
+                                                   (128, 128, 32, 32, (4, 4)), (256, 64, 16, 16, (8, 4))])
+def test_add_flat_and_tiled_forms(cuda, rows, cols, th, tw, grid, swap_b):
+    """Programs whose tiles cover one contiguous run of every operand run as
+    one flat stream (the planner says flat=N); a transposed Block index in B
+    keeps the tiled kernel.  Both bit-exact against numpy on the covered
+    region; elements outside it keep their prior contents."""
+    from tests.test_plan import _ew_program
+
+    if swap_b and (th != tw or rows != cols):
+        pytest.skip("a transposed index needs square tiles over a square array")
+    rng = np.random.default_rng(5)
+    m = _ew_program(rows, cols, th, tw, grid, swap_b=swap_b)
+    kernel = xt.plan(m)["kernel"]
+    assert ("flat=" in kernel) == (not swap_b)
+    a = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    b = rng.uniform(-1, 1, (rows, cols)).astype(np.float32)
+    c0 = rng.uniform(5, 6, (rows, cols)).astype(np.float32)
+    got = run_gpu(m, [a, b, c0.copy()], ["f32"] * 3, cuda, case=f"add {rows}x{cols} tile {th}x{tw} swap={swap_b}")[2]
+    want = c0.copy()
+    for x in range(grid[0]):
+        for y in range(grid[1]):
+            bx, by = (y, x) if swap_b else (x, y)
+            want[x * th:(x + 1) * th, y * tw:(y + 1) * tw] = (
+                a[x * th:(x + 1) * th, y * tw:(y + 1) * tw] + b[bx * th:(bx + 1) * th, by * tw:(by + 1) * tw])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("op", ["sub", "mul"])
 def test_sub_mul_bit_exact(cuda, op):
     text = f"""

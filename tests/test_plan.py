@@ -12,7 +12,7 @@ from xtile_amd import kernels as K
 @pytest.mark.parametrize(
     "name,kernel,nbytes,nflops",
     [
-        ("c1_add", "ew_binary op=add f32 tile=32x64 grid=(32,16,1)", 12582912, 0),
+        ("c1_add", "ew_binary op=add f32 tile=32x64 flat=1048576 grid=(32,16,1)", 12582912, 0),
         ("c2_softmax", "row_softmax f32 tile=1x4096 grid=(8192,1,1)", 268435456, 0),
         ("c3_matmul_f16", "gemm f16->f32 tile=128x128 k=4096 grid=(32,32,1)", 134217728, 137438953472),
         ("c4_conv2d_f16", "conv2d_nhwc f16->f32 tile=1x4x56x64 filter=3x3x64x64 grid=(32,14,1)", 38608896, 7398752256),
@@ -33,6 +33,55 @@ def test_benchmark_configs_plan(name, kernel, nbytes, nflops):
 def test_reference_kernel_forms_plan():
     assert xt.plan(K.add_rows(128, 128, 64))["kernel"].startswith("ew_binary")
     assert xt.plan(K.softmax(128, 64, 64))["kernel"] == "row_softmax f32 tile=64x64 grid=(2,1,1)"
+
+
+def _ew_program(rows, cols, th, tw, grid, swap_b=False, shared_b=0):
+    """store(load A + load B) over rows x cols f32 memrefs, th x tw tiles;
+    B's tile index optionally transposed or shared."""
+    from xtile_amd import Array, bid, convert, float32, kernel, load, store
+
+    @kernel
+    def prog(a, b, c):
+        x = bid(0)
+        y = bid(1)
+        ta = load(a, index=(x, y), shape=(th, tw))
+        tb = load(b, index=(y, x) if swap_b else (x, y), shape=(th, tw), shared=shared_b)
+        store(c, index=(x, y), tile=ta + tb)
+
+    t = Array(shape=(rows, cols), dtype=float32)
+    return convert(prog, args=(t, t, t), grid=(grid[0], grid[1], 1))
+
+
+@pytest.mark.parametrize(
+    "rows,cols,th,tw,grid,flat",
+    [
+        (1024, 1024, 32, 64, (32, 16), 1024 * 1024),  # C1: the tiles cover the whole array
+        (64, 256, 64, 256, (1, 1), 64 * 256),          # one Block
+        (256, 128, 8, 128, (32, 1), 256 * 128),        # full-width row tiles
+        (128, 64, 16, 32, (4, 2), 64 * 64),            # the grid covers the first 64 full rows: one run
+        (128, 64, 32, 16, (4, 2), 0),                  # the grid covers half of each row: holes
+        (128, 64, 16, 16, (8, 4), 128 * 64),           # every tile, Blocks of 16 x 16
+    ],
+)
+def test_elementwise_flat_run(rows, cols, th, tw, grid, flat):
+    """The Blocks of store(load A + load B) run as one flat stream exactly when
+    their tiles cover one contiguous run of every operand, each element once, at
+    the same positions."""
+    kernel = xt.plan(_ew_program(rows, cols, th, tw, grid))["kernel"]
+    assert kernel.startswith("ew_binary")
+    assert (f" flat={flat} " in kernel) if flat else ("flat=" not in kernel)
+
+
+def test_elementwise_flat_run_needs_the_same_walk():
+    """A transposed Block index in one operand or a shared operand whose index
+    the leader rule pins: B's tiles no longer sit at A's and C's positions of
+    the run, so the tiled kernel keeps the Blocks."""
+    base = dict(rows=128, cols=128, th=32, tw=32, grid=(4, 4))
+    assert " flat=16384 " in xt.plan(_ew_program(**base))["kernel"]
+    assert "flat=" not in xt.plan(_ew_program(**base, swap_b=True))["kernel"]
+    assert "flat=" not in xt.plan(_ew_program(**base, shared_b=1))["kernel"]
+    # with one Block along axis 0 the shared rule changes nothing: B walks like A
+    assert " flat=4096 " in xt.plan(_ew_program(32, 128, 32, 32, (1, 4), shared_b=1))["kernel"]
 
 
 def test_compile_returns_module_and_keeps_text():

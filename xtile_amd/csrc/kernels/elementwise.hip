@@ -101,6 +101,39 @@ __global__ __launch_bounds__(256) void ew_binary_kernel(EwArgs p) {
   }
 }
 
+// The flat form of a program whose Blocks' tiles cover one contiguous run in
+// every operand at the same relative positions: c[i] = a[i] op b[i] over the
+// run, 512 float4 per workgroup (two per thread, all four loads issued before
+// the first use).  One Block's work is then spread over several workgroups and
+// one workgroup covers parts of several Blocks; both are pure scheduling,
+// since Blocks are independent.  For C1 (1024 x 1024, 32 x 64 tiles) this
+// measured 3.25 us per launch against 4.05 us for the tiled kernel with its
+// Block decode and per-row addressing.
+template <int OP>
+__global__ __launch_bounds__(256) void ew_flat_kernel(const float4v* __restrict__ a, const float4v* __restrict__ b,
+                                                      float4v* __restrict__ c, long long nv) {
+  const long long base = (long long)blockIdx.x * 512 + threadIdx.x;
+  float4v va[2], vb[2];
+  bool ok[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const long long i = base + u * 256;
+    ok[u] = i < nv;
+    va[u] = ld_nt(a + (ok[u] ? i : 0));
+    vb[u] = ld_nt(b + (ok[u] ? i : 0));
+  }
+  issue_fence();
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    float4v vc;
+    vc.x = ew_apply<OP>(va[u].x, vb[u].x);
+    vc.y = ew_apply<OP>(va[u].y, vb[u].y);
+    vc.z = ew_apply<OP>(va[u].z, vb[u].z);
+    vc.w = ew_apply<OP>(va[u].w, vb[u].w);
+    if (ok[u]) st_nt(vc, c + base + u * 256);
+  }
+}
+
 struct SoftmaxArgs {
   const float* x;
   float* y;
@@ -346,6 +379,26 @@ hipError_t launch_ew_binary(const xt::Plan& p, void* const* bufs, hipStream_t s,
     return hipErrorInvalidValue;
   }
   const bool vec = aligned4(p.a, a.a) && aligned4(p.b, a.b) && aligned4(p.c, a.c);
+  if (p.ew_flat > 0 && p.ew_flat % 4 == 0 && vec) {
+    // aligned4 checked every operand's origin and pitch: the run starts on a
+    // 16-byte boundary in each
+    const long long nv = p.ew_flat / 4;
+    const long long wgs = (nv + 511) / 512;
+    if (!grid_fits(wgs, 256)) {
+      why = "elementwise run of " + std::to_string(p.ew_flat) + " elements exceeds one launch";
+      return hipErrorInvalidValue;
+    }
+    const float4v* fa = reinterpret_cast<const float4v*>(a.a + p.a.addr.c0);
+    const float4v* fb = reinterpret_cast<const float4v*>(a.b + p.b.addr.c0);
+    float4v* fc = reinterpret_cast<float4v*>(a.c + p.c.addr.c0);
+    const dim3 grid(static_cast<unsigned>(wgs)), block(256);
+    switch (p.ew_op) {
+      case xt::EwOp::Add: hipLaunchKernelGGL(ew_flat_kernel<0>, grid, block, 0, s, fa, fb, fc, nv); break;
+      case xt::EwOp::Sub: hipLaunchKernelGGL(ew_flat_kernel<1>, grid, block, 0, s, fa, fb, fc, nv); break;
+      default: hipLaunchKernelGGL(ew_flat_kernel<2>, grid, block, 0, s, fa, fb, fc, nv); break;
+    }
+    return hipGetLastError();
+  }
   const int vw = vec ? 4 : 1;
   const long long cv = a.cols / vw;
   const long long nvec = static_cast<long long>(a.rows) * cv;

@@ -52,7 +52,7 @@ namespace xtk {
 namespace {
 
 constexpr int SLICE = 128;  // bytes of K per LDS row and K slice
-constexpr int kDmaStages = 4;  // K stages of gemm_dma_kernel in LDS (3: 168 us on C3, 5: 135-137, 4: 131)
+constexpr int kDmaStages = 4;  // K stages of gemm_dma_kernel in LDS (C3 in one harness: 3 stages 130.6 us, 4: 131.6, 5: 124.4; in bench.py 4 and 5 both 129.7)
 constexpr int kTileGroup = 8;  // tile columns per group of the workgroup order
 
 enum { kF16 = 0, kBF16 = 1, kI8 = 2 };

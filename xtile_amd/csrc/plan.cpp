@@ -13,7 +13,6 @@
 #include "plan.h"
 
 #include <algorithm>
-
 #include <map>
 #include <set>
 #include <cstdlib>
@@ -287,6 +286,34 @@ bool check_independent(const Analysis& an, std::string& err) {
 
 // -- EwBinary ----------------------------------------------------------------
 
+// Element (Block x, y, z; row r, column c) of an access sits at
+// c0 + c + r*ld + x*sx + y*sy + z*sz: a mixed-radix number whose digits are the
+// column, the row and the grid axes of extent > 1.  When those (stride,
+// extent) pairs, sorted by stride, start at stride 1 and every stride is the
+// product of the extents before it, the map is a bijection onto
+// [c0, c0 + product of the extents): the tiles cover one contiguous run,
+// each element once.  Returns the run's length, or 0.
+int64_t contiguous_run(const Plan& p, const Access2D& a) {
+  std::vector<std::pair<int64_t, int64_t>> d;  // (stride, extent)
+  if (a.cols < 1 || a.rows < 1) return 0;
+  d.push_back({1, a.cols});
+  if (a.rows > 1) d.push_back({a.ld, a.rows});
+  const int64_t st[3] = {a.addr.sx, a.addr.sy, a.addr.sz};
+  for (int ax = 0; ax < 3; ++ax)
+    if (p.grid[ax] > 1) {
+      if (st[ax] <= 0) return 0;
+      d.push_back({st[ax], p.grid[ax]});
+    }
+  std::sort(d.begin(), d.end());
+  int64_t next = 1;
+  for (const auto& e : d) {
+    if (e.first != next) return 0;
+    if (next > (int64_t(1) << 40) / e.second) return 0;
+    next *= e.second;
+  }
+  return next;
+}
+
 bool match_ew(const Analysis& an, Plan& p, std::string& err) {
   int nstore = 0;
   const Op* st = only(an, "xt.store", nstore);
@@ -321,6 +348,13 @@ bool match_ew(const Analysis& an, Plan& p, std::string& err) {
   }
   p.kind = PlanKind::EwBinary;
   p.ew_op = bin->name == "xt.add" ? EwOp::Add : bin->name == "xt.sub" ? EwOp::Sub : EwOp::Mul;
+  // strides of grid axes of extent 1 never move a tile
+  auto same_walk = [&](const Access2D& x) {
+    return (p.grid[0] == 1 || x.addr.sx == p.c.addr.sx) && (p.grid[1] == 1 || x.addr.sy == p.c.addr.sy) &&
+           (p.grid[2] == 1 || x.addr.sz == p.c.addr.sz) && x.ld == p.c.ld && x.rows == p.c.rows &&
+           x.cols == p.c.cols;
+  };
+  p.ew_flat = same_walk(p.a) && same_walk(p.b) ? contiguous_run(p, p.c) : 0;
   double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
   double tile_bytes = double(ta.numel()) * 4;
   p.algo_bytes = blocks * tile_bytes * (la == lb ? 2 : 3);
@@ -878,6 +912,7 @@ std::string Plan::describe() const {
     case PlanKind::EwBinary:
       os << "ew_binary op=" << (ew_op == EwOp::Add ? "add" : ew_op == EwOp::Sub ? "sub" : "mul")
          << " f32 tile=" << tile(c);
+      if (ew_flat) os << " flat=" << ew_flat;
       break;
     case PlanKind::RowSoftmax:
       os << "row_softmax f32 tile=" << tile(a);

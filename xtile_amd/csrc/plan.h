@@ -114,6 +114,11 @@ struct Plan {
   // EwBinary: a op b -> c.   RowSoftmax: a -> c.   Gemm: a @ b -> c.
   Access2D a, b, c;
   EwOp ew_op = EwOp::Add;
+  // EwBinary: when every operand's tiles over the whole grid cover one
+  // contiguous run of elements, each once, and the same (Block, row, column)
+  // sits at the same position of every operand's run, the run's length (the
+  // Blocks then execute as one flat stream); 0 otherwise.
+  int64_t ew_flat = 0;
   int64_t gemm_k = 0;
   // Gemm epilogue (kernels/matmul.py:15-17): t * scale + bias with (1, TN)
   // row tiles, then an optional ftoi (the store's element type is then i8).
