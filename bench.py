@@ -566,7 +566,8 @@ def ceilings(pre: Preconditioner) -> dict:
     torch.cuda.empty_cache()
     out["note"] = ("include/xt_ceiling.h kernels, HIP graph replay: MFMA loop of 8 independent 32x32 MFMAs per "
                    "wave, 8 waves per CU, operands distributed like C3 (f16), C5 (bf16), C6 (i8); non-temporal "
-                   "float4 copy, 512 workgroups walking the array; empty kernel of 512 workgroups (C1's grid)")
+                   "float4 copy, one pass of a full grid (eight vectors a thread at 256 MiB, two at C1's size); "
+                   "empty kernel of 512 workgroups (C1's grid)")
     return out
 
 

@@ -18,9 +18,10 @@ extern "C" {
 #endif
 
 /* Streaming copy of `bytes` (a multiple of 16, both pointers 16-byte
- * aligned): at most 512 workgroups of 256 threads walk the array, each pass
- * issuing four 16-byte non-temporal loads per thread before the first
- * store.  Moves 2 * bytes through HBM. */
+ * aligned): one pass of a grid of 256-thread workgroups, each thread issuing
+ * its 16-byte non-temporal loads (two up to 32 MiB, eight beyond) before its
+ * first store; arrays of 32 GiB or more by 512 workgroups walking the array.
+ * Moves 2 * bytes through HBM. */
 int xt_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream);
 
 /* A kernel of `workgroups` 256-thread workgroups that does nothing: the

@@ -16,25 +16,29 @@ using xtk::uint4v;
 
 constexpr int kCopyU = 4;     // 16-byte vectors per thread per pass
 constexpr int kCopyWgs = 512;  // workgroups walking the array (two per CU)
+constexpr long long kOnePass = 1LL << 21;  // up to 32 MiB: one pass of a full grid
 
-// Grid-stride streaming copy: each pass issues the four loads of a thread
-// before its first store.  Of the streaming shapes measured on gfx950 (one-shot
-// grids of 256-1024 threads with 1-8 vectors a thread, temporal or
-// non-temporal accesses, 512-2048 persistent workgroups), 512 workgroups of
-// 256 threads walking the array gave the highest copy rate.
+// Streaming copy: each pass of a thread issues its U loads before its first
+// store.  Arrays of at most 32 MiB are copied in one pass of a full grid with
+// two vectors a thread (for C1's 12.6 MB 3.2-3.5 us a launch, where 512
+// walking workgroups took 3.8); larger ones in one pass with eight vectors a
+// thread (256 MiB: 6.33 TB/s, against 6.28 for two and 6.24 for four vectors
+// a thread, and 6.27-6.30 for 512 workgroups walking the array with four);
+// arrays beyond one launch's grid by 512 workgroups walking the array.
+template <int U>
 __global__ __launch_bounds__(256) void copy_kernel(const float4v* __restrict__ src, float4v* __restrict__ dst,
                                                    long long n) {
-  const long long stride = (long long)gridDim.x * 256 * kCopyU;
-  for (long long base = (long long)blockIdx.x * 256 * kCopyU + threadIdx.x; base < n; base += stride) {
-    float4v v[kCopyU];
+  const long long stride = (long long)gridDim.x * 256 * U;
+  for (long long base = (long long)blockIdx.x * 256 * U + threadIdx.x; base < n; base += stride) {
+    float4v v[U];
 #pragma unroll
-    for (int u = 0; u < kCopyU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const long long i = base + u * 256;
       v[u] = i < n ? __builtin_nontemporal_load(src + i) : float4v{0.f, 0.f, 0.f, 0.f};
     }
     xtk::issue_fence();
 #pragma unroll
-    for (int u = 0; u < kCopyU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const long long i = base + u * 256;
       if (i < n) __builtin_nontemporal_store(v[u], dst + i);
     }
@@ -102,10 +106,23 @@ int xt_ceiling_copy(const void* src, void* dst, size_t bytes, void* stream) {
   if (bytes % 16 || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
     return hipErrorInvalidValue;
   const long long n = static_cast<long long>(bytes / 16);
+  if (n < 1) return hipErrorInvalidValue;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (n <= kOnePass) {
+    const long long wgs = (n + 511) / 512;
+    hipLaunchKernelGGL(copy_kernel<2>, dim3(static_cast<unsigned>(wgs)), dim3(256), 0, s,
+                       static_cast<const float4v*>(src), static_cast<float4v*>(dst), n);
+    return hipGetLastError();
+  }
+  if (n < (1LL << 31)) {
+    const long long wgs = (n + 2047) / 2048;
+    hipLaunchKernelGGL(copy_kernel<8>, dim3(static_cast<unsigned>(wgs)), dim3(256), 0, s,
+                       static_cast<const float4v*>(src), static_cast<float4v*>(dst), n);
+    return hipGetLastError();
+  }
   long long wgs = (n + 256 * kCopyU - 1) / (256 * kCopyU);
-  if (wgs < 1) return hipErrorInvalidValue;
   if (wgs > kCopyWgs) wgs = kCopyWgs;
-  hipLaunchKernelGGL(copy_kernel, dim3(static_cast<unsigned>(wgs)), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(copy_kernel<kCopyU>, dim3(static_cast<unsigned>(wgs)), dim3(256), 0, s,
                      static_cast<const float4v*>(src), static_cast<float4v*>(dst), n);
   return hipGetLastError();
 }

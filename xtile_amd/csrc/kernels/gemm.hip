@@ -486,18 +486,16 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) vb[q] = (unsigned)h * ldb + (unsigned)((pc ^ bsw(RPI * q + h)) << 4);
   }
-  // this wave's share of stage kt: A instructions 4w .. 4w+3, B the same
+  // this wave's share of stage kt: A instructions 4w .. 4w+3 (q = 0..3), B
+  // the same (q = 4..7)
+  auto dma_one = [&](int kt, unsigned char* S, int q) {
+    const int i = wave * 4 + (q & 3);
+    if (q < 4) dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kt * KB);
+    else dma16(rb, lds_addr(S + AB + i * 1024), vb[q & 1], (unsigned)(kt * KR + RPI * i) * ldb);
+  };
   auto dma = [&](int kt, unsigned char* S) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = wave * 4 + q;
-      dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kt * KB);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = wave * 4 + q;
-      dma16(rb, lds_addr(S + AB + i * 1024), vb[q & 1], (unsigned)(kt * KR + RPI * i) * ldb);
-    }
+    for (int q = 0; q < PER; ++q) dma_one(kt, S, q);
   };
 
   // fragment offsets: A row r at r * 64, chunk c at c ^ ((r >> 2) & 3); B per
@@ -561,17 +559,19 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) read_b(S, ks, set, j);
   };
-  // MFMA number n of a K step: D = A x B, or D^T = B^T x A^T for an i8
-  // result.  Consecutive MFMAs keep their first operand (an A fragment, or
-  // for an i8 result a B fragment) for a run of four.
-  auto mma = [&](int set, int n) {
-    if constexpr (OUT_I8) {
-      const int j = n / MI, i = n % MI;
-      acc[i][j] = mfma<ELEM>(bfr[set][j], af[set][i], acc[i][j]);
-    } else {
-      const int i = n / NI, j = n % NI;
-      acc[i][j] = mfma<ELEM>(af[set][i], bfr[set][j], acc[i][j]);
-    }
+  // D = A x B, or D^T = B^T x A^T for an i8 result
+  auto mma = [&](int set, int i, int j) {
+    if constexpr (OUT_I8) acc[i][j] = mfma<ELEM>(bfr[set][j], af[set][i], acc[i][j]);
+    else acc[i][j] = mfma<ELEM>(af[set][i], bfr[set][j], acc[i][j]);
+  };
+  // MFMA n of a K step, in shells of max(i, j) (shell k holds n = k^2 ..
+  // k^2 + 2k: (0, k) .. (k-1, k), then (k, 0) .. (k, k)): the fragments of A
+  // row i and B column j are read in slot max(i, j) of the step before, so
+  // the first MFMAs of a step need only the earliest reads.
+  auto mma_n = [&](int set, int n) {
+    const int k = n < 1 ? 0 : n < 4 ? 1 : n < 9 ? 2 : 3, r = n - k * k;
+    if (r < k) mma(set, r, k);
+    else mma(set, k, r - k);
   };
 
   // The LDS reads need no wait before a barrier: those of the stage whose
@@ -587,37 +587,44 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   asm volatile("s_barrier" ::: "memory");
   read_frags(buf[0], 0, 0);
 
+  // A stage is eight slots of four MFMAs.  Slot g issues, in this order
+  // (sched_barrier fences keep the compiler from moving anything across):
+  // MFMA, this wave's DMA instruction g of stage s + NS - 1, MFMA, the A
+  // fragment read, MFMA, the two transposing reads of the B fragment, MFMA.
+  // Slots 0-3 run K step 0 on fragment set 0 and read set 1 (step 1, row and
+  // column g); slots 4-7 run step 1 and read the next stage's set 0.  Spread
+  // out this way the DMA never queues more than one instruction per wave
+  // ahead of the MFMAs; issued as a burst of eight after the barrier, the
+  // DMA held every wave's issue (C3: ~330 cycles a stage).
   auto stage = [&](int s, unsigned char* S, const unsigned char* Snext, unsigned char* Sfree) {
-    // the first MFMAs go out before the DMA instructions, so the matrix pipe
-    // is busy while they issue
+    const bool more = s + NS - 1 < nk;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) mma(0, n);
+    for (int g = 0; g < 8; ++g) {
+      const int set = g < 4 ? 0 : 1, n0 = 4 * (g & 3);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_n(set, n0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) dma_one(s + NS - 1, Sfree, g);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_n(set, n0 + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      // the last stage's reads of Snext fetch a buffer it never uses: kept
+      // unconditional so that the waits for this step's fragments do not
+      // cover them
+      if (g < 4) read_a(S, 1, 1, g);
+      else read_a(Snext, 0, 0, g - 4);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_n(set, n0 + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      if (g < 4) read_b(S, 1, 1, g);
+      else read_b(Snext, 0, 0, g - 4);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_n(set, n0 + 3);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if (s + NS - 1 < nk) dma(s + NS - 1, Sfree);
-    read_frags(S, 1, 1);
-#pragma unroll
-    for (int n = 4; n < MI * NI; ++n) mma(0, n);
-    // unconditional (the last stage reads a buffer it never uses), so that
-    // the waits for this step's fragments do not cover these reads
-    read_frags(Snext, 0, 0);
-#pragma unroll
-    for (int n = 0; n < MI * NI; ++n) mma(1, n);
-    // each K step's 12 fragment reads (4 A, 8 B) ride behind the previous
-    // step's MFMAs, one read per MFMA
-#pragma unroll
-    for (int g = 0; g < 12; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-    }
-#pragma unroll
-    for (int g = 0; g < 12; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     // B_{s+1}: this wave's DMA of stage s + 2 landed (stages s+3 .. s+NS-1
     // may stay in flight), its reads done
-    if (s + NS - 1 < nk) XT_WAIT_VM(PER * (NS - 3));
+    if (more) XT_WAIT_VM(PER * (NS - 3));
     else XT_WAIT_VM(0);
     asm volatile("s_barrier" ::: "memory");
   };
