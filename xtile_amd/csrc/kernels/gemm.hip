@@ -57,6 +57,14 @@ constexpr int kTileGroup = 8;  // tile columns per group of the workgroup order
 
 enum { kF16 = 0, kBF16 = 1, kI8 = 2 };
 
+// Waves of gemm_dma_kernel: 4 (one per SIMD, 128 x 128 each) or 8 (two per
+// SIMD, 128 x 64 each: half an LDS read more per MFMA, but a second wave to
+// issue MFMAs while one waits).  Measured in one call (bench.py, 2000
+// launches): C3 (f16) 122.6 us with 4 and 124.0 with 8, C5 (bf16) 319.9 and
+// 317.2, C6 (i8) 72.6 and 71.2.
+template <int ELEM>
+constexpr int dma_waves() { return ELEM == kF16 ? 4 : 8; }
+
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef int int4v __attribute__((ext_vector_type(4)));
 typedef int int16v __attribute__((ext_vector_type(16)));
@@ -406,8 +414,9 @@ __global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(Gem
 // 256 x 256 GEMM whose operands reach LDS by DMA (buffer_load ... lds): no
 // VGPR staging, no register transposes, no LDS stores.  f16 / bf16 or i8
 // operands; an f32 result, or (OUT_I8) the i8 result of the epilogue.
-//   * Four waves of 128 x 128 (4 x 4 tiles of v_mfma_f32_32x32x16_{f16,bf16}
-//     or v_mfma_i32_32x32x32_i8), one per SIMD.  A stage is 64 bytes of K
+//   * NW = 4 waves of 128 x 128 (4 x 4 tiles of v_mfma_f32_32x32x16_{f16,bf16}
+//     or v_mfma_i32_32x32x32_i8), one per SIMD, or NW = 8 waves of 128 x 64
+//     (4 x 2 tiles), two per SIMD.  A stage is 64 bytes of K
 //     (32 f16 / bf16 or 64 i8 values): A [256 rows][64 B] and B [KR k][BR B]
 //     (32 x 512 B, or 64 x 256 B for i8), 16 KB each, in one of NS LDS
 //     buffers (each its own LDS variable, so that reading one while DMA into
@@ -440,10 +449,13 @@ __global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(Gem
 //     LDS round trip.  A stage's DMA has NS - 2 stages of compute to land.
 //     The barrier is a bare s_barrier: __syncthreads' release fence would
 //     also wait for the DMA that should stay in flight.
-template <int ELEM, int NS, bool OUT_I8, bool EPI>
-__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
+template <int ELEM, int NS, bool OUT_I8, bool EPI, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   static_assert(NS >= 3 && NS <= 5, "stages");
-  constexpr int BM = 256, BN = 256, WM = 128, WN = 128, MI = 4, NI = 4;
+  static_assert(NW == 4 || NW == 8, "waves");
+  // NW = 4: 2 x 2 waves of 128 x 128; NW = 8: 2 x 4 waves of 128 x 64 (two
+  // waves per SIMD)
+  constexpr int BM = 256, BN = 256, WM = 128, WN = 512 / NW, MI = 4, NI = WN / 32;
   constexpr int ES = ELEM == kI8 ? 1 : 2;  // bytes per element
   constexpr int KB = 64;            // K bytes per A row and stage
   constexpr int AB = BM * KB;       // A bytes per stage
@@ -452,7 +464,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   constexpr int RPI = 1024 / BR;    // B k rows per DMA instruction
   constexpr int KSR = 32 / ES;      // B k rows per MFMA K step
   constexpr int STAGE = AB + KR * BR;
-  constexpr int PER = 8;            // DMA instructions per wave and stage
+  constexpr int PER = 32 / NW;      // DMA instructions per wave and stage
   typedef typename Acc<ELEM>::type acc_t;
   typedef __attribute__((address_space(3))) unsigned char lds_t;
   __shared__ __attribute__((aligned(1024))) unsigned char S0[STAGE];
@@ -466,7 +478,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);
   const i32x4 ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
   const unsigned lda = (unsigned)(p.lda * ES), ldb = (unsigned)(p.ldb * ES);
   const int nk = p.nk * 2;  // stages of 64 K bytes (>= 2)
@@ -486,12 +498,13 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) vb[q] = (unsigned)h * ldb + (unsigned)((pc ^ bsw(RPI * q + h)) << 4);
   }
-  // this wave's share of stage kt: A instructions 4w .. 4w+3 (q = 0..3), B
-  // the same (q = 4..7)
+  // this wave's share of stage kt: A instructions PER/2 w .. + PER/2 - 1
+  // (q < PER/2), B the same (q >= PER/2)
   auto dma_one = [&](int kt, unsigned char* S, int q) {
-    const int i = wave * 4 + (q & 3);
-    if (q < 4) dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kt * KB);
-    else dma16(rb, lds_addr(S + AB + i * 1024), vb[q & 1], (unsigned)(kt * KR + RPI * i) * ldb);
+    constexpr int H = PER / 2;
+    const int i = wave * H + (q % H);
+    if (q < H) dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kt * KB);
+    else dma16(rb, lds_addr(S + AB + i * 1024), vb[i & 1], (unsigned)(kt * KR + RPI * i) * ldb);
   };
   auto dma = [&](int kt, unsigned char* S) {
 #pragma unroll
@@ -564,14 +577,36 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
     if constexpr (OUT_I8) acc[i][j] = mfma<ELEM>(bfr[set][j], af[set][i], acc[i][j]);
     else acc[i][j] = mfma<ELEM>(af[set][i], bfr[set][j], acc[i][j]);
   };
-  // MFMA n of a K step, in shells of max(i, j) (shell k holds n = k^2 ..
-  // k^2 + 2k: (0, k) .. (k-1, k), then (k, 0) .. (k, k)): the fragments of A
-  // row i and B column j are read in slot max(i, j) of the step before, so
-  // the first MFMAs of a step need only the earliest reads.
+  // MFMA n of a K step.  NW = 4: in shells of max(i, j) (shell k holds
+  // n = k^2 .. k^2 + 2k: (0, k) .. (k-1, k), then (k, 0) .. (k, k)), the
+  // fragments of A row i and B column j being read in slot max(i, j) of the
+  // step before; NW = 8: (0,0) (1,0) (0,1) (1,1) (2,0) (3,0) (2,1) (3,1), the
+  // step before reading A0, B0, A1 in its first slot and B1, A2, A3 in its
+  // second.  Either way the first MFMAs of a step need only the earliest
+  // reads.
   auto mma_n = [&](int set, int n) {
-    const int k = n < 1 ? 0 : n < 4 ? 1 : n < 9 ? 2 : 3, r = n - k * k;
-    if (r < k) mma(set, r, k);
-    else mma(set, k, r - k);
+    if constexpr (NW == 4) {
+      const int k = n < 1 ? 0 : n < 4 ? 1 : n < 9 ? 2 : 3, r = n - k * k;
+      if (r < k) mma(set, r, k);
+      else mma(set, k, r - k);
+    } else {
+      mma(set, 2 * (n >> 2) + (n & 1), (n >> 1) & 1);
+    }
+  };
+  // the fragment reads of slot g (of MI * NI / 4 slots) of a K step
+  auto slot_reads = [&](const unsigned char* S, int ks, int set, int g) {
+    if constexpr (NW == 4) {
+      read_a(S, ks, set, g);
+      read_b(S, ks, set, g);
+    } else if (g == 0) {
+      read_a(S, ks, set, 0);
+      read_b(S, ks, set, 0);
+      read_a(S, ks, set, 1);
+    } else {
+      read_b(S, ks, set, 1);
+      read_a(S, ks, set, 2);
+      read_a(S, ks, set, 3);
+    }
   };
 
   // The LDS reads need no wait before a barrier: those of the stage whose
@@ -587,20 +622,22 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
   asm volatile("s_barrier" ::: "memory");
   read_frags(buf[0], 0, 0);
 
-  // A stage is eight slots of four MFMAs.  Slot g issues, in this order
-  // (sched_barrier fences keep the compiler from moving anything across):
-  // MFMA, this wave's DMA instruction g of stage s + NS - 1, MFMA, the A
-  // fragment read, MFMA, the two transposing reads of the B fragment, MFMA.
-  // Slots 0-3 run K step 0 on fragment set 0 and read set 1 (step 1, row and
-  // column g); slots 4-7 run step 1 and read the next stage's set 0.  Spread
-  // out this way the DMA never queues more than one instruction per wave
-  // ahead of the MFMAs; issued as a burst of eight after the barrier, the
-  // DMA held every wave's issue (C3: ~330 cycles a stage).
+  // A stage is 2 MI NI / 4 slots of four MFMAs (8 with four waves, 4 with
+  // eight).  Slot g issues, in this order (sched_barrier fences keep the
+  // compiler from moving anything across): MFMA, this wave's DMA instruction
+  // g of stage s + NS - 1, MFMA, the slot's first fragment read(s), MFMA, the
+  // rest, MFMA.  The first half of the slots runs K step 0 on fragment set 0
+  // and reads set 1; the second half runs step 1 and reads the next stage's
+  // set 0.  Spread out this way the DMA never queues more than one
+  // instruction per wave ahead of the MFMAs; issued as a burst after the
+  // barrier, it held every wave's issue (C3: ~330 cycles a stage).
+  constexpr int SLOTS = MI * NI / 2, HALF = SLOTS / 2;
+  static_assert(SLOTS == PER, "one DMA instruction per slot");
   auto stage = [&](int s, unsigned char* S, const unsigned char* Snext, unsigned char* Sfree) {
     const bool more = s + NS - 1 < nk;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      const int set = g < 4 ? 0 : 1, n0 = 4 * (g & 3);
+    for (int g = 0; g < SLOTS; ++g) {
+      const int set = g < HALF ? 0 : 1, n0 = 4 * (g % HALF);
       __builtin_amdgcn_sched_barrier(0);
       mma_n(set, n0);
       __builtin_amdgcn_sched_barrier(0);
@@ -611,13 +648,10 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(GemmArgs p) {
       // the last stage's reads of Snext fetch a buffer it never uses: kept
       // unconditional so that the waits for this step's fragments do not
       // cover them
-      if (g < 4) read_a(S, 1, 1, g);
-      else read_a(Snext, 0, 0, g - 4);
+      if (g < HALF) slot_reads(S, 1, 1, g);
+      else slot_reads(Snext, 0, 0, g - HALF);
       __builtin_amdgcn_sched_barrier(0);
       mma_n(set, n0 + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      if (g < 4) read_b(S, 1, 1, g);
-      else read_b(Snext, 0, 0, g - 4);
       __builtin_amdgcn_sched_barrier(0);
       mma_n(set, n0 + 3);
     }
@@ -742,12 +776,14 @@ template <int ELEM, bool OUT_I8>
 void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
   const dim3 grid(a.nwg), block(256);
   if (bm == 256) {
+    constexpr int NW = dma_waves<ELEM>();
+    const dim3 dblock(64 * NW);
     if constexpr (OUT_I8)
-      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, true, true>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, true, true, NW>), grid, dblock, 0, s, a);
     else if (a.has_scale || a.has_bias)
-      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, true>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, true, NW>), grid, dblock, 0, s, a);
     else
-      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, NW>), grid, dblock, 0, s, a);
   } else if (bm == 128) hipLaunchKernelGGL((gemm_kernel<ELEM, 128, 128, OUT_I8>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((gemm_kernel<ELEM, 64, 64, OUT_I8>), grid, block, 0, s, a);
 }
