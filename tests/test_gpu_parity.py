@@ -155,6 +155,38 @@ def test_matmul_bf16(cuda, m_, n_, k_, tm, tn):
     assert frob_rel(got, ref) <= MM_FROB
 
 
+@pytest.mark.parametrize(
+    "dt,mn,k_,ftoi",
+    [("f16", 256, 64, False), ("bf16", 256, 64, False), ("bf16", 512, 192, False), ("i8", 256, 128, False),
+     ("i8", 512, 384, True), ("f16", 512, 64, True), ("bf16", 256, 128, True)],
+)
+def test_matmul_dma_kernel_short_k(cuda, dt, mn, k_, ftoi):
+    """256 x 256 workgroup tiles (the DMA kernel; four waves for f16, eight
+    for bf16 and i8) with K of two to six 64-byte stages, fewer than or just
+    above the three stages its prologue puts in flight; f32 and i8 results."""
+    rng = np.random.default_rng(12)
+    dt_in = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}[dt]
+    mod = _matmul_epilogue_program(mn, mn, k_, dt_in, True, True, ftoi)
+    if dt == "i8":
+        a, b, s, bi = _i8_inputs(rng, mn, mn, k_)
+    else:
+        a = rng.normal(0, 1, (mn, k_)).astype(np.float32)
+        b = rng.normal(0, 1, (k_, mn)).astype(np.float32)
+        a, b = (f32_to_bf16_bits(a), f32_to_bf16_bits(b)) if dt == "bf16" else (a.astype(np.float16), b.astype(np.float16))
+        s = rng.uniform(0.05, 0.2, (1, mn)).astype(np.float32)
+        bi = rng.uniform(-3, 3, (1, mn)).astype(np.float32)
+    c = np.zeros((mn, mn), np.int8 if ftoi else np.float32)
+    dts = [dt, dt, "i8" if ftoi else "f32", "f32", "f32"]
+    got = run_gpu(mod, [a, b, c, s, bi], dts, cuda, case=f"mm dma {dt} {mn}x{mn}x{k_} ftoi={ftoi}")[2]
+    want = run_oracle(mod, [a, b, c, s, bi], oracle_threads())[2]
+    if dt == "i8":
+        assert np.array_equal(got, want)
+    elif ftoi:
+        assert np.mean(got != want) < 1e-3 and np.max(np.abs(got.astype(int) - want.astype(int))) <= 1
+    else:
+        assert frob_rel(got, want) <= MM_FROB
+
+
 # -- conv2d (C4) -------------------------------------------------------------------
 
 
