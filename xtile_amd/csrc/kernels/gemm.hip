@@ -52,7 +52,10 @@ namespace xtk {
 namespace {
 
 constexpr int SLICE = 128;  // bytes of K per LDS row and K slice
-constexpr int kDmaStages = 4;  // K stages of gemm_dma_kernel in LDS (C3 in one harness: 3 stages 130.6 us, 4: 131.6, 5: 124.4; in bench.py 4 and 5 both 129.7)
+// K stages of gemm_dma_kernel in LDS: a stage's DMA has two stages of compute
+// to land; three and five stages measured no faster on C3 (bench.py: four
+// and five both 129.7 us before the DMA was spread over the MFMA slots)
+constexpr int kDmaStages = 4;
 constexpr int kTileGroup = 8;  // tile columns per group of the workgroup order
 
 enum { kF16 = 0, kBF16 = 1, kI8 = 2 };
