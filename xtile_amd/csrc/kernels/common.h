@@ -143,6 +143,47 @@ __device__ __forceinline__ void decode_block(int b, int gx, int gy, int& x, int&
 // batch; every load of the batch is then in flight before the first wait.
 __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// One DPP step of wave_reduce: src from the lane `CTRL` names, or the
+// reduction's identity where the source lane lies outside the row or the
+// destination lane is masked off (bound_ctrl off keeps `old`).
+template <bool IS_MAX, int CTRL, int RM, int BM>
+__device__ __forceinline__ float dpp_or_identity(float src) {
+  const float id = IS_MAX ? -__builtin_inff() : 0.0f;
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, id),
+                                                               __builtin_bit_cast(int, src), CTRL, RM, BM, false));
+}
+
+// Max or sum over all 64 lanes of a wave (every lane active), returned to
+// every lane.  DPP steps build an inclusive prefix that ends in lane 63:
+// row_shr 1, 2, 3 of the inputs (each lane gets its four-lane group), row_shr
+// 4 into banks 1-3 and row_shr 8 into banks 2-3 (each lane 15 of a row gets
+// its row), row_bcast 15 into rows 1 and 3 and row_bcast 31 into rows 2 and
+// 3 (lane 63 gets the wave); then lane 63 is read as a scalar.  Seven VALU
+// operations with DPP operands, where a butterfly of __shfl_xor costs six
+// ds_bpermute round trips through the LDS crossbar.
+template <bool IS_MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  auto op = [](float a, float b) { return IS_MAX ? fmaxf(a, b) : a + b; };
+  float a = v;
+  a = op(a, dpp_or_identity<IS_MAX, 0x111, 0xf, 0xf>(v));  // row_shr:1
+  a = op(a, dpp_or_identity<IS_MAX, 0x112, 0xf, 0xf>(v));  // row_shr:2
+  a = op(a, dpp_or_identity<IS_MAX, 0x113, 0xf, 0xf>(v));  // row_shr:3
+  a = op(a, dpp_or_identity<IS_MAX, 0x114, 0xf, 0xe>(a));  // row_shr:4, banks 1-3
+  a = op(a, dpp_or_identity<IS_MAX, 0x118, 0xf, 0xc>(a));  // row_shr:8, banks 2-3
+  a = op(a, dpp_or_identity<IS_MAX, 0x142, 0xa, 0xf>(a));  // row_bcast:15, rows 1, 3
+  a = op(a, dpp_or_identity<IS_MAX, 0x143, 0xc, 0xf>(a));  // row_bcast:31, rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
+}
+
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32): two instructions
+// where expf takes eleven.  The product x * log2 e is rounded once, so the
+// result's relative error is at most |x| 2^-24 plus exp2's own (one ulp):
+// below 5.3e-6 wherever e^x is a normal float (x >= -87.3), and exactly 1
+// at x = 0, 0 at -inf, NaN at NaN.  Results below FLT_MIN may flush to 0.
+__device__ __forceinline__ float exp_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f);
+}
+
 __device__ __forceinline__ float wave_max(float v, int width) {
   for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;

@@ -8,7 +8,10 @@
 // Semantics follow the reference DSL: add/sub/mul are plain IEEE f32 ops
 // (xtile/dsl.py:321-325,351-352); softmax is x - max(x), exp, sum, then
 // multiply by reciprocal(sum) exactly as `x / r` is traced
-// (xtile/dsl.py:354-357, kernels/softmax.py:13-18).
+// (xtile/dsl.py:354-357, kernels/softmax.py:13-18).  exp is exp_fast
+// (common.h: relative error below 5.3e-6 for normal results, against the
+// 1e-5 relative bar of the f32 softmax), and full-wave reductions use DPP
+// (wave_reduce); together they took C2 from 43.0 to 41.9 us a launch.
 #include "common.h"
 #include "launch.h"
 
@@ -151,11 +154,14 @@ struct SoftmaxArgs {
 // previous reduction's reads before the next writes of the same slot.
 template <bool IS_MAX, int TPR>
 __device__ __forceinline__ float row_reduce(float v, float* lds) {
-  constexpr int W = TPR < 64 ? TPR : 64;
+  if constexpr (TPR >= 64) {
+    v = wave_reduce<IS_MAX>(v);
+  } else {
 #pragma unroll
-  for (int o = W >> 1; o > 0; o >>= 1) {
-    const float t = __shfl_xor(v, o, 64);
-    v = IS_MAX ? fmaxf(v, t) : v + t;
+    for (int o = TPR >> 1; o > 0; o >>= 1) {
+      const float t = __shfl_xor(v, o, 64);
+      v = IS_MAX ? fmaxf(v, t) : v + t;
+    }
   }
   if constexpr (TPR <= 64) {
     return v;
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(256) void row_softmax_kernel(SoftmaxArgs p) {
     for (int j = 0; j < NV; ++j)
 #pragma unroll
       for (int k = 0; k < VW; ++k) {
-        v[j][k] = ok[j] ? expf(v[j][k] - m) : 0.0f;
+        v[j][k] = ok[j] ? exp_fast(v[j][k] - m) : 0.0f;
         s += v[j][k];
       }
     s = row_reduce<false, TPR>(s, lds);
@@ -273,8 +279,7 @@ __global__ __launch_bounds__(TPB) void row_softmax_wide_kernel(SoftmaxArgs p) {
     float m = fmaxf(fmaxf(v[0].x, v[0].y), fmaxf(v[0].z, v[0].w));
 #pragma unroll
     for (int j = 1; j < NV; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = wave_reduce<true>(m);
     if ((threadIdx.x & 63) == 0) lds[0][w] = m;
     __syncthreads();
     m = lds[0][0];
@@ -283,14 +288,13 @@ __global__ __launch_bounds__(TPB) void row_softmax_wide_kernel(SoftmaxArgs p) {
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      v[j].x = expf(v[j].x - m);
-      v[j].y = expf(v[j].y - m);
-      v[j].z = expf(v[j].z - m);
-      v[j].w = expf(v[j].w - m);
+      v[j].x = exp_fast(v[j].x - m);
+      v[j].y = exp_fast(v[j].y - m);
+      v[j].z = exp_fast(v[j].z - m);
+      v[j].w = exp_fast(v[j].w - m);
       s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_reduce<false>(s);
     // the max slot and the sum slot are distinct, so this barrier also orders
     // every read of lds[0] above before the next row's writes to it
     if ((threadIdx.x & 63) == 0) lds[1][w] = s;
@@ -323,8 +327,7 @@ __global__ __launch_bounds__(TPB) void row_softmax_1d_kernel(const float4v* __re
   float m = fmaxf(fmaxf(v[0].x, v[0].y), fmaxf(v[0].z, v[0].w));
 #pragma unroll
   for (int j = 1; j < NV; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  m = wave_reduce<true>(m);
   if ((threadIdx.x & 63) == 0) lds[0][w] = m;
   __syncthreads();
   m = lds[0][0];
@@ -333,14 +336,13 @@ __global__ __launch_bounds__(TPB) void row_softmax_1d_kernel(const float4v* __re
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    v[j].x = expf(v[j].x - m);
-    v[j].y = expf(v[j].y - m);
-    v[j].z = expf(v[j].z - m);
-    v[j].w = expf(v[j].w - m);
+    v[j].x = exp_fast(v[j].x - m);
+    v[j].y = exp_fast(v[j].y - m);
+    v[j].z = exp_fast(v[j].z - m);
+    v[j].w = exp_fast(v[j].w - m);
     s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  s = wave_reduce<false>(s);
   if ((threadIdx.x & 63) == 0) lds[1][w] = s;
   __syncthreads();
   s = lds[1][0];
