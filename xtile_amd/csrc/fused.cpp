@@ -38,6 +38,25 @@ typedef unsigned short xu2 __attribute__((ext_vector_type(2)));
 typedef signed char xc4 __attribute__((ext_vector_type(4)));
 typedef signed char xc2 __attribute__((ext_vector_type(2)));
 struct FusedArgs { void* p[8]; };
+template <bool MX, int C, int RM, int BM>
+__device__ __forceinline__ float xdpp(float s) {
+  const float id = MX ? -__builtin_huge_valf() : 0.0f;
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, id), __builtin_bit_cast(int, s),
+                                                               C, RM, BM, false));
+}
+template <bool MX>
+__device__ __forceinline__ float xwred(float v) {
+  auto op = [](float a, float b) { return MX ? fmaxf(a, b) : a + b; };
+  float a = v;
+  a = op(a, xdpp<MX, 0x111, 0xf, 0xf>(v));
+  a = op(a, xdpp<MX, 0x112, 0xf, 0xf>(v));
+  a = op(a, xdpp<MX, 0x113, 0xf, 0xf>(v));
+  a = op(a, xdpp<MX, 0x114, 0xf, 0xe>(a));
+  a = op(a, xdpp<MX, 0x118, 0xf, 0xc>(a));
+  a = op(a, xdpp<MX, 0x142, 0xa, 0xf>(a));
+  a = op(a, xdpp<MX, 0x143, 0xc, 0xf>(a));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
+}
 __device__ __forceinline__ float xbf(unsigned short u) { return __uint_as_float((unsigned)u << 16); }
 __device__ __forceinline__ unsigned short xto_f16(float f) {
   const unsigned u = __float_as_uint(f);
@@ -385,9 +404,13 @@ class Gen {
           b << "#pragma unroll\n  for (int sr = 0; sr < " << nr << "; ++sr) {\n    float m = " << init << ";\n";
           b << "#pragma unroll\n    for (int j = 0; j < " << L.cols() << "; ++j) m = "
             << comb("m", s + "[" + idx(ks, "sr", "j") + "]") << ";\n";
-          const int w = std::min(L.TC, 64);
-          b << "#pragma unroll\n    for (int o = " << w / 2 << "; o > 0; o >>= 1) m = "
-            << comb("m", "__shfl_xor(m, o, 64)") << ";\n";
+          // a whole wave along the row: DPP steps to lane 63 (xwred), else a
+          // butterfly over the row's TC lanes
+          if (L.TC >= 64)
+            b << "    m = xwred<" << (is_max ? "true" : "false") << ">(m);\n";
+          else
+            b << "#pragma unroll\n    for (int o = " << L.TC / 2 << "; o > 0; o >>= 1) m = "
+              << comb("m", "__shfl_xor(m, o, 64)") << ";\n";
           b << "    " << v << "[sr] = m;\n  }\n";
           if (L.TC > 64) {  // the row spans TC / 64 waves: combine through LDS
             // each reduction has LDS of its own, so one barrier orders its writes before its reads
