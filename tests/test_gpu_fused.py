@@ -7,8 +7,10 @@ picks: a row spread over four or eight waves (cross-wave row reduction
 through LDS),
 several rows per thread, a column reduction over 64 or 256 threads of a
 column,
-[R, 1] and [1, 1] stores, a buffer not aligned to the row vectors (which runs on
-the interpreter instead), and agreement with the interpreter (XTILE_AMD_FUSE=0).
+[R, 1] and [1, 1] stores, ragged rows (a vector count no power-of-two thread
+row divides: the last vectors of a thread row absent), a buffer not aligned to
+the row vectors (which runs on the interpreter instead), and agreement with the
+interpreter (XTILE_AMD_FUSE=0).
 
 Bars: layernorm within 2e-5 absolute of the oracle (inputs of unit scale, a
 different summation order); column softmax within 1e-5 relative; programs
@@ -111,6 +113,74 @@ def test_fused_row_column_and_scalar_stores(cuda):
     # i8 of x - rowsum: one rounding of a difference whose rowsum may differ in the last bits
     d = np.abs(got[4].astype(np.int32) - want[4].astype(np.int32))
     assert d.max() <= 1
+
+
+_STATS100 = _STATS.replace("x256x", "x100x").replace("x256x", "x100x").replace("256x", "100x")
+
+
+def test_fused_ragged_row_column_and_scalar_stores(cuda):
+    """The stats program over 100 columns (25 float4 a row): a ragged layout of
+    16 threads a row, two vectors each, the second present for 9 of the 16.
+    Absent vectors are neither stored ([R, C] i8 and [1, C] stores) nor part of
+    the row sums; the column maxima of present columns are exact."""
+    m = xt.parse(_STATS100)
+    desc = xt.plan(m)["kernel"]
+    assert desc.startswith("fused f32 tile=16x100 threads=16x16 vw=4 ragged"), desc
+    rng = np.random.default_rng(44)
+    x = rng.normal(0, 1, (64, 100)).astype(np.float32)
+    # sentinels: a store to an absent column would overwrite them
+    bufs = [x, np.zeros((64, 1), np.float32), np.full((4, 100), 7.0, np.float32), np.zeros((4, 1), np.float32),
+            np.full((64, 100), 5, np.int8)]
+    dts = ["f32", "f32", "f32", "f32", "i8"]
+    got = run_gpu(m, bufs, dts, cuda, case="fused stats ragged 64x100")
+    want = run_oracle(m, bufs, 1)
+    scale = np.abs(x).sum(axis=1).max()
+    np.testing.assert_allclose(got[1], want[1], rtol=0, atol=1e-5 * scale)
+    assert np.array_equal(got[2], want[2])
+    np.testing.assert_allclose(got[3], want[3], rtol=0, atol=1e-5 * scale)
+    d = np.abs(got[4].astype(np.int32) - want[4].astype(np.int32))
+    assert d.max() <= 1
+
+
+@pytest.mark.parametrize(
+    "rows,cols,trow,layout",
+    [
+        (64, 3798, 1, "tile=1x3798 threads=1x512 vw=2 ragged"),  # 1899 float2: 4 rounds of 512, the last 363 present
+        (64, 1000, 1, "tile=1x1000 threads=1x128 vw=4 ragged"),   # 250 float4 over 128 threads
+        (32, 130, 4, "tile=4x130 threads=4x64 vw=2 ragged"),      # 65 float2: one present in the second round
+        (64, 4100, 1, "tile=1x4100 threads=1x512 vw=4 ragged"),   # 1025 float4: one vector in the third round
+        (8192, 2050, 1, "tile=1x2050 threads=1x512 vw=2 ragged workgroups="),  # Block walk, gamma / beta ragged
+    ],
+)
+def test_fused_ragged_layernorm(cuda, monkeypatch, rows, cols, trow, layout):
+    """Layernorm over rows whose vector count no power-of-two thread row
+    divides: against the oracle, and against the interpreter (XTILE_AMD_FUSE=0)."""
+    m = K.layernorm(rows, cols, trow)
+    assert xt.plan(m)["kernel"].startswith("fused f32 " + layout)
+    bufs = _ln_inputs(rows, cols, 45)
+    got = run_gpu(m, bufs, ["f32"] * 6, cuda, case=f"fused ragged layernorm {rows}x{cols}/{trow}")[5]
+    want = run_oracle(m, bufs, oracle_threads())[5]
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+    if rows <= 64:
+        monkeypatch.setenv("XTILE_AMD_FUSE", "0")
+        m2 = K.layernorm(rows, cols, trow)
+        assert xt.plan(m2)["kernel"].startswith("tile_vm")
+        vm = run_gpu(m2, bufs, ["f32"] * 6, cuda, case=f"interpreted layernorm {rows}x{cols}/{trow}")[5]
+        np.testing.assert_allclose(got, vm, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 3798), (256, 2050)])
+def test_fused_ragged_softmax(cuda, rows, cols):
+    """Row softmax over rows of an odd number of float2 vectors (the float4
+    softmax kernel declines them)."""
+    m = K.softmax(rows, cols, 1)
+    assert xt.plan(m)["kernel"].startswith("fused f32 tile=1x%d threads=1x512 vw=2 ragged" % cols)
+    rng = np.random.default_rng(46)
+    x = rng.normal(0, 2, (rows, cols)).astype(np.float32)
+    got = run_gpu(m, [x, np.zeros_like(x)], ["f32"] * 2, cuda, case=f"fused ragged softmax {rows}x{cols}")[1]
+    want = run_oracle(m, [x, np.zeros_like(x)], oracle_threads())[1]
+    assert np.max(np.abs(got - want) / np.abs(want)) <= 1e-5
+    np.testing.assert_allclose(got.sum(axis=1), 1.0, atol=1e-5)
 
 
 _CENTER = """

@@ -32,15 +32,18 @@ def test_random_stream_program_matches_the_oracle(cuda, seed):
         assert np.max(np.abs(got - want) / np.abs(want)) <= 1e-5
 
 
-def test_long_rows_without_float4_alignment_leave_the_softmax_kernel(cuda):
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_long_rows_without_float4_alignment_leave_the_softmax_kernel(cuda, monkeypatch, fuse):
     """3798 columns (not a multiple of 4) exceed what the softmax kernel holds
-    without float4 vectors: the planner sends the program to the tile
-    interpreter, which matches the oracle."""
+    without float4 vectors: the planner sends the program to the fused
+    kernel's ragged layout (or, with XTILE_AMD_FUSE=0, to the tile
+    interpreter); both match the oracle."""
     from xtile_amd import kernels as K
 
+    monkeypatch.setenv("XTILE_AMD_FUSE", fuse)
     mod = K.softmax(122, 3798, 2)
-    assert xt.plan(mod)["kernel"].startswith("tile_vm")
+    assert xt.plan(mod)["kernel"].startswith("fused f32 tile=2x3798" if fuse == "1" else "tile_vm")
     x = np.random.default_rng(48).normal(0, 2, (122, 3798)).astype(np.float32)
-    got = run_gpu(mod, [x, np.zeros_like(x)], ["f32"] * 2, cuda, case="softmax 122x3798 on the interpreter")[1]
+    got = run_gpu(mod, [x, np.zeros_like(x)], ["f32"] * 2, cuda, case=f"softmax 122x3798 fuse={fuse}")[1]
     want = run_oracle(mod, [x, np.zeros_like(x)], 8)[1]
     assert np.max(np.abs(got - want) / np.abs(want)) <= 1e-5

@@ -238,6 +238,28 @@ func.func @s(%a: memref<64x64xf32>, %b: memref<64x64xf32>, %c: memref<64x64xf32>
     assert xt.plan(xt.parse(text))["kernel"].startswith("ew_binary")
 
 
+@pytest.mark.parametrize(
+    "prog,args,layout",
+    [
+        # 1899 float2 a row: no power-of-two thread row divides it, so 512 threads take
+        # four vectors each and the last 149 of the fourth round are absent
+        ("layernorm", (64, 3798, 1), "fused f32 tile=1x3798 threads=1x512 vw=2 ragged insts=17"),
+        ("layernorm", (64, 1000, 1), "fused f32 tile=1x1000 threads=1x128 vw=4 ragged insts=17"),
+        ("layernorm", (32, 130, 4), "fused f32 tile=4x130 threads=4x64 vw=2 ragged insts=17"),
+        ("softmax", (64, 3798, 1), "fused f32 tile=1x3798 threads=1x512 vw=2 ragged insts=8"),
+        # rows that a power-of-two thread row divides keep the exact layout
+        ("layernorm", (8192, 4096, 1), "fused f32 tile=1x4096 threads=1x512 vw=4 workgroups=512 insts=17"),
+        ("layernorm", (96, 48, 16), "fused f32 tile=16x48 threads=16x4 vw=4 insts=17"),
+    ],
+)
+def test_fused_ragged_rows(prog, args, layout):
+    """Rows whose vector count has no power-of-two divisor wide enough to keep a
+    thread's share at 64 elements or fewer run on a ragged fused layout instead
+    of the interpreter."""
+    m = getattr(K, prog)(*args)
+    assert xt.plan(m)["kernel"].startswith(layout)
+
+
 def test_fused_kernels_are_compiled_into_the_code_object_cache(tmp_path, monkeypatch):
     """Planning a fused program compiles it with hiprtc (no GPU needed) and
     writes the code object and its source under XTILE_AMD_JIT_CACHE."""
@@ -258,7 +280,8 @@ def test_fused_kernels_are_compiled_into_the_code_object_cache(tmp_path, monkeyp
 def test_softmax_rows_above_2048_need_float4_vectors():
     assert xt.plan(K.softmax(64, 4096, 1))["kernel"].startswith("row_softmax")
     assert xt.plan(K.softmax(64, 2047, 1))["kernel"].startswith("row_softmax")
-    assert xt.plan(K.softmax(122, 3798, 2))["kernel"].startswith("tile_vm")
+    # 1899 float2 a row: the fused kernel's ragged layout (the interpreter before it)
+    assert xt.plan(K.softmax(122, 3798, 2))["kernel"].startswith("fused f32 tile=2x3798 threads=1x512 vw=2 ragged")
 
 
 def test_native_binding_has_the_reference_stage_names():

@@ -9,7 +9,13 @@
 // (VW TC)) of VW consecutive columns, so each row access is a VW-wide vector
 // load or store and consecutive threads touch consecutive vectors.  A [1, C]
 // value is held by every tr, an [R, 1] value by every tc, a [1, 1] value by
-// every thread: broadcasts are register reads.
+// every thread: broadcasts are register reads.  TC divides the CV = C / VW
+// vectors of a row when that keeps at most 64 elements a thread; otherwise
+// (rows whose vector count has no large power-of-two divisor, e.g. 3798
+// floats = 1899 float2) the row is "ragged": TC is the largest power of two
+// <= min(CV, 512), SC = ceil(CV / TC), and vector tc + sc TC exists only below
+// CV: its loads read zeros, its stores are skipped and column reductions
+// skip it.
 //
 // Ops (the interpreter's semantics, kernels/tilevm.hip): loads convert f16 /
 // bf16 / i8 exactly and stores round (nearest even for f16 / bf16; round,
@@ -82,6 +88,8 @@ __device__ __forceinline__ float xto_i8(float v) {
 
 struct Layout {
   int R = 1, C = 1, VW = 1, TR = 1, TC = 1, SR = 1, SC = 1;
+  int CV = 1;           // vectors of VW columns in a row
+  bool ragged = false;  // SC * TC > CV: the last vectors of a thread row are absent
   int threads() const { return TR * TC; }
   int cols() const { return SC * VW; }  // register columns of a thread
 };
@@ -171,6 +179,7 @@ class Gen {
     out.workgroups = static_cast<int>(wgs);
     std::ostringstream lay;
     lay << "fused f32 tile=" << L.R << "x" << L.C << " threads=" << L.TR << "x" << L.TC << " vw=" << L.VW;
+    if (L.ragged) lay << " ragged";
     if (hoist_) lay << " workgroups=" << wgs;
     out.layout = lay.str();
     return true;
@@ -198,7 +207,8 @@ class Gen {
   static long long walkers(long long blocks, long long resident, long long stream_bytes) {
     constexpr long long kInFlight = 16LL << 20;
     long long target = stream_bytes > 0 ? kInFlight / (2 * stream_bytes) : resident;
-    target = std::max(256LL, std::min(resident, target / 256 * 256));
+    // the nearest multiple of 256 (rows a little over 16 KB are not halved)
+    target = std::max(256LL, std::min(resident, (target + 128) / 256 * 256));
     long long best = target;
     double best_cost = 1e300;
     for (long long w = std::max(256LL, target / 2 / 256 * 256); w <= std::min(resident, target * 2); w += 256) {
@@ -269,11 +279,25 @@ class Gen {
     }
     L.VW = vw;
     const int cv = L.C / L.VW;
+    L.CV = cv;
     // up to 512 threads (8 waves) a workgroup: 4096-float rows at two float4 a thread
     L.TC = pow2_divisor(cv, 512);
     L.TR = pow2_divisor(L.R, 512 / L.TC);
     L.SR = L.R / L.TR;
     L.SC = cv / L.TC;
+    L.ragged = false;
+    if (L.SR * L.cols() > 64) {
+      // ragged rows: the widest power-of-two thread row, the last vectors guarded
+      int tc = 1;
+      while (tc * 2 <= std::min(cv, 512)) tc *= 2;
+      if (tc > L.TC) {
+        L.TC = tc;
+        L.TR = pow2_divisor(L.R, 512 / L.TC);
+        L.SR = L.R / L.TR;
+        L.SC = (cv + tc - 1) / tc;
+        L.ragged = L.SC * tc != cv;
+      }
+    }
     if (L.SR * L.cols() > 64) {
       why = "fused kernels keep at most 64 elements of a tile per thread";
       return false;
@@ -300,6 +324,11 @@ class Gen {
     return s.str();
   }
 
+  // vector sc of this thread's row exists (ragged rows only)
+  std::string present(const std::string& sc) const {
+    return "tc + (" + sc + ") * " + std::to_string(L.TC) + " < " + std::to_string(L.CV);
+  }
+
   // element offset of register (sr, sc) of a tile of kind k (row pitch ld)
   std::string elem_off(VKind k, long long ld) const {
     std::string s = "0";
@@ -323,7 +352,14 @@ class Gen {
         b << "#pragma unroll\n    for (int sc = 0; sc < " << (k.c ? L.SC : 1) << "; ++sc) {\n";
         b << "      const long long off = org + " << elem_off(k, acc.stride[1]) << ";\n";
         const std::string dst = v + "[" + idx(k, "sr", "sc * " + std::to_string(vw) + " + e") + "]";
-        load_code(b, in.kind, acc.elem, vw, dst);
+        if (k.c && L.ragged) {
+          b << "      if (" << present("sc") << ") {\n";
+          load_code(b, in.kind, acc.elem, vw, dst);
+          b << "      } else {\n#pragma unroll\n        for (int e = 0; e < " << vw << "; ++e) " << dst
+            << " = 0.0f;\n      }\n";
+        } else {
+          load_code(b, in.kind, acc.elem, vw, dst);
+        }
         b << "    }\n  }\n";
         slot_[in.dst] = {i, k};
         return true;
@@ -347,7 +383,9 @@ class Gen {
         b << "#pragma unroll\n    for (int sc = 0; sc < " << (k.c ? L.SC : 1) << "; ++sc) {\n";
         b << "      const long long off = org + " << elem_off(k, acc.stride[1]) << ";\n";
         const std::string s = src + "[" + idx(k, "sr", "sc * " + std::to_string(vw) + " + e") + "]";
+        if (k.c && L.ragged) b << "      if (" << present("sc") << ") {\n";
         store_code(b, in.kind, acc.elem, vw, s);
+        if (k.c && L.ragged) b << "      }\n";
         b << "    }\n  }\n";
         return true;
       }
@@ -402,8 +440,13 @@ class Gen {
           const int nr = ks.r ? L.SR : 1;
           b << "  float " << v << "[" << nr << "];\n";
           b << "#pragma unroll\n  for (int sr = 0; sr < " << nr << "; ++sr) {\n    float m = " << init << ";\n";
-          b << "#pragma unroll\n    for (int j = 0; j < " << L.cols() << "; ++j) m = "
-            << comb("m", s + "[" + idx(ks, "sr", "j") + "]") << ";\n";
+          if (L.ragged)  // absent vectors take no part
+            b << "#pragma unroll\n    for (int j = 0; j < " << L.cols() << "; ++j) if ("
+              << present("j / " + std::to_string(L.VW)) << ") m = " << comb("m", s + "[" + idx(ks, "sr", "j") + "]")
+              << ";\n";
+          else
+            b << "#pragma unroll\n    for (int j = 0; j < " << L.cols() << "; ++j) m = "
+              << comb("m", s + "[" + idx(ks, "sr", "j") + "]") << ";\n";
           // a whole wave along the row: DPP steps to lane 63 (xwred), else a
           // butterfly over the row's TC lanes
           if (L.TC >= 64)
