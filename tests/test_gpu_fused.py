@@ -9,8 +9,8 @@ several rows per thread, a column reduction over 64 or 256 threads of a
 column,
 [R, 1] and [1, 1] stores, ragged rows (a vector count no power-of-two thread
 row divides: the last vectors of a thread row absent), a buffer not aligned to
-the row vectors (which runs on the interpreter instead), and agreement with the
-interpreter (XTILE_AMD_FUSE=0).
+the row vectors (which runs the program's scalar-access variant instead), and
+agreement with the interpreter (XTILE_AMD_FUSE=0).
 
 Bars: layernorm within 2e-5 absolute of the oracle (inputs of unit scale, a
 different summation order); column softmax within 1e-5 relative; programs
@@ -236,9 +236,10 @@ def test_fused_and_interpreted_layernorm_agree(cuda, monkeypatch):
     np.testing.assert_allclose(got, ref, rtol=0, atol=2e-5)
 
 
-def test_misaligned_buffer_runs_on_the_interpreter(cuda):
+def test_misaligned_buffer_runs_the_scalar_variant(cuda):
     """A buffer offset by one f32 cannot be read as 16-byte vectors: the
-    launch takes the interpreter for it and the result is unchanged."""
+    launch takes the program's scalar-access variant (vw = 1, built on first
+    use) and the result is unchanged."""
     import torch
 
     m = K.bias_add(128, 256)
@@ -253,6 +254,28 @@ def test_misaligned_buffer_runs_on_the_interpreter(cuda):
     xt.launch(m, torch.from_numpy(a).to(cuda), torch.from_numpy(v).to(cuda), out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), a + v)
+
+
+def test_misaligned_buffer_of_a_program_the_interpreter_declines(cuda):
+    """Layernorm over 4 x 4096 Blocks needs more LDS than the interpreter has,
+    so before the scalar variant a misaligned buffer made the launch fail;
+    now it runs with scalar row accesses and matches the oracle."""
+    import torch
+
+    m = K.layernorm(256, 4096, 4)
+    desc = xt.plan(m)["kernel"]
+    assert desc.startswith("fused f32 tile=4x4096 threads=1x512 vw=4"), desc
+    bufs = _ln_inputs(256, 4096, 48)
+    want = run_oracle(m, bufs, oracle_threads())[5]
+    print("[gpu] misaligned layernorm 256x4096/4", flush=True)
+    store = torch.zeros(256 * 4096 + 1, dtype=torch.float32, device=cuda)
+    x = store[1:].view(256, 4096)
+    assert x.data_ptr() % 16 == 4
+    x.copy_(torch.from_numpy(bufs[0]).to(cuda))
+    dev = [x] + [torch.from_numpy(b).to(cuda) for b in bufs[1:]]
+    xt.launch(m, *dev)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(dev[5].cpu().numpy(), want, rtol=0, atol=2e-5)
 
 
 def test_misaligned_softmax_rows_above_2048_run_on_the_interpreter(cuda):

@@ -129,7 +129,7 @@ std::string replace_x(const char* pattern, const std::string& x) {
 
 class Gen {
  public:
-  Gen(const VmPlan& vm, const int32_t grid[3]) : vm_(vm) {
+  Gen(const VmPlan& vm, const int32_t grid[3], int max_vw) : vm_(vm), max_vw_(max_vw) {
     for (int d = 0; d < 3; ++d) grid_[d] = grid[d];
   }
 
@@ -187,6 +187,7 @@ class Gen {
 
  private:
   const VmPlan& vm_;
+  int max_vw_ = 4;
   int grid_[3];
   Layout L;
   std::map<int, std::pair<int, VKind>> slot_;  // LDS slot -> (value id, kind)
@@ -263,7 +264,7 @@ class Gen {
   }
 
   bool layout(std::string& why) {
-    int vw = 4;
+    int vw = max_vw_ >= 4 ? 4 : max_vw_ >= 2 ? 2 : 1;
     for (; vw > 1; vw /= 2) {
       if (L.C % vw) continue;
       bool ok = true;
@@ -565,7 +566,7 @@ class Gen {
 
 }  // namespace
 
-bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why) {
+bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why, int max_vw) {
   if (vm.access.size() > 8) {
     why = "fused kernels take at most 8 loads and stores";
     return false;
@@ -585,7 +586,7 @@ bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::strin
       return false;
     }
   }
-  Gen g(vm, grid);
+  Gen g(vm, grid, max_vw);
   return g.run(out, why);
 }
 

@@ -125,6 +125,36 @@ bool compile_fused(xt::FusedPlan& fp, std::string& err) {
   return true;
 }
 
+namespace {
+
+// Index of the first access whose buffer is not aligned to vw elements, or -1.
+int misaligned(const xt::VmPlan& vm, void* const* bufs, int vw, uintptr_t& align) {
+  for (size_t k = 0; k < vm.access.size(); ++k) {
+    const xt::VmAccess& a = vm.access[k];
+    align = static_cast<uintptr_t>(vw) * xt::elem_bytes(a.elem);
+    if (reinterpret_cast<uintptr_t>(bufs[a.arg]) % align) return static_cast<int>(a.arg);
+  }
+  return -1;
+}
+
+std::mutex g_scalar_mu;
+
+// The plan's scalar-access variant, generated and compiled on first use
+// (nullptr, with `err`, when the program does not fit the fused layout with
+// vw = 1 or does not compile).
+const xt::FusedPlan* scalar_variant(const xt::Plan& p, std::string& err) {
+  xt::FusedPlan* fp = p.fused.get();
+  std::lock_guard<std::mutex> lock(g_scalar_mu);
+  if (!fp->scalar) {
+    auto sp = std::make_shared<xt::FusedPlan>();
+    if (!xt::fuse_vm(p.vm, p.grid, *sp, err, 1) || !compile_fused(*sp, err)) return nullptr;
+    fp->scalar = std::move(sp);
+  }
+  return fp->scalar.get();
+}
+
+}  // namespace
+
 hipError_t launch_fused(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why) {
   const xt::FusedPlan* fp = p.fused.get();
   if (!fp || fp->code.empty()) {
@@ -136,16 +166,30 @@ hipError_t launch_fused(const xt::Plan& p, void* const* bufs, hipStream_t s, std
     why = "fused kernels take at most 8 memref accesses";
     return hipErrorInvalidValue;
   }
-  // row accesses are vw-element vectors: a buffer not aligned to one goes to the interpreter
-  for (const xt::VmAccess& a : vm.access) {
-    const uintptr_t align = static_cast<uintptr_t>(fp->vw) * xt::elem_bytes(a.elem);
-    if (reinterpret_cast<uintptr_t>(bufs[a.arg]) % align) {
-      if (p.vm_fallback) return launch_tilevm(p, bufs, s, why);
-      why = "buffer " + std::to_string(a.arg) + " is not aligned to " + std::to_string(align) +
-            " bytes, which the fused kernel's row vectors need, and the tile interpreter cannot run "
-            "this program: " + p.vm_fallback_why;
+  // Row accesses are vw-element vectors.  A buffer not aligned to one runs
+  // the program's scalar-access variant (vw = 1), or the interpreter when
+  // that variant does not fit the fused layout.
+  uintptr_t align = 0;
+  int bad = misaligned(vm, bufs, fp->vw, align);
+  if (bad >= 0 && fp->vw > 1) {
+    std::string err;
+    const xt::FusedPlan* sp = scalar_variant(p, err);
+    if (sp) {
+      fp = sp;
+      bad = misaligned(vm, bufs, 1, align);
+    } else if (p.vm_fallback) {
+      return launch_tilevm(p, bufs, s, why);
+    } else {
+      why = "buffer " + std::to_string(bad) + " is not aligned to " + std::to_string(align) +
+            " bytes, which the fused kernel's row vectors need; its scalar variant: " + err +
+            "; the tile interpreter: " + p.vm_fallback_why;
       return hipErrorInvalidValue;
     }
+  }
+  if (bad >= 0) {
+    if (p.vm_fallback) return launch_tilevm(p, bufs, s, why);
+    why = "buffer " + std::to_string(bad) + " is not aligned to its " + std::to_string(align) + "-byte elements";
+    return hipErrorInvalidValue;
   }
   const long long blocks = static_cast<long long>(p.grid[0]) * p.grid[1] * p.grid[2];
   if (blocks < 1 || blocks > 0x7fffffffLL || blocks * fp->threads >= (1LL << 32)) {

@@ -104,6 +104,9 @@ struct FusedPlan {
   std::string layout;        // for describe()
   std::string code;          // the gfx950 code object (filled by the runtime's compile)
   uint64_t id = 0;           // hash of `source` (filled with `code`), keys the loaded kernels
+  // the same program with scalar row accesses (vw = 1), built and compiled by
+  // the first launch whose buffers are not aligned to the vw-element vectors
+  std::shared_ptr<FusedPlan> scalar;
 };
 
 struct Plan {
@@ -142,7 +145,8 @@ struct Plan {
 // program's main [R, C] tile or a [1, C] / [R, 1] / [1, 1] broadcast of it and
 // the ops are loads, stores, unary, binary and reductions (fused.cpp).
 // Returns false, with `why` set, when the program does not fit.
-bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why);
+// max_vw caps the row vector width (4, 2 or 1 elements)
+bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why, int max_vw = 4);
 
 // Builds the plan of function `func` (empty name: the only function).
 // Returns false and sets `error` when the program is not one the HIP
