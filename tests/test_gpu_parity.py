@@ -245,6 +245,41 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
 
 
 @pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil,dt",
+    [
+        (2, 12, 12, 128, 128, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # 295 KB filter: M 288, 3 tiles
+        (4, 16, 16, 128, 256, 3, 3, 8, 16, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # 8 x 2 = 16 workgroups (XCD runs)
+        (2, 9, 11, 256, 256, 3, 3, 5, 6, (1, 1, 1, 1), (2, 2), (1, 1), "bf16"),    # stride 2: M = 60, one partial tile
+        (1, 7, 7, 512, 128, 3, 3, 7, 7, (2, 2, 2, 2), (1, 1), (2, 2), "f16"),      # dilation 2, 144 K stages
+        (3, 10, 10, 64, 256, 1, 1, 5, 10, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),    # 1 x 1, Cout 256
+        (2, 16, 16, 96, 128, 5, 5, 5, 15, (2, 1, 1, 2), (1, 1), (1, 1), "bf16"),   # Cin 96: three stages a tap, asymmetric pad
+        (2, 14, 14, 256, 128, 3, 3, 4, 12, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),   # no padding: 12 x 12 outputs
+    ],
+)
+def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
+    """Filters too large for the band kernel's LDS (Cin * Cout * taps * 2
+    bytes above ~150 KB) with Cout a multiple of 128 take the implicit-GEMM
+    kernel (conv_igemm.hip): operands by DMA, the input gathered per tap,
+    padding and rows past M read as zeros."""
+    rng = np.random.default_rng(9)
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
+                   pad=pad, stride=stride, dilation=dil)
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+    if dt == "bf16":
+        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    else:
+        x, f = x.astype(np.float16), f.astype(np.float16)
+    o = np.zeros((n, oh, ow, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
+                  case=f"conv igemm {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil} {dt}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+
+
+@pytest.mark.parametrize(
     "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil",
     [
         (1, 32, 64, 128, 64, 3, 3, 32, 64, (1, 1, 1, 1), (1, 1), (1, 1)),  # kernels/conv2d.py defaults

@@ -951,6 +951,8 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   if (try_band(p, bufs, s, max_lds, cus, e)) return e;
+  // filters beyond the band kernel's LDS: the implicit GEMM with DMA operands
+  if (launch_conv2d_igemm(p, bufs, s, e)) return e;
   // the persistent kernel: f16 / bf16 in, f32 out, one image per Block, every
   // output channel, 16-byte channel runs; anything else takes the generic kernel
   if (!persistent_ok) return launch_conv2d_general(p, bufs, s, why);

@@ -1,0 +1,312 @@
+// xt.load_conv2d as an implicit GEMM whose operands reach LDS by DMA: the path
+// for filters too large for the LDS-resident filter of the band and
+// persistent kernels (conv.hip), e.g. 3x3 convolutions with 128 or more input
+// and output channels.
+//
+// Semantics (lib/xt/XTOps.cpp:43-90, lib/xt/XTToNova.cpp:110-142,353-437):
+//   out[n, oh, ow, o] = sum_{kh,kw,c} src[n, oh*sh - pad_t + kh*dh,
+//                                         ow*sw - pad_l + kw*dw, c] * f[kh, kw, c, o]
+// with source elements outside the image read as zero.  Used when the Blocks
+// tile the whole output (one image per Block, every output channel, one
+// filter), so the launch is one GEMM:
+//   M = N*OH*OW output pixels (NHWC order: the output is C[M][CO]),
+//   N = CO, K = KH*KW*Cin in the filter's (kh, kw, c) order (B = f as
+//   [K][CO], row-major HWIO).
+// Every output pixel sums its K terms in the same order as the other conv
+// kernels; Blocks are independent (README.md:85-89), so the regrouping is a
+// scheduling choice.
+//
+//   * Workgroup tile 128 pixels x 128 channels, four waves of 64 x 64 (2 x 2
+//     tiles of v_mfma_f32_32x32x16_{f16,bf16}); 64 KB of LDS, so two
+//     workgroups share a CU and one's barrier waits are the other's MFMA time.
+//   * A K stage is one tap's 32 channels (64 bytes of every pixel row):
+//     A [128 rows][64 B] is an im2col gather done by the DMA itself: lane L of
+//     A instruction i fetches 16 bytes of pixel row 16 i + L/4 at the tap's
+//     source position, or, outside the image (padding) or past M, an offset
+//     past the buffer's end, which the DMA writes as zeros.  B [32 k][256 B]
+//     is 32 filter rows of 128 output channels.
+//   * LDS layouts as in the DMA GEMM (gemm.hip): A row r keeps its 16-byte
+//     chunk c at c ^ ((r >> 2) & 3), B row k at c ^ 4 (k & 3); A fragments are
+//     ds_read_b128, B fragments ds_read_b64_tr_b16 (K-contiguous lanes from the
+//     channel-contiguous filter rows).
+//   * Four stages in LDS, three in flight: before the barrier of stage s each
+//     wave waits (vmcnt) for its own DMA of stage s only; after it the DMA of
+//     stage s + 3 goes into the buffer stage s - 1 left.
+//   * Results: a half-wave stores one 128-byte run of 32 channels per
+//     accumulator register (non-temporal); rows past M are not stored.
+#include "common.h"
+#include "launch.h"
+
+namespace xtk {
+namespace {
+
+constexpr unsigned kIgOutOfRange = 0x80000000u;  // the input and the filter are < 2 GiB
+typedef float float16v_t __attribute__((ext_vector_type(16)));
+
+struct IgArgs {
+  const unsigned char* src;   // NHWC input
+  const unsigned char* filt;  // [K][CO]
+  float* out;                 // [M][CO]
+  unsigned src_bytes, filt_bytes;
+  int H, W, C, KW, CO;
+  int OH, OW;
+  int pad_t, pad_l, sh, sw, dh, dw;
+  int M;        // N * OH * OW
+  int stages;   // K / 32: one tap's 32 channels each
+  int cs;       // stages per tap: C / 32
+  int ntiles;   // 128-channel tiles: CO / 128
+  int nwg;      // ceil(M / 128) * ntiles
+  Div31 d_ohw, d_ow;
+};
+
+template <bool BF16>
+__device__ __forceinline__ float16v_t ig_mfma(uint4v a, uint4v b, float16v_t c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b), c, 0,
+                                                  0, 0);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
+  constexpr int BM = 128, BN = 128, KB = 64, AB = BM * KB, BR = BN * 2, KR = 32, KSR = 16;
+  constexpr int STAGE = AB + KR * BR;  // 16 KB
+  constexpr int MI = 2, NI = 2;
+  constexpr int PER = 4;  // DMA instructions per wave and stage: two of A, two of B
+  typedef __attribute__((address_space(3))) unsigned char lds_t;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * STAGE];
+  auto buf = [&](int q) { return smem + (q & 3) * STAGE; };
+
+  // workgroup -> (pixel tile, channel tile); with a multiple of 8 workgroups
+  // the 8 XCDs receive contiguous runs, so the channel tiles of one pixel
+  // tile share its input rows in one L2
+  int L = blockIdx.x;
+  if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
+  const int mt = L / p.ntiles;
+  const int m0 = mt * BM, n0 = (L - mt * p.ntiles) * BN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const i32x4 ra = raw_rsrc(p.src, p.src_bytes), rb = raw_rsrc(p.filt, p.filt_bytes);
+  const unsigned ldb = (unsigned)p.CO * 2u;
+
+  // A: this wave's instructions 2 wave + q cover pixel rows 16 (2 wave + q) +
+  // lane / 4; the lane fetches global chunk (lane % 4) ^ ((lane / 16) % 4)
+  // of the stage's 64 bytes, which lands at LDS chunk lane % 4 of its row.
+  int ih0[2], iw0[2];
+  unsigned abase[2];
+  {
+    const unsigned gc = (unsigned)((lane & 3) ^ ((lane >> 4) & 3));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int pix = m0 + 16 * (2 * wave + q) + (lane >> 2);
+      if (pix < p.M) {
+        const int n = (int)p.d_ohw((unsigned)pix);
+        const int rem = pix - n * p.OH * p.OW;
+        const int oh = (int)p.d_ow((unsigned)rem);
+        const int ow = rem - oh * p.OW;
+        ih0[q] = oh * p.sh - p.pad_t;
+        iw0[q] = ow * p.sw - p.pad_l;
+        // the pixel's (possibly out-of-image) origin; valid taps add a
+        // non-negative offset that brings the sum inside the image
+        abase[q] = (unsigned)(((n * p.H + ih0[q]) * p.W + iw0[q]) * p.C) * 2u + gc * 16u;
+      } else {
+        ih0[q] = -(1 << 30);  // never inside the image
+        iw0[q] = 0;
+        abase[q] = 0;
+      }
+    }
+  }
+  // B: instruction 2 wave + q covers filter rows 4 (2 wave + q) + lane / 16;
+  // the lane at LDS chunk lane % 16 of row k fetches global chunk
+  // (lane % 16) ^ 4 (k % 4), and k % 4 = lane / 16.
+  const unsigned vb = (unsigned)(lane >> 4) * ldb + (unsigned)n0 * 2u +
+                      (unsigned)(((lane & 15) ^ (4 * (lane >> 4))) << 4);
+
+  // tap state of the next stage to load
+  int lkh = 0, lkw = 0, lcc = 0, lkt = 0;
+  auto dma_stage = [&](unsigned char* S) {
+    const int dih = lkh * p.dh, diw = lkw * p.dw;
+    const unsigned soff = (unsigned)(((dih * p.W + diw) * p.C + lcc * 32) * 2);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * wave + q;
+      const bool in = (unsigned)(ih0[q] + dih) < (unsigned)p.H && (unsigned)(iw0[q] + diw) < (unsigned)p.W;
+      dma16(ra, lds_addr(S + i * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = 2 * wave + q;
+      dma16(rb, lds_addr(S + AB + i * 1024), vb, (unsigned)(lkt * KR + 4 * i) * ldb);
+    }
+    // next stage: the next 32 channels, then the next tap
+    ++lkt;
+    if (++lcc == p.cs) {
+      lcc = 0;
+      if (++lkw == p.KW) {
+        lkw = 0;
+        ++lkh;
+      }
+    }
+  };
+
+  // fragment offsets (as in the DMA GEMM): A row r at r * 64, chunk c at
+  // c ^ ((r >> 2) & 3); B tile j, read h at boff[j][h] in the stage's first
+  // K step, KSR rows further for the second
+  const int lrow = lane & 31, hi = lane >> 5;
+  int arow[MI], asw[MI], boff[NI][2];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int r = wm * 64 + i * 32 + lrow;
+    arow[i] = r * KB;
+    asw[i] = (r >> 2) & 3;
+  }
+  {
+    const int g = lane >> 4, li = lane & 15;
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
+        const int cb = (wn * 64 + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
+        boff[j][h] = AB + k * BR + (((cb >> 4) ^ (4 * (k & 3))) << 4) + (cb & 15);
+      }
+  }
+  float16v_t acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  auto compute = [&](const unsigned char* S) {
+    uint4v af[2][MI], bf[2][NI];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        af[ks][i] = *reinterpret_cast<const uint4v*>(S + arow[i] + (((ks * 2 + hi) ^ asw[i]) << 4));
+      lds_t* const f = (lds_t*)(S + ks * KSR * BR);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const uint2v l2 = __builtin_bit_cast(
+            uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[j][0])));
+        const uint2v h2 = __builtin_bit_cast(
+            uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[j][1])));
+        bf[ks][j] = uint4v{l2[0], l2[1], h2[0], h2[1]};
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = ig_mfma<BF16>(af[ks][i], bf[ks][j], acc[i][j]);
+  };
+
+  // prologue: stages 0 .. 2 in flight
+  const int ns = p.stages;
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+    if (q < ns) dma_stage(buf(q));
+  for (int s = 0; s < ns; ++s) {
+    // this wave's DMA of stage s landed (stages s + 1, s + 2 may still fly)
+    if (s + 2 < ns) XTK_WAIT_VM(2 * PER);
+    else if (s + 1 < ns) XTK_WAIT_VM(PER);
+    else XTK_WAIT_VM(0);
+    // every wave's DMA of stage s landed and every wave is done with stage
+    // s - 1; a bare barrier (__syncthreads' fence would wait for every DMA)
+    asm volatile("s_barrier" ::: "memory");
+    if (s + 3 < ns) dma_stage(buf(s + 3));
+    compute(buf(s));
+  }
+
+  // D = A x B per 32 x 32 tile: lane l holds channel l % 32 of tile j and
+  // register v pixel row 8 (v / 4) + 4 (l / 32) + v % 4 of tile i
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + lrow;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+        const float x = acc[i][j][v];
+        if (row < p.M) __builtin_nontemporal_store(x, p.out + (long long)row * p.CO + col);
+      }
+    }
+}
+
+}  // namespace
+
+bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
+  const xt::ConvPlan& c = p.conv;
+  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16) return false;
+  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || c.C % 32 || c.CO % 128) return false;
+  if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
+      c.ch.axis == c.cw.axis)
+    return false;
+  // the Blocks tile images [0, gB) x every output row and column once, in the
+  // output's natural NHWC addressing, with one filter
+  const long long gB = p.grid[c.cb.axis], gH = p.grid[c.ch.axis], gW = p.grid[c.cw.axis];
+  if (gH * c.TH != c.out_H || gW * c.TW != c.out_W || c.out_C != c.CO) return false;
+  auto step = [&](const xt::TileAddr& t, int axis) { return axis == 0 ? t.sx : axis == 1 ? t.sy : t.sz; };
+  const long long plane = c.out_H * c.out_W * c.out_C;
+  if (c.out_addr.c0 != 0 || (gB > 1 && step(c.out_addr, c.cb.axis) != plane) ||
+      (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
+      (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
+    return false;
+  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || c.filt_addr.c0 % 8) return false;
+  // the source batch entries the Blocks read: images [0, gB) of an NHWC tensor
+  const long long src_bytes = gB * c.H * c.W * c.C * 2;
+  const long long K = c.KH * c.KW * c.C;
+  const long long filt_bytes = K * c.CO * 2;
+  const long long M = gB * c.out_H * c.out_W;
+  if (src_bytes >= (1LL << 31) || filt_bytes >= (1LL << 31) || M >= (1LL << 31) || c.out_H * c.out_W >= (1LL << 31))
+    return false;
+  const unsigned char* src = static_cast<const unsigned char*>(bufs[c.src_arg]);
+  const unsigned char* filt = static_cast<const unsigned char*>(bufs[c.filt_arg]) + c.filt_addr.c0 * 2;
+  float* out = static_cast<float*>(bufs[c.out_arg]);
+  for (const void* ptr : {(const void*)src, (const void*)filt, (const void*)out})
+    if (reinterpret_cast<uintptr_t>(ptr) % 16) return false;
+  IgArgs a;
+  a.src = src;
+  a.filt = filt;
+  a.out = out;
+  a.src_bytes = static_cast<unsigned>(src_bytes);
+  a.filt_bytes = static_cast<unsigned>(filt_bytes);
+  a.H = (int)c.H;
+  a.W = (int)c.W;
+  a.C = (int)c.C;
+  a.KW = (int)c.KW;
+  a.CO = (int)c.CO;
+  a.OH = (int)c.out_H;
+  a.OW = (int)c.out_W;
+  a.pad_t = (int)c.pad_top;
+  a.pad_l = (int)c.pad_left;
+  a.sh = (int)c.stride_h;
+  a.sw = (int)c.stride_w;
+  a.dh = (int)c.dil_h;
+  a.dw = (int)c.dil_w;
+  a.M = (int)M;
+  a.stages = (int)(K / 32);
+  a.cs = (int)(c.C / 32);
+  a.ntiles = (int)(c.CO / 128);
+  const long long nwg = (M + 127) / 128 * a.ntiles;
+  if (!grid_fits(nwg, 256)) return false;
+  a.nwg = (int)nwg;
+  a.d_ohw = div31((unsigned)(c.out_H * c.out_W));
+  a.d_ow = div31((unsigned)c.out_W);
+  if (c.elem == xt::Elem::BF16) hipLaunchKernelGGL(conv_igemm_kernel<true>, dim3(a.nwg), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(conv_igemm_kernel<false>, dim3(a.nwg), dim3(256), 0, s, a);
+  e = hipGetLastError();
+  return true;
+}
+
+}  // namespace xtk
