@@ -254,13 +254,16 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
         (3, 10, 10, 64, 256, 1, 1, 5, 10, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),    # 1 x 1, Cout 256
         (2, 16, 16, 96, 128, 5, 5, 5, 15, (2, 1, 1, 2), (1, 1), (1, 1), "bf16"),   # Cin 96: three stages a tap, asymmetric pad
         (2, 14, 14, 256, 128, 3, 3, 4, 12, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),   # no padding: 12 x 12 outputs
+        (2, 12, 12, 256, 64, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),    # Cout 64: 256 x 64 tiles
+        (2, 10, 10, 160, 192, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),  # Cout 192: three 64-channel tiles
     ],
 )
 def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
     """Filters too large for the band kernel's LDS (Cin * Cout * taps * 2
-    bytes above ~150 KB) with Cout a multiple of 128 take the implicit-GEMM
-    kernel (conv_igemm.hip): operands by DMA, the input gathered per tap,
-    padding and rows past M read as zeros."""
+    bytes above ~150 KB) with Cout a multiple of 64 take the implicit-GEMM
+    kernel (conv_igemm.hip; 128 x 128 tiles for Cout a multiple of 128, else
+    256 x 64): operands by DMA, the input gathered per tap, padding and rows
+    past M read as zeros."""
     rng = np.random.default_rng(9)
     mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
                    pad=pad, stride=stride, dilation=dil)
@@ -275,6 +278,29 @@ def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil
     o = np.zeros((n, oh, ow, cout), np.float32)
     got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
                   case=f"conv igemm {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil} {dt}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+
+
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,th,tw,dt",
+    [(32, 56, 56, 64, 64, 4, 56, "f16"), (3, 12, 20, 32, 128, 2, 10, "f16"), (2, 9, 7, 64, 64, 9, 7, "bf16")],
+)
+def test_conv2d_igemm_where_the_band_kernel_applies(cuda, monkeypatch, n, h, w, cin, cout, th, tw, dt):
+    """XTILE_AMD_CONV_IGEMM=1 puts the implicit-GEMM kernel ahead of the band
+    kernel: C4's shape (256 x 64 tiles, 392 workgroups) and small ones, 3 x 3
+    "same" convolutions, against the oracle."""
+    monkeypatch.setenv("XTILE_AMD_CONV_IGEMM", "1")
+    rng = np.random.default_rng(10)
+    mod = K.conv2d(n, h, w, cin, cout, 3, 3, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16)
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (3, 3, cin, cout)).astype(np.float32)
+    if dt == "bf16":
+        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    else:
+        x, f = x.astype(np.float16), f.astype(np.float16)
+    o = np.zeros((n, h, w, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda, case=f"conv igemm-first {n}x{h}x{w}x{cin}->{cout} {dt}")[2]
     want = run_oracle(mod, [x, f, o], oracle_threads())[2]
     assert frob_rel(got, want) <= MM_FROB
 

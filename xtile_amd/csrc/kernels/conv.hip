@@ -38,6 +38,7 @@
 // channel and an f32 result; else the generic kernel (conv_general.hip),
 // which takes every tile shape the planner accepts.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.h"
@@ -950,6 +951,11 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   if (e != hipSuccess) return e;
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
+  // XTILE_AMD_CONV_IGEMM=1 puts the implicit-GEMM kernel first (tests run it
+  // on shapes the band kernel takes)
+  const char* igemm_env = std::getenv("XTILE_AMD_CONV_IGEMM");
+  const bool igemm_first = igemm_env && igemm_env[0] == '1';
+  if (igemm_first && launch_conv2d_igemm(p, bufs, s, e)) return e;
   if (try_band(p, bufs, s, max_lds, cus, e)) return e;
   // filters beyond the band kernel's LDS: the implicit GEMM with DMA operands
   if (launch_conv2d_igemm(p, bufs, s, e)) return e;

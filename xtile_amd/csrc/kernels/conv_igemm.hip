@@ -16,24 +16,31 @@
 // kernels; Blocks are independent (README.md:85-89), so the regrouping is a
 // scheduling choice.
 //
-//   * Workgroup tile 128 pixels x 128 channels, four waves of 64 x 64 (2 x 2
-//     tiles of v_mfma_f32_32x32x16_{f16,bf16}); 64 KB of LDS, so two
-//     workgroups share a CU and one's barrier waits are the other's MFMA time.
+//   * Workgroup tiles of 128 pixels x 128 channels (Cout a multiple of 128)
+//     or 256 x 64, four waves of 64 x 64 (2 x 2 tiles of
+//     v_mfma_f32_32x32x16_{f16,bf16}); 64 or 80 KB of LDS, so two workgroups
+//     share a CU and one's barrier waits are the other's MFMA time.
 //   * A K stage is one tap's 32 channels (64 bytes of every pixel row):
-//     A [128 rows][64 B] is an im2col gather done by the DMA itself: lane L of
+//     A [BM rows][64 B] is an im2col gather done by the DMA itself: lane L of
 //     A instruction i fetches 16 bytes of pixel row 16 i + L/4 at the tap's
 //     source position, or, outside the image (padding) or past M, an offset
-//     past the buffer's end, which the DMA writes as zeros.  B [32 k][256 B]
-//     is 32 filter rows of 128 output channels.
+//     past the buffer's end, which the DMA writes as zeros.  B [32 k][2 BN B]
+//     is 32 filter rows of BN output channels.
 //   * LDS layouts as in the DMA GEMM (gemm.hip): A row r keeps its 16-byte
-//     chunk c at c ^ ((r >> 2) & 3), B row k at c ^ 4 (k & 3); A fragments are
+//     chunk c at c ^ ((r >> 2) & 3), B row k at c ^ ig_bsw(k); A fragments are
 //     ds_read_b128, B fragments ds_read_b64_tr_b16 (K-contiguous lanes from the
 //     channel-contiguous filter rows).
-//   * Four stages in LDS, three in flight: before the barrier of stage s each
-//     wave waits (vmcnt) for its own DMA of stage s only; after it the DMA of
-//     stage s + 3 goes into the buffer stage s - 1 left.
+//   * Four stages in LDS, three in flight (the pipeline is described at the
+//     loop).
 //   * Results: a half-wave stores one 128-byte run of 32 channels per
 //     accumulator register (non-temporal); rows past M are not stored.
+//   * Measured (one MI355X, 30 launches, inputs not rotated): 3 x 3, stride 1,
+//     batch 32: 28 x 28 x 128 -> 128 18.3 us (405 TFLOP/s; 161 us on the
+//     generic kernel before), 14 x 14 x 256 -> 256 29.7 us (256 us), 7 x 7 x
+//     512 -> 512 53.4 us (341 us; 52 workgroups for 256 CUs); 1 x 1 56 x 56 x
+//     256 -> 64 16.5 us (the per-unit kernel: 19.7).  C4's shape runs on the
+//     band kernel: this one re-reads every input pixel once per tap from L2
+//     and took 17.3 us there against 13.0.
 #include "common.h"
 #include "launch.h"
 
@@ -54,8 +61,8 @@ struct IgArgs {
   int M;        // N * OH * OW
   int stages;   // K / 32: one tap's 32 channels each
   int cs;       // stages per tap: C / 32
-  int ntiles;   // 128-channel tiles: CO / 128
-  int nwg;      // ceil(M / 128) * ntiles
+  int ntiles;   // channel tiles: CO / BN
+  int nwg;      // ceil(M / BM) * ntiles
   Div31 d_ohw, d_ow;
 };
 
@@ -69,15 +76,37 @@ __device__ __forceinline__ float16v_t ig_mfma(uint4v a, uint4v b, float16v_t c) 
                                                   0, 0);
 }
 
-template <bool BF16>
+// B row k keeps its 16-byte chunk c at c ^ ig_bsw(k): the four rows a
+// half-wave's transposing read covers (k .. k+3, 32 bytes each) then fall in
+// four different 32-byte bank groups of the 256-byte bank window, for rows of
+// 256 bytes (BN = 128: XOR 4 (k % 4)) or 128 bytes (BN = 64: XOR 2 ((k / 2) % 2)).
+template <int BN>
+__device__ __forceinline__ int ig_bsw(int k) {
+  return BN == 128 ? 4 * (k & 3) : 2 * ((k >> 1) & 1);
+}
+
+// BM x BN workgroup tiles, four waves in a WGM x (4 / WGM) layout of 64 x 64
+// wave tiles: (BM, BN) = (128, 128) with 2 x 2 waves or (256, 64) with 4 x 1.
+template <bool BF16, int BM, int BN>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
-  constexpr int BM = 128, BN = 128, KB = 64, AB = BM * KB, BR = BN * 2, KR = 32, KSR = 16;
-  constexpr int STAGE = AB + KR * BR;  // 16 KB
+  // stages in LDS (64 or 80 KB, two workgroups a CU): five, or a pipeline
+  // that also read each stage's fragments during the previous stage's MFMAs
+  // and spread the DMA over them, measured slower on 3 x 3 convs with 128 to
+  // 512 channels (e.g. 28 x 28 x 128: 18.3 us with this loop at four stages,
+  // 19.2 at five, 21.1 / 23.2 pipelined)
+  constexpr int NS = 4;
+  constexpr int KB = 64, AB = BM * KB, BR = BN * 2, KR = 32, KSR = 16;
+  constexpr int STAGE = AB + KR * BR;  // 16 KB or 20 KB
+  constexpr int WGM = BM / 64, WGN = 4 / WGM;
+  static_assert(WGM * WGN == 4 && BN == 64 * WGN, "wave layout");
   constexpr int MI = 2, NI = 2;
-  constexpr int PER = 4;  // DMA instructions per wave and stage: two of A, two of B
+  constexpr int PA = BM / 64;        // A DMA instructions per wave and stage (16 rows each)
+  constexpr int PB = BN / 64;        // B DMA instructions per wave and stage
+  constexpr int PER = PA + PB;       // DMA instructions per wave and stage
+  constexpr int CPR = BR / 16, RPI = 1024 / BR;  // B chunks per row, rows per DMA instruction
   typedef __attribute__((address_space(3))) unsigned char lds_t;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * STAGE];
-  auto buf = [&](int q) { return smem + (q & 3) * STAGE; };
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
+  auto buf = [&](int q) { return smem + (q % NS) * STAGE; };
 
   // workgroup -> (pixel tile, channel tile); with a multiple of 8 workgroups
   // the 8 XCDs receive contiguous runs, so the channel tiles of one pixel
@@ -88,21 +117,21 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   const int m0 = mt * BM, n0 = (L - mt * p.ntiles) * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
   const i32x4 ra = raw_rsrc(p.src, p.src_bytes), rb = raw_rsrc(p.filt, p.filt_bytes);
   const unsigned ldb = (unsigned)p.CO * 2u;
 
-  // A: this wave's instructions 2 wave + q cover pixel rows 16 (2 wave + q) +
-  // lane / 4; the lane fetches global chunk (lane % 4) ^ ((lane / 16) % 4)
+  // A: this wave's instructions PA wave + q cover pixel rows 16 (PA wave + q)
+  // + lane / 4; the lane fetches global chunk (lane % 4) ^ ((lane / 16) % 4)
   // of the stage's 64 bytes, which lands at LDS chunk lane % 4 of its row.
-  int ih0[2], iw0[2];
-  unsigned abase[2];
+  int ih0[PA], iw0[PA];
+  unsigned abase[PA];
   {
     const unsigned gc = (unsigned)((lane & 3) ^ ((lane >> 4) & 3));
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int pix = m0 + 16 * (2 * wave + q) + (lane >> 2);
+    for (int q = 0; q < PA; ++q) {
+      const int pix = m0 + 16 * (PA * wave + q) + (lane >> 2);
       if (pix < p.M) {
         const int n = (int)p.d_ohw((unsigned)pix);
         const int rem = pix - n * p.OH * p.OW;
@@ -120,29 +149,34 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
       }
     }
   }
-  // B: instruction 2 wave + q covers filter rows 4 (2 wave + q) + lane / 16;
-  // the lane at LDS chunk lane % 16 of row k fetches global chunk
-  // (lane % 16) ^ 4 (k % 4), and k % 4 = lane / 16.
-  const unsigned vb = (unsigned)(lane >> 4) * ldb + (unsigned)n0 * 2u +
-                      (unsigned)(((lane & 15) ^ (4 * (lane >> 4))) << 4);
+  // B: instruction PB wave + q covers filter rows RPI (PB wave + q) + lane /
+  // CPR; the lane at LDS chunk lane % CPR of row k fetches global chunk
+  // (lane % CPR) ^ ig_bsw(k), and ig_bsw(k) depends on lane / CPR only.
+  const unsigned vb = (unsigned)(lane / CPR) * ldb + (unsigned)n0 * 2u +
+                      (unsigned)(((lane % CPR) ^ ig_bsw<BN>(lane / CPR)) << 4);
 
   // tap state of the next stage to load
   int lkh = 0, lkw = 0, lcc = 0, lkt = 0;
-  auto dma_stage = [&](unsigned char* S) {
-    const int dih = lkh * p.dh, diw = lkw * p.dw;
-    const unsigned soff = (unsigned)(((dih * p.W + diw) * p.C + lcc * 32) * 2);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = 2 * wave + q;
+  int dih = 0, diw = 0;
+  unsigned soff = 0;
+  auto tap_begin = [&]() {
+    dih = lkh * p.dh;
+    diw = lkw * p.dw;
+    soff = (unsigned)(((dih * p.W + diw) * p.C + lcc * 32) * 2);
+  };
+  // DMA instruction q of the stage being loaded (A for q < PA, then B)
+  auto dma_one = [&](unsigned char* S, int q) {
+    if (q < PA) {
+      const int i = PA * wave + q;
       const bool in = (unsigned)(ih0[q] + dih) < (unsigned)p.H && (unsigned)(iw0[q] + diw) < (unsigned)p.W;
       dma16(ra, lds_addr(S + i * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
+    } else {
+      const int i = PB * wave + (q - PA);
+      dma16(rb, lds_addr(S + AB + i * 1024), vb, (unsigned)(lkt * KR + RPI * i) * ldb);
     }
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int i = 2 * wave + q;
-      dma16(rb, lds_addr(S + AB + i * 1024), vb, (unsigned)(lkt * KR + 4 * i) * ldb);
-    }
-    // next stage: the next 32 channels, then the next tap
+  };
+  // after a stage's DMA: the next 32 channels, then the next tap
+  auto tap_next = [&]() {
     ++lkt;
     if (++lcc == p.cs) {
       lcc = 0;
@@ -151,6 +185,12 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
         ++lkh;
       }
     }
+  };
+  auto dma_stage = [&](unsigned char* S) {
+    tap_begin();
+#pragma unroll
+    for (int q = 0; q < PER; ++q) dma_one(S, q);
+    tap_next();
   };
 
   // fragment offsets (as in the DMA GEMM): A row r at r * 64, chunk c at
@@ -172,7 +212,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
       for (int h = 0; h < 2; ++h) {
         const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
         const int cb = (wn * 64 + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
-        boff[j][h] = AB + k * BR + (((cb >> 4) ^ (4 * (k & 3))) << 4) + (cb & 15);
+        boff[j][h] = AB + k * BR + (((cb >> 4) ^ ig_bsw<BN>(k)) << 4) + (cb & 15);
       }
   }
   float16v_t acc[MI][NI];
@@ -210,20 +250,23 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
         for (int j = 0; j < NI; ++j) acc[i][j] = ig_mfma<BF16>(af[ks][i], bf[ks][j], acc[i][j]);
   };
 
-  // prologue: stages 0 .. 2 in flight
+  // NS - 1 stages in flight.  Before the barrier of stage s each wave waits
+  // (vmcnt) for its own DMA of stage s only (s + 1 .. s + NS - 2 may stay in
+  // flight); after it every wave's DMA of stage s has landed and every wave
+  // is done with stage s - 1, whose buffer then receives stage s + NS - 1.
+  // The barriers are bare s_barriers: __syncthreads' release fence would wait
+  // for every DMA in flight.
   const int ns = p.stages;
 #pragma unroll
-  for (int q = 0; q < 3; ++q)
+  for (int q = 0; q < NS - 1; ++q)
     if (q < ns) dma_stage(buf(q));
   for (int s = 0; s < ns; ++s) {
-    // this wave's DMA of stage s landed (stages s + 1, s + 2 may still fly)
-    if (s + 2 < ns) XTK_WAIT_VM(2 * PER);
-    else if (s + 1 < ns) XTK_WAIT_VM(PER);
+    const int fly = min(ns - 1, s + NS - 2) - s;  // this wave's later stages in flight
+    if (fly >= 2) XTK_WAIT_VM(2 * PER);
+    else if (fly >= 1) XTK_WAIT_VM(PER);
     else XTK_WAIT_VM(0);
-    // every wave's DMA of stage s landed and every wave is done with stage
-    // s - 1; a bare barrier (__syncthreads' fence would wait for every DMA)
     asm volatile("s_barrier" ::: "memory");
-    if (s + 3 < ns) dma_stage(buf(s + 3));
+    if (s + NS - 1 < ns) dma_stage(buf(s + NS - 1));
     compute(buf(s));
   }
 
@@ -248,7 +291,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
 bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
   const xt::ConvPlan& c = p.conv;
   if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16) return false;
-  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || c.C % 32 || c.CO % 128) return false;
+  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || c.C % 32 || c.CO % 64) return false;
   if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
       c.ch.axis == c.cw.axis)
     return false;
@@ -297,14 +340,23 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.M = (int)M;
   a.stages = (int)(K / 32);
   a.cs = (int)(c.C / 32);
-  a.ntiles = (int)(c.CO / 128);
-  const long long nwg = (M + 127) / 128 * a.ntiles;
+  // 128 x 128 tiles when Cout allows, else 256 x 64
+  const bool wide = c.CO % 128 == 0;
+  const int bm = wide ? 128 : 256, bn = wide ? 128 : 64;
+  a.ntiles = (int)(c.CO / bn);
+  const long long nwg = (M + bm - 1) / bm * a.ntiles;
   if (!grid_fits(nwg, 256)) return false;
   a.nwg = (int)nwg;
   a.d_ohw = div31((unsigned)(c.out_H * c.out_W));
   a.d_ow = div31((unsigned)c.out_W);
-  if (c.elem == xt::Elem::BF16) hipLaunchKernelGGL(conv_igemm_kernel<true>, dim3(a.nwg), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(conv_igemm_kernel<false>, dim3(a.nwg), dim3(256), 0, s, a);
+  const bool bf = c.elem == xt::Elem::BF16;
+  if (wide) {
+    if (bf) hipLaunchKernelGGL((conv_igemm_kernel<true, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((conv_igemm_kernel<false, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a);
+  } else {
+    if (bf) hipLaunchKernelGGL((conv_igemm_kernel<true, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((conv_igemm_kernel<false, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);
+  }
   e = hipGetLastError();
   return true;
 }
