@@ -283,6 +283,33 @@ def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil
 
 
 @pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,first",
+    [
+        (2, 12, 12, 256, 128, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), "0"),  # 295 KB filter: 128 x 128 tiles
+        (2, 8, 8, 320, 64, 3, 3, 8, 8, (1, 1, 1, 1), (1, 1), "0"),      # Cin 320: 256 x 64 tiles, 5 stages a tap
+        (2, 13, 11, 128, 192, 3, 3, 7, 6, (1, 1, 1, 1), (2, 2), "0"),   # Cout 192: band declines (> 128)
+        (1, 32, 64, 128, 64, 3, 3, 32, 64, (1, 1, 1, 1), (1, 1), "1"),  # kernels/conv2d.py, implicit GEMM first
+    ],
+)
+def test_conv2d_igemm_i8_bit_exact(cuda, monkeypatch, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, first):
+    """i8 source and filter (the reference's own load_conv2d dtype) on the
+    implicit-GEMM kernel: a K stage is 64 channels, filter fragments by
+    ds_read_b64_tr_b8, exact i32 sums rounded to f32 once: bit-exact."""
+    monkeypatch.setenv("XTILE_AMD_CONV_IGEMM", first)
+    rng = np.random.default_rng(11)
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.int8, pad=pad, stride=stride)
+    oh = (h + pad[0] + pad[2] - (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - (kw - 1) - 1) // stride[1] + 1
+    x = rng.integers(-128, 128, (n, h, w, cin), dtype=np.int8)
+    f = rng.integers(-128, 128, (kh, kw, cin, cout), dtype=np.int8)
+    o = np.zeros((n, oh, ow, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], ["i8", "i8", "f32"], cuda,
+                  case=f"conv igemm i8 {n}x{h}x{w}x{cin}->{cout} s{stride} first={first}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize(
     "n,h,w,cin,cout,th,tw,dt",
     [(32, 56, 56, 64, 64, 4, 56, "f16"), (3, 12, 20, 32, 128, 2, 10, "f16"), (2, 9, 7, 64, 64, 9, 7, "bf16")],
 )

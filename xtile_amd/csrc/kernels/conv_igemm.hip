@@ -18,18 +18,20 @@
 //
 //   * Workgroup tiles of 128 pixels x 128 channels (Cout a multiple of 128)
 //     or 256 x 64, four waves of 64 x 64 (2 x 2 tiles of
-//     v_mfma_f32_32x32x16_{f16,bf16}); 64 or 80 KB of LDS, so two workgroups
-//     share a CU and one's barrier waits are the other's MFMA time.
-//   * A K stage is one tap's 32 channels (64 bytes of every pixel row):
+//     v_mfma_f32_32x32x16_{f16,bf16}, f32 sums, or v_mfma_i32_32x32x32_i8,
+//     exact i32 sums rounded to f32 once); 64 or 80 KB of LDS, so two
+//     workgroups share a CU and one's barrier waits are the other's MFMA time.
+//   * A K stage is 64 bytes of one tap's channels in every pixel row (32
+//     f16 / bf16 or 64 i8 channels):
 //     A [BM rows][64 B] is an im2col gather done by the DMA itself: lane L of
 //     A instruction i fetches 16 bytes of pixel row 16 i + L/4 at the tap's
 //     source position, or, outside the image (padding) or past M, an offset
-//     past the buffer's end, which the DMA writes as zeros.  B [32 k][2 BN B]
-//     is 32 filter rows of BN output channels.
+//     past the buffer's end, which the DMA writes as zeros.  B [64 / esize
+//     k][BN esize B] holds the stage's filter rows for BN output channels.
 //   * LDS layouts as in the DMA GEMM (gemm.hip): A row r keeps its 16-byte
 //     chunk c at c ^ ((r >> 2) & 3), B row k at c ^ ig_bsw(k); A fragments are
-//     ds_read_b128, B fragments ds_read_b64_tr_b16 (K-contiguous lanes from the
-//     channel-contiguous filter rows).
+//     ds_read_b128, B fragments ds_read_b64_tr_b16 / _tr_b8 (K-contiguous
+//     lanes from the channel-contiguous filter rows).
 //   * Four stages in LDS, three in flight (the pipeline is described at the
 //     loop).
 //   * Results: a half-wave stores one 128-byte run of 32 channels per
@@ -59,16 +61,32 @@ struct IgArgs {
   int OH, OW;
   int pad_t, pad_l, sh, sw, dh, dw;
   int M;        // N * OH * OW
-  int stages;   // K / 32: one tap's 32 channels each
-  int cs;       // stages per tap: C / 32
+  int stages;   // K * esize / 64: 64 bytes of one tap's channels each
+  int cs;       // stages per tap: C * esize / 64
   int ntiles;   // channel tiles: CO / BN
   int nwg;      // ceil(M / BM) * ntiles
   Div31 d_ohw, d_ow;
 };
 
-template <bool BF16>
-__device__ __forceinline__ float16v_t ig_mfma(uint4v a, uint4v b, float16v_t c) {
-  if constexpr (BF16)
+enum { kIgF16 = 0, kIgBF16 = 1, kIgI8 = 2 };
+typedef int int16v_t __attribute__((ext_vector_type(16)));
+
+// f16 / bf16 accumulate in f32; i8 in i32 (exact), rounded to f32 once when stored
+template <int ELEM>
+struct IgAcc {
+  typedef float16v_t type;
+};
+template <>
+struct IgAcc<kIgI8> {
+  typedef int16v_t type;
+};
+
+template <int ELEM>
+__device__ __forceinline__ typename IgAcc<ELEM>::type ig_mfma(uint4v a, uint4v b, typename IgAcc<ELEM>::type c) {
+  if constexpr (ELEM == kIgI8)
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0,
+                                                 0, 0);
+  else if constexpr (ELEM == kIgBF16)
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
   else
@@ -76,18 +94,21 @@ __device__ __forceinline__ float16v_t ig_mfma(uint4v a, uint4v b, float16v_t c) 
                                                   0, 0);
 }
 
-// B row k keeps its 16-byte chunk c at c ^ ig_bsw(k): the four rows a
-// half-wave's transposing read covers (k .. k+3, 32 bytes each) then fall in
-// four different 32-byte bank groups of the 256-byte bank window, for rows of
-// 256 bytes (BN = 128: XOR 4 (k % 4)) or 128 bytes (BN = 64: XOR 2 ((k / 2) % 2)).
-template <int BN>
+// B row k (BR = BN * esize bytes) keeps its 16-byte chunk c at c ^ ig_bsw(k),
+// so that the rows one 16-lane group of a transposing read covers fall in
+// distinct bank groups of the 256-byte bank window.  16-bit: four rows of 32
+// bytes (ds_read_b64_tr_b16); rows of 256 bytes XOR 4 (k % 4), of 128 bytes
+// XOR 2 ((k / 2) % 2).  8-bit: eight rows of 16 bytes (ds_read_b64_tr_b8);
+// rows of 128 bytes XOR (k / 2) % 4, of 64 bytes XOR (k / 4) % 2.
+template <int ES, int BR>
 __device__ __forceinline__ int ig_bsw(int k) {
-  return BN == 128 ? 4 * (k & 3) : 2 * ((k >> 1) & 1);
+  if constexpr (ES == 2) return BR == 256 ? 4 * (k & 3) : 2 * ((k >> 1) & 1);
+  else return BR == 128 ? (k >> 1) & 3 : (k >> 2) & 1;
 }
 
 // BM x BN workgroup tiles, four waves in a WGM x (4 / WGM) layout of 64 x 64
 // wave tiles: (BM, BN) = (128, 128) with 2 x 2 waves or (256, 64) with 4 x 1.
-template <bool BF16, int BM, int BN>
+template <int ELEM, int BM, int BN>
 __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // stages in LDS (64 or 80 KB, two workgroups a CU): five, or a pipeline
   // that also read each stage's fragments during the previous stage's MFMAs
@@ -95,8 +116,12 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // 512 channels (e.g. 28 x 28 x 128: 18.3 us with this loop at four stages,
   // 19.2 at five, 21.1 / 23.2 pipelined)
   constexpr int NS = 4;
-  constexpr int KB = 64, AB = BM * KB, BR = BN * 2, KR = 32, KSR = 16;
+  constexpr int ES = ELEM == kIgI8 ? 1 : 2;  // bytes per element
+  // a stage is 64 bytes of K: 32 f16 / bf16 or 64 i8 channels; a K step of
+  // the MFMAs is 32 bytes (KSR filter rows)
+  constexpr int KB = 64, AB = BM * KB, BR = BN * ES, KR = 64 / ES, KSR = 32 / ES;
   constexpr int STAGE = AB + KR * BR;  // 16 KB or 20 KB
+  typedef typename IgAcc<ELEM>::type acc_t;
   constexpr int WGM = BM / 64, WGN = 4 / WGM;
   static_assert(WGM * WGN == 4 && BN == 64 * WGN, "wave layout");
   constexpr int MI = 2, NI = 2;
@@ -120,7 +145,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   const int wm = wave / WGN, wn = wave % WGN;
 
   const i32x4 ra = raw_rsrc(p.src, p.src_bytes), rb = raw_rsrc(p.filt, p.filt_bytes);
-  const unsigned ldb = (unsigned)p.CO * 2u;
+  const unsigned ldb = (unsigned)(p.CO * ES);
 
   // A: this wave's instructions PA wave + q cover pixel rows 16 (PA wave + q)
   // + lane / 4; the lane fetches global chunk (lane % 4) ^ ((lane / 16) % 4)
@@ -141,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
         iw0[q] = ow * p.sw - p.pad_l;
         // the pixel's (possibly out-of-image) origin; valid taps add a
         // non-negative offset that brings the sum inside the image
-        abase[q] = (unsigned)(((n * p.H + ih0[q]) * p.W + iw0[q]) * p.C) * 2u + gc * 16u;
+        abase[q] = (unsigned)(((n * p.H + ih0[q]) * p.W + iw0[q]) * p.C) * (unsigned)ES + gc * 16u;
       } else {
         ih0[q] = -(1 << 30);  // never inside the image
         iw0[q] = 0;
@@ -152,8 +177,8 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // B: instruction PB wave + q covers filter rows RPI (PB wave + q) + lane /
   // CPR; the lane at LDS chunk lane % CPR of row k fetches global chunk
   // (lane % CPR) ^ ig_bsw(k), and ig_bsw(k) depends on lane / CPR only.
-  const unsigned vb = (unsigned)(lane / CPR) * ldb + (unsigned)n0 * 2u +
-                      (unsigned)(((lane % CPR) ^ ig_bsw<BN>(lane / CPR)) << 4);
+  const unsigned vb = (unsigned)(lane / CPR) * ldb + (unsigned)(n0 * ES) +
+                      (unsigned)(((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4);
 
   // tap state of the next stage to load
   int lkh = 0, lkw = 0, lcc = 0, lkt = 0;
@@ -162,7 +187,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   auto tap_begin = [&]() {
     dih = lkh * p.dh;
     diw = lkw * p.dw;
-    soff = (unsigned)(((dih * p.W + diw) * p.C + lcc * 32) * 2);
+    soff = (unsigned)((dih * p.W + diw) * p.C * ES + lcc * 64);
   };
   // DMA instruction q of the stage being loaded (A for q < PA, then B)
   auto dma_one = [&](unsigned char* S, int q) {
@@ -210,18 +235,24 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
     for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
-        const int cb = (wn * 64 + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
-        boff[j][h] = AB + k * BR + (((cb >> 4) ^ ig_bsw<BN>(k)) << 4) + (cb & 15);
+        int k, cb;
+        if constexpr (ES == 2) {
+          k = 8 * (g >> 1) + 4 * h + (li >> 2);
+          cb = (wn * 64 + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
+        } else {
+          k = 16 * (g >> 1) + 8 * h + (li >> 1);
+          cb = wn * 64 + j * 32 + 16 * (g & 1) + 8 * (li & 1);
+        }
+        boff[j][h] = AB + k * BR + (((cb >> 4) ^ ig_bsw<ES, BR>(k)) << 4) + (cb & 15);
       }
   }
-  float16v_t acc[MI][NI];
+  acc_t acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
   auto compute = [&](const unsigned char* S) {
     uint4v af[2][MI], bf[2][NI];
@@ -233,12 +264,18 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
       lds_t* const f = (lds_t*)(S + ks * KSR * BR);
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const uint2v l2 = __builtin_bit_cast(
-            uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[j][0])));
-        const uint2v h2 = __builtin_bit_cast(
-            uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[j][1])));
+        uint2v l2, h2;
+        if constexpr (ES == 2) {
+          l2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                              reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[j][0])));
+          h2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                              reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[j][1])));
+        } else {
+          l2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                              reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[j][0])));
+          h2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                              reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[j][1])));
+        }
         bf[ks][j] = uint4v{l2[0], l2[1], h2[0], h2[1]};
       }
     }
@@ -247,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = ig_mfma<BF16>(af[ks][i], bf[ks][j], acc[i][j]);
+        for (int j = 0; j < NI; ++j) acc[i][j] = ig_mfma<ELEM>(af[ks][i], bf[ks][j], acc[i][j]);
   };
 
   // NS - 1 stages in flight.  Before the barrier of stage s each wave waits
@@ -280,7 +317,9 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
-        const float x = acc[i][j][v];
+        // through a scalar (a bit-cast of an ext_vector element lvalue reads
+        // element 0); an i8 sum is an exact i32, rounded to f32 once
+        const float x = static_cast<float>(acc[i][j][v]);
         if (row < p.M) __builtin_nontemporal_store(x, p.out + (long long)row * p.CO + col);
       }
     }
@@ -290,8 +329,11 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
 
 bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
   const xt::ConvPlan& c = p.conv;
-  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16) return false;
-  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || c.C % 32 || c.CO % 64) return false;
+  const bool i8 = c.elem == xt::Elem::I8;
+  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16 && !i8) return false;
+  const long long es = i8 ? 1 : 2;
+  // a K stage is 64 bytes of one tap's channels
+  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || (c.C * es) % 64 || c.CO % 64) return false;
   if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
       c.ch.axis == c.cw.axis)
     return false;
@@ -305,16 +347,16 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
       (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
-  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || c.filt_addr.c0 % 8) return false;
+  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || (c.filt_addr.c0 * es) % 16) return false;
   // the source batch entries the Blocks read: images [0, gB) of an NHWC tensor
-  const long long src_bytes = gB * c.H * c.W * c.C * 2;
+  const long long src_bytes = gB * c.H * c.W * c.C * es;
   const long long K = c.KH * c.KW * c.C;
-  const long long filt_bytes = K * c.CO * 2;
+  const long long filt_bytes = K * c.CO * es;
   const long long M = gB * c.out_H * c.out_W;
   if (src_bytes >= (1LL << 31) || filt_bytes >= (1LL << 31) || M >= (1LL << 31) || c.out_H * c.out_W >= (1LL << 31))
     return false;
   const unsigned char* src = static_cast<const unsigned char*>(bufs[c.src_arg]);
-  const unsigned char* filt = static_cast<const unsigned char*>(bufs[c.filt_arg]) + c.filt_addr.c0 * 2;
+  const unsigned char* filt = static_cast<const unsigned char*>(bufs[c.filt_arg]) + c.filt_addr.c0 * es;
   float* out = static_cast<float*>(bufs[c.out_arg]);
   for (const void* ptr : {(const void*)src, (const void*)filt, (const void*)out})
     if (reinterpret_cast<uintptr_t>(ptr) % 16) return false;
@@ -338,8 +380,8 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.dh = (int)c.dil_h;
   a.dw = (int)c.dil_w;
   a.M = (int)M;
-  a.stages = (int)(K / 32);
-  a.cs = (int)(c.C / 32);
+  a.stages = (int)(K * es / 64);
+  a.cs = (int)(c.C * es / 64);
   // 128 x 128 tiles when Cout allows, else 256 x 64
   const bool wide = c.CO % 128 == 0;
   const int bm = wide ? 128 : 256, bn = wide ? 128 : 64;
@@ -349,14 +391,16 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.nwg = (int)nwg;
   a.d_ohw = div31((unsigned)(c.out_H * c.out_W));
   a.d_ow = div31((unsigned)c.out_W);
-  const bool bf = c.elem == xt::Elem::BF16;
-  if (wide) {
-    if (bf) hipLaunchKernelGGL((conv_igemm_kernel<true, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((conv_igemm_kernel<false, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a);
-  } else {
-    if (bf) hipLaunchKernelGGL((conv_igemm_kernel<true, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((conv_igemm_kernel<false, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);
-  }
+  const int el = i8 ? kIgI8 : c.elem == xt::Elem::BF16 ? kIgBF16 : kIgF16;
+#define XT_IG(E)                                                                                       \
+  do {                                                                                                 \
+    if (wide) hipLaunchKernelGGL((conv_igemm_kernel<E, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((conv_igemm_kernel<E, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);       \
+  } while (0)
+  if (el == kIgI8) XT_IG(kIgI8);
+  else if (el == kIgBF16) XT_IG(kIgBF16);
+  else XT_IG(kIgF16);
+#undef XT_IG
   e = hipGetLastError();
   return true;
 }
