@@ -282,6 +282,44 @@ def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil
     assert frob_rel(got, want) <= MM_FROB
 
 
+def test_conv2d_igemm_k_split_in_a_graph(cuda):
+    """A K-split implicit-GEMM conv (52 tiles: K in 4 ranges, a zero-fill
+    kernel, then partial sums added atomically) captured in a HIP graph and
+    replayed three times, with eager work and synchronisations between the
+    replays: every replay matches the eager launch and the oracle (the
+    atomic addition order may change the last bits, so to a relative 1e-6)."""
+    import torch
+
+    rng = np.random.default_rng(12)
+    n, h, w, cin, cout = 32, 7, 7, 512, 512
+    mod = K.conv2d(n, h, w, cin, cout, 3, 3, 7, 7)
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float16)
+    f = rng.normal(0, 0.1, (3, 3, cin, cout)).astype(np.float16)
+    o = np.zeros((n, h, w, cout), np.float32)
+    eager = run_gpu(mod, [x, f, o], ["f16", "f16", "f32"], cuda, case="conv igemm k-split eager")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(eager, want) <= MM_FROB
+    print("[gpu] conv igemm k-split graph capture", flush=True)
+    dx, df = torch.from_numpy(x).to(cuda), torch.from_numpy(f).to(cuda)
+    do = torch.full((n, h, w, cout), 7.0, dtype=torch.float32, device=cuda)  # the zero fill must clear this
+    stream = torch.cuda.Stream(device=cuda)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        xt.launch(mod, dx, df, do, stream=stream)  # warm-up outside the capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            xt.launch(mod, dx, df, do, stream=stream)
+    torch.cuda.synchronize()
+    for r in range(3):
+        do.fill_(float(r + 3))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = do.cpu().numpy()
+        assert frob_rel(got, eager) <= 1e-6, r
+        assert frob_rel(got, want) <= MM_FROB, r
+
+
 @pytest.mark.parametrize(
     "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,first",
     [

@@ -36,6 +36,11 @@
 //     loop).
 //   * Results: a half-wave stores one 128-byte run of 32 channels per
 //     accumulator register (non-temporal); rows past M are not stored.
+//   * When the tiles fill at most half the CUs (deep layers: few pixels, many
+//     channels), f16 / bf16 tiles split K into ranges of whole stages, one
+//     workgroup each, whose partial sums are added atomically into the
+//     zero-filled output (so the f32 addition order, and the last bits,
+//     vary between runs; i8 is never split and stays exact).
 //   * Measured (one MI355X, 30 launches, inputs not rotated): 3 x 3, stride 1,
 //     batch 32: 28 x 28 x 128 -> 128 18.3 us (405 TFLOP/s; 161 us on the
 //     generic kernel before), 14 x 14 x 256 -> 256 29.7 us (256 us), 7 x 7 x
@@ -43,6 +48,8 @@
 //     256 -> 64 16.5 us (the per-unit kernel: 19.7).  C4's shape runs on the
 //     band kernel: this one re-reads every input pixel once per tap from L2
 //     and took 17.3 us there against 13.0.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
@@ -64,7 +71,10 @@ struct IgArgs {
   int stages;   // K * esize / 64: 64 bytes of one tap's channels each
   int cs;       // stages per tap: C * esize / 64
   int ntiles;   // channel tiles: CO / BN
-  int nwg;      // ceil(M / BM) * ntiles
+  int tiles;    // ceil(M / BM) * ntiles
+  int ksplit;   // K ranges per tile (1: one workgroup per tile)
+  int kstages;  // stages per K range (the last may have fewer)
+  int nwg;      // tiles * ksplit
   Div31 d_ohw, d_ow;
 };
 
@@ -133,11 +143,13 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
   auto buf = [&](int q) { return smem + (q % NS) * STAGE; };
 
-  // workgroup -> (pixel tile, channel tile); with a multiple of 8 workgroups
-  // the 8 XCDs receive contiguous runs, so the channel tiles of one pixel
-  // tile share its input rows in one L2
+  // workgroup -> (K range, pixel tile, channel tile); with a multiple of 8
+  // workgroups the 8 XCDs receive contiguous runs, so the channel tiles of
+  // one pixel tile share its input rows in one L2
   int L = blockIdx.x;
   if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
+  const int kr = L / p.tiles;
+  L -= kr * p.tiles;
   const int mt = L / p.ntiles;
   const int m0 = mt * BM, n0 = (L - mt * p.ntiles) * BN;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -181,7 +193,11 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
                       (unsigned)(((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4);
 
   // tap state of the next stage to load
-  int lkh = 0, lkw = 0, lcc = 0, lkt = 0;
+  // this workgroup's stages [s_begin, s_begin + ns)
+  const int s_begin = kr * p.kstages;
+  int lkt = s_begin, lcc = s_begin % p.cs, lkh = 0, lkw = s_begin / p.cs;
+  lkh = lkw / p.KW;
+  lkw -= lkh * p.KW;
   int dih = 0, diw = 0;
   unsigned soff = 0;
   auto tap_begin = [&]() {
@@ -293,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // is done with stage s - 1, whose buffer then receives stage s + NS - 1.
   // The barriers are bare s_barriers: __syncthreads' release fence would wait
   // for every DMA in flight.
-  const int ns = p.stages;
+  const int ns = min(p.kstages, p.stages - s_begin);
 #pragma unroll
   for (int q = 0; q < NS - 1; ++q)
     if (q < ns) dma_stage(buf(q));
@@ -320,9 +336,21 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
         // through a scalar (a bit-cast of an ext_vector element lvalue reads
         // element 0); an i8 sum is an exact i32, rounded to f32 once
         const float x = static_cast<float>(acc[i][j][v]);
-        if (row < p.M) __builtin_nontemporal_store(x, p.out + (long long)row * p.CO + col);
+        if (row >= p.M) continue;
+        float* const o = p.out + (long long)row * p.CO + col;
+        // K split: the ranges' partial sums meet in the zero-filled output
+        // (f16 / bf16 only; the order of the additions varies)
+        if (p.ksplit > 1) __hip_atomic_fetch_add(o, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else __builtin_nontemporal_store(x, o);
       }
     }
+}
+
+// Zero-fills n floats (a kernel, not hipMemsetAsync, so that a captured graph
+// replays it correctly).
+__global__ __launch_bounds__(256) void ig_zero_kernel(float4v* __restrict__ o, long long n4) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) __builtin_nontemporal_store(float4v{0.f, 0.f, 0.f, 0.f}, o + i);
 }
 
 }  // namespace
@@ -386,9 +414,31 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   const bool wide = c.CO % 128 == 0;
   const int bm = wide ? 128 : 256, bn = wide ? 128 : 64;
   a.ntiles = (int)(c.CO / bn);
-  const long long nwg = (M + bm - 1) / bm * a.ntiles;
-  if (!grid_fits(nwg, 256)) return false;
+  const long long tiles = (M + bm - 1) / bm * a.ntiles;
+  // K split when the tiles fill at most half the CUs (f16 / bf16: i8 sums stay
+  // exact and whole): up to one workgroup a CU, at least 16 stages each.
+  // Measured (batch 32, 3 x 3): 7 x 7 x 512 -> 512 (52 tiles) 56.9 us whole,
+  // 27.7 split in 4; 14 x 14 x 256 -> 256 (98 tiles) 31.3 / 27.9 in 2; 28 x 28
+  // x 128 -> 128 (196 tiles) 19.8 whole, 33.0 in 2 (the zero fill and the
+  // atomic adds of the output cost more than the idle CUs)
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  long long ksplit = 1;
+  if (!i8 && tiles * 2 <= cus) ksplit = std::max(1LL, std::min<long long>(cus / tiles, a.stages / 16));
+  a.kstages = (int)((a.stages + ksplit - 1) / ksplit);
+  ksplit = (a.stages + a.kstages - 1) / a.kstages;
+  const long long nwg = tiles * ksplit;
+  if (!grid_fits(nwg, 256) || M * c.CO % 4) return false;
+  a.tiles = (int)tiles;
+  a.ksplit = (int)ksplit;
   a.nwg = (int)nwg;
+  if (ksplit > 1) {
+    const long long n4 = M * c.CO / 4;
+    hipLaunchKernelGGL(ig_zero_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<float4v*>(out), n4);
+  }
   a.d_ohw = div31((unsigned)(c.out_H * c.out_W));
   a.d_ow = div31((unsigned)c.out_W);
   const int el = i8 ? kIgI8 : c.elem == xt::Elem::BF16 ? kIgBF16 : kIgF16;
