@@ -590,6 +590,59 @@ def test_matmul_epilogue_variants(cuda, dt, scale, bias, ftoi):
         assert frob_rel(got, want) <= MM_FROB
 
 
+@pytest.mark.parametrize(
+    "dt,m_,n_,k_",
+    [("f16", 1024, 1024, 4096),   # 16 tiles of 256 x 256: K in 8 ranges of 16 stages
+     ("bf16", 1024, 2048, 2048),  # 32 tiles: 4 ranges
+     ("f16", 512, 768, 1536)],    # 6 tiles: K 1536 = 48 stages, 3 ranges
+)
+def test_matmul_k_split(cuda, dt, m_, n_, k_):
+    """f32 GEMMs without an epilogue whose 256 x 256 tiles fill at most an
+    eighth of the CUs split K; the partial sums are added atomically into the
+    zero-filled output (the output starts non-zero here, so the fill is
+    checked too)."""
+    rng = np.random.default_rng(14)
+    mod = K.matmul_bf16(m_, n_, k_, 256, 128) if dt == "bf16" else K.matmul_f16(m_, n_, k_, 128, 128)
+    a = rng.normal(0, 1, (m_, k_)).astype(np.float32)
+    b = rng.normal(0, 1, (k_, n_)).astype(np.float32)
+    a, b = (f32_to_bf16_bits(a), f32_to_bf16_bits(b)) if dt == "bf16" else (a.astype(np.float16), b.astype(np.float16))
+    c = np.full((m_, n_), 5.0, np.float32)
+    got = run_gpu(mod, [a, b, c], [dt, dt, "f32"], cuda, case=f"mm k-split {dt} {m_}x{n_}x{k_}")[2]
+    want = run_oracle(mod, [a, b, np.zeros_like(c)], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+
+
+def test_matmul_k_split_in_a_graph(cuda):
+    """A K-split GEMM (zero-fill kernel, then atomic partial sums) captured in
+    a HIP graph and replayed three times with eager work between: every replay
+    matches the eager launch to a relative 1e-6 (the addition order varies)."""
+    import torch
+
+    rng = np.random.default_rng(15)
+    m_, n_, k_ = 1024, 1024, 4096
+    mod = K.matmul_f16(m_, n_, k_, 128, 128)
+    a = rng.normal(0, 1, (m_, k_)).astype(np.float16)
+    b = rng.normal(0, 1, (k_, n_)).astype(np.float16)
+    eager = run_gpu(mod, [a, b, np.zeros((m_, n_), np.float32)], ["f16", "f16", "f32"], cuda, case="mm k-split eager")[2]
+    print("[gpu] mm k-split graph capture", flush=True)
+    da, db = torch.from_numpy(a).to(cuda), torch.from_numpy(b).to(cuda)
+    dc = torch.zeros(m_, n_, dtype=torch.float32, device=cuda)
+    stream = torch.cuda.Stream(device=cuda)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        xt.launch(mod, da, db, dc, stream=stream)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            xt.launch(mod, da, db, dc, stream=stream)
+    torch.cuda.synchronize()
+    for r in range(3):
+        dc.fill_(float(r - 7))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert frob_rel(dc.cpu().numpy(), eager) <= 1e-6, r
+
+
 def test_reference_traced_matmul_program(cuda):
     """tests/golden/dsl/matmul_int8_epilogue.mlir is the text the reference's own
     tracer (xtile/dsl.py) wrote for the kernels/matmul.py program: parsed as-is

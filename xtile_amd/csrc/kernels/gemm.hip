@@ -45,6 +45,8 @@
 //     remapped so that each XCD receives a contiguous run of tiles, and tiles
 //     are ordered in groups of GROUP tile columns so that concurrently resident
 //     workgroups share A and B panels in their XCD's L2.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
@@ -87,6 +89,10 @@ struct GemmArgs {
   int nwg;
   int group;
   int has_scale, has_bias;
+  // K split (DMA kernel, f32 results without an epilogue): nwg = tiles *
+  // ksplit workgroups, K range r covering stages [r kstages, (r + 1)
+  // kstages) of 64 K bytes; ksplit = 1, tiles = nwg otherwise
+  int tiles, ksplit, kstages;
 };
 
 template <int ELEM>
@@ -121,11 +127,19 @@ struct TilePtrs {
   const float* Bias;
 };
 
-template <int ELEM, int BM, int BN>
-__device__ __forceinline__ TilePtrs gemm_tile_of(const GemmArgs& p) {
-  constexpr int ES = ELEM == kI8 ? 1 : 2;
+// The workgroup's linear id with contiguous runs per XCD: the K range is
+// gemm_lin / tiles, the tile gemm_lin % tiles.
+__device__ __forceinline__ int gemm_lin(const GemmArgs& p) {
   int L = blockIdx.x;
   if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
+  return L;
+}
+
+template <int ELEM, int BM, int BN, bool KS = false>
+__device__ __forceinline__ TilePtrs gemm_tile_of(const GemmArgs& p) {
+  constexpr int ES = ELEM == kI8 ? 1 : 2;
+  int L = gemm_lin(p);
+  if constexpr (KS) L -= (L / p.tiles) * p.tiles;
   const int subs = p.sub_m * p.sub_n;
   const int s = L % subs;
   int blk = L / subs;
@@ -452,8 +466,9 @@ __global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(Gem
 //     LDS round trip.  A stage's DMA has NS - 2 stages of compute to land.
 //     The barrier is a bare s_barrier: __syncthreads' release fence would
 //     also wait for the DMA that should stay in flight.
-template <int ELEM, int NS, bool OUT_I8, bool EPI, int NW>
+template <int ELEM, int NS, bool OUT_I8, bool EPI, int NW, bool KS = false>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
+  static_assert(!KS || (!EPI && !OUT_I8), "K split only without an epilogue");
   static_assert(NS >= 3 && NS <= 5, "stages");
   static_assert(NW == 4 || NW == 8, "waves");
   // NW = 4: 2 x 2 waves of 128 x 128; NW = 8: 2 x 4 waves of 128 x 64 (two
@@ -477,14 +492,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) unsigned char S4[NS > 4 ? STAGE : 16];
   unsigned char* const buf[5] = {S0, S1, S2, S3, S4};
 
-  const TilePtrs t = gemm_tile_of<ELEM, BM, BN>(p);
+  const TilePtrs t = gemm_tile_of<ELEM, BM, BN, KS>(p);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / (NW / 2), wn = wave % (NW / 2);
   const i32x4 ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
   const unsigned lda = (unsigned)(p.lda * ES), ldb = (unsigned)(p.ldb * ES);
-  const int nk = p.nk * 2;  // stages of 64 K bytes (>= 2)
+  // this workgroup's stages of 64 K bytes: [kbase, kbase + nk)
+  const int kbase = KS ? (gemm_lin(p) / p.tiles) * p.kstages : 0;
+  const int nk = KS ? min(p.kstages, p.nk * 2 - kbase) : p.nk * 2;
 
   // B row k keeps its 16-byte chunk c at c ^ bsw(k)
   auto bsw = [](int k) { return ES == 2 ? 4 * (k & 3) : 2 * (k & 7); };
@@ -506,8 +523,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   auto dma_one = [&](int kt, unsigned char* S, int q) {
     constexpr int H = PER / 2;
     const int i = wave * H + (q % H);
-    if (q < H) dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kt * KB);
-    else dma16(rb, lds_addr(S + AB + i * 1024), vb[i & 1], (unsigned)(kt * KR + RPI * i) * ldb);
+    const int kg = kt + kbase;
+    if (q < H) dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kg * KB);
+    else dma16(rb, lds_addr(S + AB + i * 1024), vb[i & 1], (unsigned)(kg * KR + RPI * i) * ldb);
   };
   auto dma = [&](int kt, unsigned char* S) {
 #pragma unroll
@@ -715,7 +733,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
         for (int v = 0; v < 16; ++v) {
           const long long off = t.c_off + (long long)(wm * WM + i * 32 + (v >> 2) * 8 + orow + (v & 3)) * p.ldc + n;
           const float x = (float)acc[i][j][v];
-          __builtin_nontemporal_store(EPI ? scale_bias(x, sv, bv, hs, hb) : x, static_cast<float*>(p.c) + off);
+          float* const o = static_cast<float*>(p.c) + off;
+          // K split (never with an epilogue): the ranges' partial sums meet
+          // in the zero-filled output, in an order that varies
+          if constexpr (KS) __hip_atomic_fetch_add(o, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else __builtin_nontemporal_store(EPI ? scale_bias(x, sv, bv, hs, hb) : x, o);
         }
     }
   }
@@ -775,6 +797,37 @@ Cover cover_dim(const xt::Plan& p, long long w, bool is_m) {
   return c;
 }
 
+// Zero-fills rows x (4 cols4) floats at pitch ld (a kernel, not
+// hipMemsetAsync, so that a captured graph replays it correctly).
+__global__ __launch_bounds__(256) void gemm_zero_kernel(float* __restrict__ c, long long ld, int rows, int cols4) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long r = i / cols4;
+  if (r >= rows) return;
+  const long long q = i - r * cols4;
+  __builtin_nontemporal_store(float4v{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<float4v*>(c + r * ld) + q);
+}
+
+// The C tiles of all Blocks form one [M][N] region at c0 with pitch ld:
+// along one grid axis the Blocks step A and C by TM rows (B fixed), along
+// the other B and C by TN columns (A fixed).
+bool c_region(const xt::Plan& p, long long& M, long long& N) {
+  if (p.grid[2] != 1) return false;
+  const long long TM = p.a.rows, TN = p.b.cols;
+  for (int am = 0; am < 2; ++am) {
+    const int an = 1 - am;
+    const bool m_ok = p.grid[am] == 1 || (axis_step(p.a.addr, am) == TM * p.a.ld &&
+                                          axis_step(p.c.addr, am) == TM * p.c.ld && axis_step(p.b.addr, am) == 0);
+    const bool n_ok = p.grid[an] == 1 || (axis_step(p.b.addr, an) == TN && axis_step(p.c.addr, an) == TN &&
+                                          axis_step(p.a.addr, an) == 0);
+    if (m_ok && n_ok) {
+      M = TM * p.grid[am];
+      N = TN * p.grid[an];
+      return true;
+    }
+  }
+  return false;
+}
+
 template <int ELEM, bool OUT_I8>
 void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
   const dim3 grid(a.nwg), block(256);
@@ -785,6 +838,8 @@ void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
       hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, true, true, NW>), grid, dblock, 0, s, a);
     else if (a.has_scale || a.has_bias)
       hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, true, NW>), grid, dblock, 0, s, a);
+    else if (a.ksplit > 1)
+      hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, NW, true>), grid, dblock, 0, s, a);
     else
       hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, NW>), grid, dblock, 0, s, a);
   } else if (bm == 128) hipLaunchKernelGGL((gemm_kernel<ELEM, 128, 128, OUT_I8>), grid, block, 0, s, a);
@@ -883,7 +938,38 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   }
   a.nwg = static_cast<int>(nwg);
   a.group = kTileGroup;
+  a.tiles = a.nwg;
+  a.ksplit = 1;
+  a.kstages = a.nk * 2;
   const bool out_i8 = p.c.elem == xt::Elem::I8;
+  // K split: when the 256 x 256 tiles fill at most an eighth of the CUs, f32
+  // results of f16 / bf16 products without an epilogue split K into ranges
+  // of at least 16 stages, one workgroup each, adding their partial sums
+  // atomically into the zero-filled output (the f32 addition order, and so
+  // the last bits, vary between runs; i8 sums stay exact and whole).
+  // Measured (f16, 30 launches): 1024 x 1024 x 4096 (16 tiles) 79.2 us whole,
+  // 42.8 in 8 ranges; 2048^3 (64 tiles) 47.3 whole, 71.4 in 4; 1024 x 8192 x
+  // 8192 (128 tiles) 155.9 whole, 164.4 in 2.
+  long long M = 0, N = 0;
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  float* const cbase = static_cast<float*>(bufs[p.c.arg]) + p.c.addr.c0;
+  if (bm == 256 && !i8 && !out_i8 && !p.gemm_scale && !p.gemm_bias && nwg * 8 <= cus && c_region(p, M, N) &&
+      N % 4 == 0 && p.c.ld % 4 == 0 && reinterpret_cast<uintptr_t>(cbase) % 16 == 0 && M < (1LL << 31)) {
+    const long long nk2 = a.nk * 2LL;
+    long long ks = std::min<long long>(cus / nwg, nk2 / 16);
+    if (ks > 1) {
+      a.kstages = (int)((nk2 + ks - 1) / ks);
+      ks = (nk2 + a.kstages - 1) / a.kstages;
+      a.ksplit = (int)ks;
+      a.nwg = (int)(nwg * ks);
+      const long long n4 = M * (N / 4);
+      hipLaunchKernelGGL(gemm_zero_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, cbase, p.c.ld,
+                         (int)M, (int)(N / 4));
+    }
+  }
   switch (p.a.elem) {
     case xt::Elem::I8: out_i8 ? launch_t<kI8, true>(bm, a, s) : launch_t<kI8, false>(bm, a, s); break;
     case xt::Elem::BF16: out_i8 ? launch_t<kBF16, true>(bm, a, s) : launch_t<kBF16, false>(bm, a, s); break;
