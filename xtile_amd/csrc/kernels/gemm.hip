@@ -17,10 +17,13 @@
 // and bias columns).  Blocks are independent (README.md:85-89), so both are
 // pure scheduling choices.
 //
-// Programs whose Blocks map onto 256 x 256 workgroup tiles run on
-// gemm_dma_kernel (operands landed in LDS by DMA; described where it is
-// defined), whatever the element type and result.  Smaller tiles run on
-// gemm_kernel, one template for BM x BN in {128 x 128, 64 x 64}:
+// Programs whose Blocks map onto 256 x 256, 256 x 128, 128 x 256 or 128 x 128
+// workgroup tiles run on gemm_dma_kernel (operands landed in LDS by DMA;
+// described where it is defined), whatever the element type and result:
+// 256 x 256 when its tiles fill the CUs (or are few enough to split K), else
+// the first smaller tile whose tiles fill them, else the one with the most
+// tiles (launch_gemm).  Blocks that map onto 64 x 64 tiles only run on
+// gemm_kernel, a template for BM x BN tiles (instantiated at 64 x 64):
 //   * 4 waves of (BM/2) x (BN/2), v_mfma_f32_32x32x16_{f16,bf16} or
 //     v_mfma_i32_32x32x32_i8.  Every fragment is 16 bytes per lane, so one
 //     K slice is 128 bytes of every row whatever the element type (64 f16/bf16
@@ -466,14 +469,16 @@ __global__ __launch_bounds__(256, BM * BN >= 65536 ? 1 : 2) void gemm_kernel(Gem
 //     LDS round trip.  A stage's DMA has NS - 2 stages of compute to land.
 //     The barrier is a bare s_barrier: __syncthreads' release fence would
 //     also wait for the DMA that should stay in flight.
-template <int ELEM, int NS, bool OUT_I8, bool EPI, int NW, bool KS = false>
-__global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
+template <int ELEM, int NS, bool OUT_I8, bool EPI, int NW, bool KS = false, int BMT = 256, int BNT = 256>
+__global__ __launch_bounds__(64 * NW, BMT * BNT <= 128 * 128 ? 2 : 1) void gemm_dma_kernel(GemmArgs p) {
   static_assert(!KS || (!EPI && !OUT_I8), "K split only without an epilogue");
   static_assert(NS >= 3 && NS <= 5, "stages");
   static_assert(NW == 4 || NW == 8, "waves");
-  // NW = 4: 2 x 2 waves of 128 x 128; NW = 8: 2 x 4 waves of 128 x 64 (two
-  // waves per SIMD)
-  constexpr int BM = 256, BN = 256, WM = 128, WN = 512 / NW, MI = 4, NI = WN / 32;
+  static_assert((BMT == 256 || BMT == 128) && (BNT == 256 || BNT == 128) && (NW == 4 || BMT * BNT == 65536),
+                "tiles");
+  // NW = 4: 2 x 2 waves of (BM / 2) x (BN / 2); NW = 8 (256 x 256 only): 2 x 4
+  // waves of 128 x 64 (two waves per SIMD)
+  constexpr int BM = BMT, BN = BNT, WM = BM / 2, WN = 2 * BN / NW, MI = WM / 32, NI = WN / 32;
   constexpr int ES = ELEM == kI8 ? 1 : 2;  // bytes per element
   constexpr int KB = 64;            // K bytes per A row and stage
   constexpr int AB = BM * KB;       // A bytes per stage
@@ -482,7 +487,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   constexpr int RPI = 1024 / BR;    // B k rows per DMA instruction
   constexpr int KSR = 32 / ES;      // B k rows per MFMA K step
   constexpr int STAGE = AB + KR * BR;
-  constexpr int PER = 32 / NW;      // DMA instructions per wave and stage
+  constexpr int PA = BM / 16 / NW;  // A DMA instructions (16 rows each) per wave and stage
+  constexpr int PB = KR * BR / 1024 / NW;  // B DMA instructions per wave and stage
+  constexpr int PER = PA + PB;      // DMA instructions per wave and stage
   typedef typename Acc<ELEM>::type acc_t;
   typedef __attribute__((address_space(3))) unsigned char lds_t;
   __shared__ __attribute__((aligned(1024))) unsigned char S0[STAGE];
@@ -497,14 +504,17 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / (NW / 2), wn = wave % (NW / 2);
+  static_assert(WM * 2 == BM && WN * (NW / 2) == BN, "wave layout");
   const i32x4 ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
   const unsigned lda = (unsigned)(p.lda * ES), ldb = (unsigned)(p.ldb * ES);
   // this workgroup's stages of 64 K bytes: [kbase, kbase + nk)
   const int kbase = KS ? (gemm_lin(p) / p.tiles) * p.kstages : 0;
   const int nk = KS ? min(p.kstages, p.nk * 2 - kbase) : p.nk * 2;
 
-  // B row k keeps its 16-byte chunk c at c ^ bsw(k)
-  auto bsw = [](int k) { return ES == 2 ? 4 * (k & 3) : 2 * (k & 7); };
+  // B row k keeps its 16-byte chunk c at c ^ bsw(k) (rows of 128-byte i8:
+  // (k / 2) % 4, so the eight rows a half-wave's tr_b8 read covers still
+  // fall in distinct 16-byte bank groups)
+  auto bsw = [](int k) { return ES == 2 ? 4 * (k & 3) : BR == 128 ? (k >> 1) & 3 : 2 * (k & 7); };
   // DMA lane offsets.  A instruction i (rows 16i .. 16i+15): lane L holds
   // row 16i + L/4 at position L%4, i.e. chunk (L%4) ^ ((L/16) & 3).  B
   // instruction i (k rows RPI i .. + RPI - 1, CPR chunks each): lane
@@ -518,14 +528,17 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) vb[q] = (unsigned)h * ldb + (unsigned)((pc ^ bsw(RPI * q + h)) << 4);
   }
-  // this wave's share of stage kt: A instructions PER/2 w .. + PER/2 - 1
-  // (q < PER/2), B the same (q >= PER/2)
+  // this wave's share of stage kt: A instructions PA w .. + PA - 1 (q < PA),
+  // B instructions PB w .. + PB - 1 (q >= PA)
   auto dma_one = [&](int kt, unsigned char* S, int q) {
-    constexpr int H = PER / 2;
-    const int i = wave * H + (q % H);
     const int kg = kt + kbase;
-    if (q < H) dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kg * KB);
-    else dma16(rb, lds_addr(S + AB + i * 1024), vb[i & 1], (unsigned)(kg * KR + RPI * i) * ldb);
+    if (q < PA) {
+      const int i = wave * PA + q;
+      dma16(ra, lds_addr(S + i * 1024), va, (unsigned)(16 * i) * lda + (unsigned)kg * KB);
+    } else {
+      const int i = wave * PB + (q - PA);
+      dma16(rb, lds_addr(S + AB + i * 1024), vb[i & 1], (unsigned)(kg * KR + RPI * i) * ldb);
+    }
   };
   auto dma = [&](int kt, unsigned char* S) {
 #pragma unroll
@@ -606,19 +619,53 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   // second.  Either way the first MFMAs of a step need only the earliest
   // reads.
   auto mma_n = [&](int set, int n) {
-    if constexpr (NW == 4) {
+    if constexpr (NW == 4 && MI == 4 && NI == 4) {
       const int k = n < 1 ? 0 : n < 4 ? 1 : n < 9 ? 2 : 3, r = n - k * k;
       if (r < k) mma(set, r, k);
       else mma(set, k, r - k);
+    } else if constexpr (NW == 4) {
+      // the same shells over an MI x NI grid (MI, NI in {2, 4})
+      int c = 0, mi = 0, mj = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int r = 0; r < k; ++r)
+          if (r < MI && k < NI) {
+            if (c == n) mi = r, mj = k;
+            ++c;
+          }
+#pragma unroll
+        for (int r = 0; r <= k; ++r)
+          if (k < MI && r < NI) {
+            if (c == n) mi = k, mj = r;
+            ++c;
+          }
+      }
+      mma(set, mi, mj);
     } else {
       mma(set, 2 * (n >> 2) + (n & 1), (n >> 1) & 1);
     }
   };
   // the fragment reads of slot g (of MI * NI / 4 slots) of a K step
   auto slot_reads = [&](const unsigned char* S, int ks, int set, int g) {
-    if constexpr (NW == 4) {
+    if constexpr (NW == 4 && MI == 4 && NI == 4) {
       read_a(S, ks, set, g);
       read_b(S, ks, set, g);
+    } else if constexpr (NW == 4) {
+      // slot 0: A0 B0 A1 B1 (the first four MFMAs' shells); slot 1 of a
+      // 4 x 2 or 2 x 4 grid: the rest (A2 A3 or B2 B3)
+      if (g == 0) {
+        read_a(S, ks, set, 0);
+        read_b(S, ks, set, 0);
+        read_a(S, ks, set, 1);
+        read_b(S, ks, set, 1);
+      } else if constexpr (MI == 4) {
+        read_a(S, ks, set, 2);
+        read_a(S, ks, set, 3);
+      } else {
+        read_b(S, ks, set, 2);
+        read_b(S, ks, set, 3);
+      }
     } else if (g == 0) {
       read_a(S, ks, set, 0);
       read_b(S, ks, set, 0);
@@ -653,7 +700,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
   // instruction per wave ahead of the MFMAs; issued as a burst after the
   // barrier, it held every wave's issue (C3: ~330 cycles a stage).
   constexpr int SLOTS = MI * NI / 2, HALF = SLOTS / 2;
-  static_assert(SLOTS == PER, "one DMA instruction per slot");
+  // one DMA instruction per slot, two in the first slots of a tile smaller
+  // than 256 x 256 (6 for 4 slots, 4 for 2)
+  static_assert(PER >= SLOTS && PER <= 2 * SLOTS, "DMA instructions per slot");
   auto stage = [&](int s, unsigned char* S, const unsigned char* Snext, unsigned char* Sfree) {
     const bool more = s + NS - 1 < nk;
 #pragma unroll
@@ -662,7 +711,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_dma_kernel(GemmArgs p) {
       __builtin_amdgcn_sched_barrier(0);
       mma_n(set, n0);
       __builtin_amdgcn_sched_barrier(0);
-      if (more) dma_one(s + NS - 1, Sfree, g);
+      if (more) {
+        dma_one(s + NS - 1, Sfree, g);
+        if (g + SLOTS < PER) dma_one(s + NS - 1, Sfree, g + SLOTS);
+      }
       __builtin_amdgcn_sched_barrier(0);
       mma_n(set, n0 + 1);
       __builtin_amdgcn_sched_barrier(0);
@@ -828,10 +880,22 @@ bool c_region(const xt::Plan& p, long long& M, long long& N) {
   return false;
 }
 
-template <int ELEM, bool OUT_I8>
-void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
+// The DMA kernel at a tile smaller than 256 x 256 (four waves).
+template <int ELEM, bool OUT_I8, int BMT, int BNT>
+void launch_small_t(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(a.nwg), block(256);
-  if (bm == 256) {
+  if constexpr (OUT_I8)
+    hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, true, true, 4, false, BMT, BNT>), grid, block, 0, s, a);
+  else if (a.has_scale || a.has_bias)
+    hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, true, 4, false, BMT, BNT>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, 4, false, BMT, BNT>), grid, block, 0, s, a);
+}
+
+template <int ELEM, bool OUT_I8>
+void launch_t(int bm, int bn, const GemmArgs& a, hipStream_t s) {
+  const dim3 grid(a.nwg), block(256);
+  if (bm == 256 && bn == 256) {
     constexpr int NW = dma_waves<ELEM>();
     const dim3 dblock(64 * NW);
     if constexpr (OUT_I8)
@@ -842,8 +906,15 @@ void launch_t(int bm, const GemmArgs& a, hipStream_t s) {
       hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, NW, true>), grid, dblock, 0, s, a);
     else
       hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, NW>), grid, dblock, 0, s, a);
-  } else if (bm == 128) hipLaunchKernelGGL((gemm_kernel<ELEM, 128, 128, OUT_I8>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((gemm_kernel<ELEM, 64, 64, OUT_I8>), grid, block, 0, s, a);
+  } else if (bm == 256) {
+    launch_small_t<ELEM, OUT_I8, 256, 128>(a, s);
+  } else if (bm == 128 && bn == 256) {
+    launch_small_t<ELEM, OUT_I8, 128, 256>(a, s);
+  } else if (bm == 128) {
+    launch_small_t<ELEM, OUT_I8, 128, 128>(a, s);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<ELEM, 64, 64, OUT_I8>), grid, block, 0, s, a);
+  }
 }
 
 }  // namespace
@@ -902,21 +973,63 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
       return hipErrorInvalidValue;
     }
   }
-  // Largest square workgroup tile the Blocks can be split or fused into.
-  int bm = 0;
-  Cover cm, cn;
-  for (int w : {256, 128, 64}) {
-    cm = cover_dim(p, w, true);
-    cn = cover_dim(p, w, false);
-    if (cm.ok && cn.ok && !(cm.axis >= 0 && cm.axis == cn.axis)) {
-      bm = w;
-      break;
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  const bool out_i8 = p.c.elem == xt::Elem::I8;
+  long long M = 0, N = 0;
+  float* const cbase = static_cast<float*>(bufs[p.c.arg]) + p.c.addr.c0;
+  const bool can_split = !i8 && !out_i8 && !p.gemm_scale && !p.gemm_bias && c_region(p, M, N) && N % 4 == 0 &&
+                         p.c.ld % 4 == 0 && reinterpret_cast<uintptr_t>(cbase) % 16 == 0 && M < (1LL << 31);
+  // Workgroup tile, all on the DMA kernel: 256 x 256 when the Blocks map onto
+  // it and its tiles fill the CUs, or are few enough for the K split below;
+  // else the first of 256 x 128, 128 x 256, 128 x 128 whose tiles fill the
+  // CUs, else the one with the most tiles (a 2048^3 f16 GEMM: 64 tiles of
+  // 256 x 256, 256 of 128 x 128); 64 x 64 (register-staged) when none maps.
+  struct Cand {
+    int bm = 0, bn = 0;
+    Cover cm, cn;
+    long long tiles = 0;
+  };
+  auto try_tile = [&](int bmv, int bnv, Cand& c) {
+    c.bm = bmv;
+    c.bn = bnv;
+    c.cm = cover_dim(p, bmv, true);
+    c.cn = cover_dim(p, bnv, false);
+    if (!c.cm.ok || !c.cn.ok || (c.cm.axis >= 0 && c.cm.axis == c.cn.axis)) return false;
+    long long g[3] = {p.grid[0], p.grid[1], p.grid[2]};
+    if (c.cm.axis >= 0) g[c.cm.axis] /= c.cm.factor;
+    if (c.cn.axis >= 0) g[c.cn.axis] /= c.cn.factor;
+    c.tiles = g[0] * g[1] * g[2] * c.cm.sub * c.cn.sub;
+    return true;
+  };
+  Cand pick, c256;
+  const bool has256 = try_tile(256, 256, c256);
+  if (has256 && (c256.tiles >= cus || (can_split && c256.tiles * 8 <= cus))) {
+    pick = c256;
+  } else {
+    Cand most = has256 ? c256 : Cand{};
+    bool found = false;
+    const int shapes[3][2] = {{256, 128}, {128, 256}, {128, 128}};
+    for (const auto& sh : shapes) {
+      Cand c;
+      if (!try_tile(sh[0], sh[1], c)) continue;
+      if (c.tiles >= cus) {
+        pick = c;
+        found = true;
+        break;
+      }
+      if (c.tiles > most.tiles) most = c;
+    }
+    if (!found) pick = most;
+    if (pick.bm == 0 && try_tile(64, 64, pick) == false) {
+      why = "matmul Blocks cannot be mapped onto 64x64 workgroup tiles";
+      return hipErrorInvalidValue;
     }
   }
-  if (bm == 0) {
-    why = "matmul Blocks cannot be mapped onto 64x64 workgroup tiles";
-    return hipErrorInvalidValue;
-  }
+  const int bm = pick.bm, bn = pick.bn;
+  const Cover cm = pick.cm, cn = pick.cn;
   a.mul[0] = a.mul[1] = a.mul[2] = 1;
   int vg[3] = {p.grid[0], p.grid[1], p.grid[2]};
   if (cm.axis >= 0) {
@@ -941,7 +1054,6 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   a.tiles = a.nwg;
   a.ksplit = 1;
   a.kstages = a.nk * 2;
-  const bool out_i8 = p.c.elem == xt::Elem::I8;
   // K split: when the 256 x 256 tiles fill at most an eighth of the CUs, f32
   // results of f16 / bf16 products without an epilogue split K into ranges
   // of at least 16 stages, one workgroup each, adding their partial sums
@@ -950,14 +1062,7 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   // Measured (f16, 30 launches): 1024 x 1024 x 4096 (16 tiles) 79.2 us whole,
   // 42.8 in 8 ranges; 2048^3 (64 tiles) 47.3 whole, 71.4 in 4; 1024 x 8192 x
   // 8192 (128 tiles) 155.9 whole, 164.4 in 2.
-  long long M = 0, N = 0;
-  int cus = 256, dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-    cus = 256;
-  float* const cbase = static_cast<float*>(bufs[p.c.arg]) + p.c.addr.c0;
-  if (bm == 256 && !i8 && !out_i8 && !p.gemm_scale && !p.gemm_bias && nwg * 8 <= cus && c_region(p, M, N) &&
-      N % 4 == 0 && p.c.ld % 4 == 0 && reinterpret_cast<uintptr_t>(cbase) % 16 == 0 && M < (1LL << 31)) {
+  if (bm == 256 && bn == 256 && can_split && nwg * 8 <= cus) {
     const long long nk2 = a.nk * 2LL;
     long long ks = std::min<long long>(cus / nwg, nk2 / 16);
     if (ks > 1) {
@@ -971,9 +1076,11 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
     }
   }
   switch (p.a.elem) {
-    case xt::Elem::I8: out_i8 ? launch_t<kI8, true>(bm, a, s) : launch_t<kI8, false>(bm, a, s); break;
-    case xt::Elem::BF16: out_i8 ? launch_t<kBF16, true>(bm, a, s) : launch_t<kBF16, false>(bm, a, s); break;
-    default: out_i8 ? launch_t<kF16, true>(bm, a, s) : launch_t<kF16, false>(bm, a, s); break;
+    case xt::Elem::I8: out_i8 ? launch_t<kI8, true>(bm, bn, a, s) : launch_t<kI8, false>(bm, bn, a, s); break;
+    case xt::Elem::BF16:
+      out_i8 ? launch_t<kBF16, true>(bm, bn, a, s) : launch_t<kBF16, false>(bm, bn, a, s);
+      break;
+    default: out_i8 ? launch_t<kF16, true>(bm, bn, a, s) : launch_t<kF16, false>(bm, bn, a, s); break;
   }
   return hipGetLastError();
 }
