@@ -592,13 +592,13 @@ def test_matmul_epilogue_variants(cuda, dt, scale, bias, ftoi):
 
 @pytest.mark.parametrize(
     "dt,m_,n_,k_",
-    [("f16", 1024, 1024, 4096),   # 16 tiles of 256 x 256: K in 8 ranges of 16 stages
-     ("bf16", 1024, 2048, 2048),  # 32 tiles: 4 ranges
-     ("f16", 512, 768, 1536)],    # 6 tiles: K 1536 = 48 stages, 3 ranges
+    [("f16", 1024, 1024, 4096),   # 64 tiles of 128 x 128: K in 4 ranges of 32 stages
+     ("bf16", 1024, 2048, 2048),  # 128 tiles: 2 ranges
+     ("f16", 512, 768, 1536)],    # 24 tiles: K 1536 = 48 stages, 3 ranges
 )
 def test_matmul_k_split(cuda, dt, m_, n_, k_):
-    """f32 GEMMs without an epilogue whose 256 x 256 tiles fill at most an
-    eighth of the CUs split K; the partial sums are added atomically into the
+    """f32 GEMMs without an epilogue whose 256 x 256 tiles would fill at most
+    an eighth of the CUs run 128 x 128 tiles and split K; the partial sums are added atomically into the
     zero-filled output (the output starts non-zero here, so the fill is
     checked too)."""
     rng = np.random.default_rng(14)

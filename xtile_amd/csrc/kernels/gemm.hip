@@ -888,6 +888,8 @@ void launch_small_t(const GemmArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, true, true, 4, false, BMT, BNT>), grid, block, 0, s, a);
   else if (a.has_scale || a.has_bias)
     hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, true, 4, false, BMT, BNT>), grid, block, 0, s, a);
+  else if (BMT == 128 && BNT == 128 && a.ksplit > 1)
+    hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, 4, true, 128, 128>), grid, block, 0, s, a);
   else
     hipLaunchKernelGGL((gemm_dma_kernel<ELEM, kDmaStages, false, false, 4, false, BMT, BNT>), grid, block, 0, s, a);
 }
@@ -1004,9 +1006,15 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
     c.tiles = g[0] * g[1] * g[2] * c.cm.sub * c.cn.sub;
     return true;
   };
-  Cand pick, c256;
+  Cand pick, c256, c128;
   const bool has256 = try_tile(256, 256, c256);
-  if (has256 && (c256.tiles >= cus || (can_split && c256.tiles * 8 <= cus))) {
+  // A GEMM of at most CUs / 8 tiles of 256 x 256 that can split K takes 128
+  // x 128 tiles with the split (1024 x 1024 x 4096 f16: 42.3 us on 16 tiles
+  // of 256 x 256 in 8 K ranges, 28.2 on 64 of 128 x 128 in 4; hipBLASLt 25.1)
+  const bool tiny = can_split && has256 && c256.tiles * 8 <= cus;
+  if (tiny && try_tile(128, 128, c128)) {
+    pick = c128;
+  } else if (has256 && (c256.tiles >= cus || tiny)) {
     pick = c256;
   } else {
     Cand most = has256 ? c256 : Cand{};
@@ -1062,7 +1070,7 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   // Measured (f16, 30 launches): 1024 x 1024 x 4096 (16 tiles) 79.2 us whole,
   // 42.8 in 8 ranges; 2048^3 (64 tiles) 47.3 whole, 71.4 in 4; 1024 x 8192 x
   // 8192 (128 tiles) 155.9 whole, 164.4 in 2.
-  if (bm == 256 && bn == 256 && can_split && nwg * 8 <= cus) {
+  if (can_split && ((bm == 256 && bn == 256 && nwg * 8 <= cus) || (tiny && bm == 128 && bn == 128 && nwg * 2 <= cus))) {
     const long long nk2 = a.nk * 2LL;
     long long ks = std::min<long long>(cus / nwg, nk2 / 16);
     if (ks > 1) {
