@@ -612,6 +612,42 @@ def test_matmul_k_split(cuda, dt, m_, n_, k_):
     assert frob_rel(got, want) <= MM_FROB
 
 
+@pytest.mark.parametrize(
+    "dt,m_,n_,k_,scale,bias,ftoi",
+    [("f16", 4096, 2176, 256, False, False, False),   # 16 x 17 = 272 tiles of 256 x 128
+     ("bf16", 4096, 2176, 384, True, True, False),
+     ("i8", 4096, 2176, 512, True, True, True),        # i8 B rows of 128 bytes
+     ("f16", 2176, 4096, 256, False, True, False),    # 17 x 16 = 272 tiles of 128 x 256
+     ("i8", 2176, 4096, 256, False, False, False),
+     ("i8", 640, 1152, 512, True, False, True)],      # 5 x 9 = 45 tiles of 128 x 128
+)
+def test_matmul_rectangular_dma_tiles(cuda, dt, m_, n_, k_, scale, bias, ftoi):
+    """GEMMs whose Blocks do not map onto 256 x 256 tiles (M or N an odd
+    multiple of 128) run the DMA kernel at 256 x 128, 128 x 256 or 128 x 128,
+    with every epilogue form and i8 results."""
+    rng = np.random.default_rng(16)
+    dt_in = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}[dt]
+    mod = _matmul_epilogue_program(m_, n_, k_, dt_in, scale, bias, ftoi)
+    if dt == "i8":
+        a, b, s, bi = _i8_inputs(rng, m_, n_, k_)
+    else:
+        a = rng.normal(0, 1, (m_, k_)).astype(np.float32)
+        b = rng.normal(0, 1, (k_, n_)).astype(np.float32)
+        a, b = (f32_to_bf16_bits(a), f32_to_bf16_bits(b)) if dt == "bf16" else (a.astype(np.float16), b.astype(np.float16))
+        s = rng.uniform(0.05, 0.2, (1, n_)).astype(np.float32)
+        bi = rng.uniform(-3, 3, (1, n_)).astype(np.float32)
+    c = np.zeros((m_, n_), np.int8 if ftoi else np.float32)
+    dts = [dt, dt, "i8" if ftoi else "f32", "f32", "f32"]
+    got = run_gpu(mod, [a, b, c, s, bi], dts, cuda, case=f"mm rect {dt} {m_}x{n_}x{k_} s={scale} b={bias} ftoi={ftoi}")[2]
+    want = run_oracle(mod, [a, b, c, s, bi], oracle_threads())[2]
+    if dt == "i8":
+        assert np.array_equal(got, want)
+    elif ftoi:
+        assert np.mean(got != want) < 1e-3 and np.max(np.abs(got.astype(int) - want.astype(int))) <= 1
+    else:
+        assert frob_rel(got, want) <= MM_FROB
+
+
 def test_matmul_k_split_in_a_graph(cuda):
     """A K-split GEMM (zero-fill kernel, then atomic partial sums) captured in
     a HIP graph and replayed three times with eager work between: every replay
