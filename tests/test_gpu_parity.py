@@ -256,6 +256,11 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
         (2, 14, 14, 256, 128, 3, 3, 4, 12, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),   # no padding: 12 x 12 outputs
         (2, 12, 12, 256, 64, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),    # Cout 64: 256 x 64 tiles
         (2, 10, 10, 160, 192, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),  # Cout 192: three 64-channel tiles
+        (2, 12, 12, 256, 32, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),    # Cout 32: half a 64-channel tile
+        (2, 14, 14, 48, 64, 3, 3, 7, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),     # Cin 48: taps padded to 64 channels
+        (2, 16, 16, 16, 40, 3, 3, 4, 8, (1, 1, 1, 1), (2, 2), (1, 1), "bf16"),     # Cin 16, Cout 40, stride 2
+        (3, 9, 9, 1024, 48, 1, 1, 3, 9, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),      # 1 x 1, Cout 48
+        (1, 11, 13, 24, 200, 5, 5, 11, 13, (2, 2, 2, 2), (1, 1), (1, 1), "bf16"),  # Cin 24, Cout 200 (4 tiles, last 8 wide)
     ],
 )
 def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
@@ -327,6 +332,8 @@ def test_conv2d_igemm_k_split_in_a_graph(cuda):
         (2, 8, 8, 320, 64, 3, 3, 8, 8, (1, 1, 1, 1), (1, 1), "0"),      # Cin 320: 256 x 64 tiles, 5 stages a tap
         (2, 13, 11, 128, 192, 3, 3, 7, 6, (1, 1, 1, 1), (2, 2), "0"),   # Cout 192: band declines (> 128)
         (1, 32, 64, 128, 64, 3, 3, 32, 64, (1, 1, 1, 1), (1, 1), "1"),  # kernels/conv2d.py, implicit GEMM first
+        (2, 10, 10, 48, 80, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), "0"),    # Cin 48 padded to 64, Cout 80 (two tiles)
+        (2, 12, 12, 272, 16, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), "0"),   # Cin 272 = 4 stages + 16, Cout 16
     ],
 )
 def test_conv2d_igemm_i8_bit_exact(cuda, monkeypatch, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, first):

@@ -34,8 +34,8 @@
 //
 // Kernel choice (launch_conv2d): the band kernel below when the Blocks tile
 // the whole output and filter + halo fit in LDS; else, for the same tiling
-// with Cout % 64 == 0 and Cin * esize % 64 == 0, the implicit GEMM with DMA
-// operands (conv_igemm.hip); else the persistent kernel above for f16 / bf16
+// with Cin * esize and Cout * esize multiples of 16, the implicit GEMM with
+// DMA operands (conv_igemm.hip); else the persistent kernel above for f16 / bf16
 // with Cin % 32 == 0, Cout % 16 == 0 (<= 128), one image per Block, every
 // output channel and an f32 result; else the generic kernel
 // (conv_general.hip), which takes every tile shape the planner accepts.

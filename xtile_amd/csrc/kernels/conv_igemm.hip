@@ -8,7 +8,8 @@
 //                                         ow*sw - pad_l + kw*dw, c] * f[kh, kw, c, o]
 // with source elements outside the image read as zero.  Used when the Blocks
 // tile the whole output (one image per Block, every output channel, one
-// filter), so the launch is one GEMM:
+// filter) and Cin * esize, Cout * esize are multiples of 16, so the launch is
+// one GEMM:
 //   M = N*OH*OW output pixels (NHWC order: the output is C[M][CO]),
 //   N = CO, K = KH*KW*Cin in the filter's (kh, kw, c) order (B = f as
 //   [K][CO], row-major HWIO).
@@ -22,7 +23,9 @@
 //     exact i32 sums rounded to f32 once); 64 or 80 KB of LDS, so two
 //     workgroups share a CU and one's barrier waits are the other's MFMA time.
 //   * A K stage is 64 bytes of one tap's channels in every pixel row (32
-//     f16 / bf16 or 64 i8 channels):
+//     f16 / bf16 or 64 i8 channels; a tap's last stage is padded with zeros
+//     when Cin is not a multiple of that, and a channel tile past Cout reads
+//     zeros and is not stored):
 //     A [BM rows][64 B] is an im2col gather done by the DMA itself: lane L of
 //     A instruction i fetches 16 bytes of pixel row 16 i + L/4 at the tap's
 //     source position, or, outside the image (padding) or past M, an offset
@@ -164,6 +167,9 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // of the stage's 64 bytes, which lands at LDS chunk lane % 4 of its row.
   int ih0[PA], iw0[PA];
   unsigned abase[PA];
+  // channel of the lane's 16 bytes within a stage (a stage past the last
+  // channel reads zeros: channels are padded to whole stages per tap)
+  const int ach = ((lane & 3) ^ ((lane >> 4) & 3)) * (16 / ES);
   {
     const unsigned gc = (unsigned)((lane & 3) ^ ((lane >> 4) & 3));
 #pragma unroll
@@ -191,6 +197,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // (lane % CPR) ^ ig_bsw(k), and ig_bsw(k) depends on lane / CPR only.
   const unsigned vb = (unsigned)(lane / CPR) * ldb + (unsigned)(n0 * ES) +
                       (unsigned)(((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4);
+  // the lane's filter row within a DMA instruction, and whether its 16 bytes
+  // lie within Cout (a tile past Cout reads zeros)
+  const int brow = lane / CPR;
+  const bool bcol = n0 * ES + (((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4) < p.CO * ES;
 
   // tap state of the next stage to load
   // this workgroup's stages [s_begin, s_begin + ns)
@@ -207,13 +217,19 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   };
   // DMA instruction q of the stage being loaded (A for q < PA, then B)
   auto dma_one = [&](unsigned char* S, int q) {
+    const int c0 = lcc * KR;  // the stage's first channel
     if (q < PA) {
       const int i = PA * wave + q;
-      const bool in = (unsigned)(ih0[q] + dih) < (unsigned)p.H && (unsigned)(iw0[q] + diw) < (unsigned)p.W;
+      const bool in = (unsigned)(ih0[q] + dih) < (unsigned)p.H && (unsigned)(iw0[q] + diw) < (unsigned)p.W &&
+                      c0 + ach < p.C;
       dma16(ra, lds_addr(S + i * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
     } else {
+      // filter rows tap * C + c0 + RPI i + brow (rows past the tap's
+      // channels, or columns past Cout, read zeros)
       const int i = PB * wave + (q - PA);
-      dma16(rb, lds_addr(S + AB + i * 1024), vb, (unsigned)(lkt * KR + RPI * i) * ldb);
+      const bool in = bcol && c0 + RPI * i + brow < p.C;
+      dma16(rb, lds_addr(S + AB + i * 1024), in ? vb : kIgOutOfRange,
+            (unsigned)((lkh * p.KW + lkw) * p.C + c0 + RPI * i) * ldb);
     }
   };
   // after a stage's DMA: the next 32 channels, then the next tap
@@ -336,7 +352,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
         // through a scalar (a bit-cast of an ext_vector element lvalue reads
         // element 0); an i8 sum is an exact i32, rounded to f32 once
         const float x = static_cast<float>(acc[i][j][v]);
-        if (row >= p.M) continue;
+        if (row >= p.M || col >= p.CO) continue;
         float* const o = p.out + (long long)row * p.CO + col;
         // K split: the ranges' partial sums meet in the zero-filled output
         // (f16 / bf16 only; the order of the additions varies)
@@ -360,8 +376,10 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   const bool i8 = c.elem == xt::Elem::I8;
   if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16 && !i8) return false;
   const long long es = i8 ? 1 : 2;
-  // a K stage is 64 bytes of one tap's channels
-  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || (c.C * es) % 64 || c.CO % 64) return false;
+  // a K stage is 64 bytes of one tap's channels (the last stage of a tap
+  // padded with zeros), read in 16-byte pieces: Cin * esize and Cout * esize
+  // multiples of 16
+  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || (c.C * es) % 16 || (c.CO * es) % 16) return false;
   if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
       c.ch.axis == c.cw.axis)
     return false;
@@ -408,12 +426,12 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.dh = (int)c.dil_h;
   a.dw = (int)c.dil_w;
   a.M = (int)M;
-  a.stages = (int)(K * es / 64);
-  a.cs = (int)(c.C * es / 64);
+  a.cs = (int)((c.C * es + 63) / 64);
+  a.stages = (int)(c.KH * c.KW) * a.cs;
   // 128 x 128 tiles when Cout allows, else 256 x 64
   const bool wide = c.CO % 128 == 0;
   const int bm = wide ? 128 : 256, bn = wide ? 128 : 64;
-  a.ntiles = (int)(c.CO / bn);
+  a.ntiles = (int)((c.CO + bn - 1) / bn);
   const long long tiles = (M + bm - 1) / bm * a.ntiles;
   // K split when the tiles fill at most half the CUs (f16 / bf16: i8 sums stay
   // exact and whole): up to one workgroup a CU, at least 16 stages each.
