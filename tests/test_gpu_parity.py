@@ -508,6 +508,26 @@ def test_conv2d_batch_tile_channel_subset_and_bf16_result(cuda, et, rt):
         assert frob_rel(got, want) <= MM_FROB
 
 
+@pytest.mark.parametrize("et", ["i8", "bf16"])
+def test_conv2d_batch_tiles_covering_the_output(cuda, et):
+    """Blocks of 2 images x the whole image x every output channel cover the
+    output: the implicit-GEMM kernel takes them (the band kernel wants one
+    image per Block)."""
+    rng = np.random.default_rng(17)
+    src, filt = (4, 12, 16, 32), (3, 3, 32, 64)
+    res, out = (2, 12, 16, 64), (4, 12, 16, 64)
+    mod = xt.parse(_conv_text(src, filt, out, res, (2, 1, 1), "%bid#0, %c0, %c0, %c0", "%bid#0, %c0, %c0, %c0",
+                              (1, 1, 1, 1), (1, 1), (1, 1), et, "f32"))
+    x, f = _conv_inputs(rng, et, 4, 12, 16, 32, 64, 3, 3)
+    o = np.zeros(out, np.float32)
+    got = run_gpu(mod, [x, f, o], [et, et, "f32"], cuda, case=f"conv batch tiles of 2 {et}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    if et == "i8":
+        assert np.array_equal(got, want)
+    else:
+        assert frob_rel(got, want) <= MM_FROB
+
+
 # -- matmul epilogue and i8 (kernels/matmul.py) ---------------------------------
 
 

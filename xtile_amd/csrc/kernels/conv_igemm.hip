@@ -7,7 +7,7 @@
 //   out[n, oh, ow, o] = sum_{kh,kw,c} src[n, oh*sh - pad_t + kh*dh,
 //                                         ow*sw - pad_l + kw*dw, c] * f[kh, kw, c, o]
 // with source elements outside the image read as zero.  Used when the Blocks
-// tile the whole output (one image per Block, every output channel, one
+// tile the whole output (TB images per Block, every output channel, one
 // filter) and Cin * esize, Cout * esize are multiples of 16, so the launch is
 // one GEMM:
 //   M = N*OH*OW output pixels (NHWC order: the output is C[M][CO]),
@@ -379,7 +379,7 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   // a K stage is 64 bytes of one tap's channels (the last stage of a tap
   // padded with zeros), read in 16-byte pieces: Cin * esize and Cout * esize
   // multiples of 16
-  if (c.out_elem != xt::Elem::F32 || c.TB != 1 || c.TC != c.CO || (c.C * es) % 16 || (c.CO * es) % 16) return false;
+  if (c.out_elem != xt::Elem::F32 || c.TC != c.CO || (c.C * es) % 16 || (c.CO * es) % 16) return false;
   if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
       c.ch.axis == c.cw.axis)
     return false;
@@ -388,17 +388,18 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   const long long gB = p.grid[c.cb.axis], gH = p.grid[c.ch.axis], gW = p.grid[c.cw.axis];
   if (gH * c.TH != c.out_H || gW * c.TW != c.out_W || c.out_C != c.CO) return false;
   auto step = [&](const xt::TileAddr& t, int axis) { return axis == 0 ? t.sx : axis == 1 ? t.sy : t.sz; };
+  // a Block holds TB images: the Blocks cover images [0, gB TB)
   const long long plane = c.out_H * c.out_W * c.out_C;
-  if (c.out_addr.c0 != 0 || (gB > 1 && step(c.out_addr, c.cb.axis) != plane) ||
+  if (c.out_addr.c0 != 0 || (gB > 1 && step(c.out_addr, c.cb.axis) != c.TB * plane) ||
       (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
   if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || (c.filt_addr.c0 * es) % 16) return false;
   // the source batch entries the Blocks read: images [0, gB) of an NHWC tensor
-  const long long src_bytes = gB * c.H * c.W * c.C * es;
+  const long long src_bytes = gB * c.TB * c.H * c.W * c.C * es;
   const long long K = c.KH * c.KW * c.C;
   const long long filt_bytes = K * c.CO * es;
-  const long long M = gB * c.out_H * c.out_W;
+  const long long M = gB * c.TB * c.out_H * c.out_W;
   if (src_bytes >= (1LL << 31) || filt_bytes >= (1LL << 31) || M >= (1LL << 31) || c.out_H * c.out_W >= (1LL << 31))
     return false;
   const unsigned char* src = static_cast<const unsigned char*>(bufs[c.src_arg]);
