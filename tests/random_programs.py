@@ -282,6 +282,107 @@ def conv_case(seed: int):
     raise RuntimeError("no plannable conv drawn")
 
 
+def wide_conv_case(seed: int):
+    """Random `load_conv2d` programs in the implicit-GEMM kernel's range: Blocks
+    tiling the whole output, Cin and Cout multiples of 8 (16 for i8) up to 320
+    and 256, 1x1 to 5x5 filters, strides, dilations and asymmetric pads.
+    Returns (module, host inputs, dtypes, description)."""
+    import xtile_amd as xt
+    from xtile_amd import kernels as K
+
+    rng = np.random.default_rng(25_000 + seed)
+    dts = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}
+    for _ in range(200):
+        dt = str(rng.choice(list(dts)))
+        q = 16 if dt == "i8" else 8
+        n = int(rng.integers(1, 3))
+        kh, kw = int(rng.choice([1, 3, 5])), int(rng.choice([1, 3, 5]))
+        sh, sw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        dh, dw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        pad = tuple(int(rng.integers(0, k // 2 + 1)) for k in (kh, kw, kh, kw))
+        h, w = int(rng.integers(5, 17)), int(rng.integers(5, 17))
+        cin = q * int(rng.integers(1, 320 // q + 1))
+        cout = q * int(rng.integers(1, 256 // q + 1))
+        oh = (h + pad[0] + pad[2] - dh * (kh - 1) - 1) // sh + 1
+        ow = (w + pad[1] + pad[3] - dw * (kw - 1) - 1) // sw + 1
+        if oh < 1 or ow < 1:
+            continue
+        th = int(rng.choice([d for d in range(1, oh + 1) if oh % d == 0]))
+        tw = int(rng.choice([d for d in range(1, ow + 1) if ow % d == 0]))
+        try:
+            mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=dts[dt], pad=pad, stride=(sh, sw),
+                           dilation=(dh, dw))
+            xt.plan(mod)
+        except (ValueError, NotImplementedError):
+            continue
+        if dt == "i8":
+            x = rng.integers(-128, 128, (n, h, w, cin), dtype=np.int8)
+            f = rng.integers(-128, 128, (kh, kw, cin, cout), dtype=np.int8)
+        else:
+            x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+            f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+            x, f = (f32_to_bf16_bits(x), f32_to_bf16_bits(f)) if dt == "bf16" else (x.astype(np.float16),
+                                                                                     f.astype(np.float16))
+        o = np.zeros((n, oh, ow, cout), np.float32)
+        desc = (f"{dt} {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{sh},{sw} d{dh},{dw} pad{pad} "
+                f"tile {th}x{tw}")
+        return mod, [x, f, o], [dt, dt, "f32"], desc
+    raise RuntimeError("no plannable conv drawn")
+
+
+def wide_gemm_case(seed: int):
+    """Random matmul programs for the DMA kernel's tile choice: M and N
+    multiples of 128 up to 2048 (odd multiples included, so 256 x 128, 128 x
+    256 and 128 x 128 tiles and the K split all occur), K multiples of 128 up
+    to 2048, 64 x 64 Block tiles, f32 results of f16 / bf16 (some with scale
+    and bias) and the i8 epilogue with an i8 result.  Returns (module, host
+    inputs, dtypes, output index, description)."""
+    import xtile_amd as xt
+    from xtile_amd import Array, bid, cdiv, convert, float32, int8, kernel, load, matmul, store, astype
+
+    rng = np.random.default_rng(35_000 + seed)
+    dt = str(rng.choice(["f16", "bf16", "i8"]))
+    while True:
+        m, n, k = 128 * int(rng.integers(1, 17)), 128 * int(rng.integers(1, 17)), 128 * int(rng.integers(1, 17))
+        if m * n * k <= 2**31:
+            break
+    epi = dt == "i8" or bool(rng.random() < 0.4)
+    ftoi = dt == "i8"
+
+    @kernel
+    def prog(lhs, rhs, res, sc, bi, tm, tn, tk):
+        x = bid(0)
+        y = bid(1)
+        t = matmul(load(lhs, index=(x, 0), shape=(tm, tk)), load(rhs, index=(0, y), shape=(tk, tn), shared=1))
+        if epi:
+            t = t * load(sc, index=(0, y), shape=(1, tn), shared=1)
+            t = t + load(bi, index=(0, y), shape=(1, tn), shared=1)
+        if ftoi:
+            t = astype(t, dtype=int8)
+        store(res, index=(x, y), tile=t)
+
+    dt_in = {"i8": xt.int8, "f16": xt.float16, "bf16": xt.bfloat16}[dt]
+    args = (Array(shape=(m, k), dtype=dt_in), Array(shape=(k, n), dtype=dt_in),
+            Array(shape=(m, n), dtype=int8 if ftoi else float32), Array(shape=(1, n), dtype=float32),
+            Array(shape=(1, n), dtype=float32), 64, 64, k)
+    mod = convert(prog, args=args, grid=(cdiv(m, 64), cdiv(n, 64), 1))
+    if dt == "i8":
+        a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+        b = rng.integers(-128, 128, (k, n), dtype=np.int8)
+        s = (rng.uniform(0.5, 2.0, (1, n)) / (np.sqrt(k) * 64)).astype(np.float32)
+        bias = rng.uniform(-20, 20, (1, n)).astype(np.float32)
+    else:
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+        a, b = (a.astype(np.float16), b.astype(np.float16)) if dt == "f16" else (f32_to_bf16_bits(a),
+                                                                               f32_to_bf16_bits(b))
+        s = rng.uniform(0.5, 2.0, (1, n)).astype(np.float32)
+        bias = rng.uniform(-2, 2, (1, n)).astype(np.float32)
+    c = np.zeros((m, n), np.int8 if ftoi else np.float32)
+    desc = f"{dt} {m}x{n}x{k} epilogue={epi} ftoi={ftoi}"
+    return mod, [a, b, c, s, bias], [dt, dt, "i8" if ftoi else "f32", "f32", "f32"], 2, desc
+
+
 def gemm_case(seed: int):
     """A random matmul program of xtile_amd.kernels: f16 / bf16 (f32 result)
     or the i8 epilogue form (i8 result of A @ B * scale + bias), M, N, K

@@ -14,7 +14,7 @@ import pytest
 
 import xtile_amd as xt
 from tests.gpu_util import frob_rel, run_gpu, run_oracle
-from tests.random_programs import conv_case
+from tests.random_programs import conv_case, wide_conv_case
 
 pytestmark = pytest.mark.gpu
 
@@ -24,6 +24,20 @@ def test_random_conv_matches_the_oracle(cuda, seed):
     mod, host, dtypes, desc = conv_case(seed)
     got = run_gpu(mod, host, dtypes, cuda, case=f"random conv {seed}: {desc}")[2]
     want = run_oracle(mod, host, 4)[2]
+    if dtypes[0] == "i8":
+        assert np.array_equal(got, want)
+    else:
+        assert frob_rel(got, want) <= 1e-3
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_wide_conv_matches_the_oracle(cuda, seed):
+    """Cin / Cout multiples of 8 (16 for i8) up to 320 / 256 over the whole
+    output (tests/random_programs.py: wide_conv_case): the implicit-GEMM kernel
+    wherever the band kernel declines."""
+    mod, host, dtypes, desc = wide_conv_case(seed)
+    got = run_gpu(mod, host, dtypes, cuda, case=f"random wide conv {seed}: {desc}")[2]
+    want = run_oracle(mod, host, 8)[2]
     if dtypes[0] == "i8":
         assert np.array_equal(got, want)
     else:

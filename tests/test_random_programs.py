@@ -44,3 +44,13 @@ def test_random_gemm_plans_onto_the_gemm_kernel(seed):
 
     mod, host, dtypes, out, desc = gemm_case(seed)
     assert xt.plan(mod)["kernel"].startswith("gemm")
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_wide_cases_plan(seed):
+    from tests.random_programs import wide_conv_case, wide_gemm_case
+
+    mod, host, dtypes, desc = wide_conv_case(seed)
+    assert xt.plan(mod)["kernel"].startswith("conv2d_nhwc")
+    mod, host, dtypes, out, desc = wide_gemm_case(seed)
+    assert xt.plan(mod)["kernel"].startswith("gemm")
