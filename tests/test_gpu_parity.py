@@ -723,3 +723,39 @@ def test_reference_traced_matmul_program(cuda):
     got = run_gpu(mod, [a, b, c, s, bias], ["i8", "i8", "i8", "f32", "f32"], cuda, case="reference-traced matmul")[2]
     want = run_oracle(mod, [a, b, c, s, bias], oracle_threads())[2]
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil,dt",
+    [
+        (1, 64, 64, 3, 64, 7, 7, 8, 32, (3, 3, 3, 3), (2, 2), (1, 1), "f16"),   # the RGB stem
+        (2, 30, 40, 3, 64, 7, 7, 5, 20, (3, 3, 3, 3), (2, 2), (1, 1), "bf16"),
+        (2, 20, 150, 3, 24, 3, 3, 4, 150, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),  # 2 pixel chunks, Cout 24
+        (1, 17, 33, 1, 8, 5, 5, 13, 17, (2, 1, 2, 3), (1, 2), (2, 1), "f16"),   # Cin 1, row dilation
+        (3, 10, 12, 5, 136, 3, 3, 5, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # Cout tile past 128
+        (2, 31, 29, 6, 72, 3, 3, 15, 29, (0, 1, 1, 1), (2, 1), (1, 1), "bf16"),
+        (1, 40, 300, 4, 32, 1, 1, 8, 300, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),  # 1 x 1, 3 chunks
+    ],
+)
+def test_conv2d_few_input_channels(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
+    """Cin * 2 bytes not a multiple of 16 (Cin 1-7: the RGB stem) with the
+    Blocks covering the output take the LDS-patch kernel (conv_small.hip): the
+    KH input rows of 128 output pixels staged in LDS, K in runs of KW * Cin
+    rounded up to 16 with zero filter rows, pixels past the row and channels
+    past Cout not stored."""
+    rng = np.random.default_rng(21)
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
+                   pad=pad, stride=stride, dilation=dil)
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
+    x = rng.normal(0, 0.5, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+    if dt == "bf16":
+        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    else:
+        x, f = x.astype(np.float16), f.astype(np.float16)
+    o = np.zeros((n, oh, ow, cout), np.float32)
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
+                  case=f"conv few channels {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil} {dt}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB

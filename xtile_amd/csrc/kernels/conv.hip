@@ -35,7 +35,9 @@
 // Kernel choice (launch_conv2d): the band kernel below when the Blocks tile
 // the whole output and filter + halo fit in LDS; else, for the same tiling
 // with Cin * esize and Cout * esize multiples of 16, the implicit GEMM with
-// DMA operands (conv_igemm.hip); else the persistent kernel above for f16 / bf16
+// DMA operands (conv_igemm.hip); for that tiling with f16 / bf16 Cin * 2 not
+// a multiple of 16 (the RGB stem), Cout % 8 == 0 and column dilation 1, the
+// LDS-patch kernel (conv_small.hip); else the persistent kernel above for f16 / bf16
 // with Cin % 32 == 0, Cout % 16 == 0 (<= 128), one image per Block, every
 // output channel and an f32 result; else the generic kernel
 // (conv_general.hip), which takes every tile shape the planner accepts.
@@ -961,6 +963,8 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   if (try_band(p, bufs, s, max_lds, cus, e)) return e;
   // filters beyond the band kernel's LDS: the implicit GEMM with DMA operands
   if (launch_conv2d_igemm(p, bufs, s, e)) return e;
+  // Cin below 8 (the RGB stem): input rows staged in LDS, K in runs of KW * Cin
+  if (launch_conv2d_small(p, bufs, s, e)) return e;
   // the persistent kernel: f16 / bf16 in, f32 out, one image per Block, every
   // output channel, 16-byte channel runs; anything else takes the generic kernel
   if (!persistent_ok) return launch_conv2d_general(p, bufs, s, why);

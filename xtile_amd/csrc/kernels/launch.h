@@ -56,6 +56,8 @@ hipError_t launch_conv2d_general(const xt::Plan& p, void* const* bufs, hipStream
 // The implicit-GEMM conv kernel (conv_igemm.hip): false, with nothing
 // launched, when the plan is outside what it takes; else `e` is the launch's status.
 bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e);
+// The few-input-channel conv kernel (conv_small.hip), same contract.
+bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e);
 hipError_t launch_tilevm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
 
 // Fused tile programs (fused_jit.cpp): compile_fused fills fp.code from
