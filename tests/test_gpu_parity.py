@@ -735,27 +735,39 @@ def test_reference_traced_matmul_program(cuda):
         (3, 10, 12, 5, 136, 3, 3, 5, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # Cout tile past 128
         (2, 31, 29, 6, 72, 3, 3, 15, 29, (0, 1, 1, 1), (2, 1), (1, 1), "bf16"),
         (1, 40, 300, 4, 32, 1, 1, 8, 300, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),  # 1 x 1, 3 chunks
+        (1, 64, 64, 3, 64, 7, 7, 8, 32, (3, 3, 3, 3), (2, 2), (1, 1), "i8"),
+        (2, 20, 150, 5, 48, 3, 3, 4, 150, (1, 1, 1, 1), (1, 1), (1, 1), "i8"),
+        (1, 17, 33, 12, 16, 5, 5, 13, 17, (2, 1, 2, 3), (1, 2), (2, 1), "i8"),
+        (1, 30, 40, 15, 32, 7, 7, 5, 20, (3, 3, 3, 3), (2, 2), (1, 1), "i8"),   # one staging round
     ],
 )
 def test_conv2d_few_input_channels(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
-    """Cin * 2 bytes not a multiple of 16 (Cin 1-7: the RGB stem) with the
-    Blocks covering the output take the LDS-patch kernel (conv_small.hip): the
+    """Cin * esize not a multiple of 16 (the RGB stem; f16 / bf16 within the
+    matmul bar, i8 bit-exact) with the Blocks covering the output take the
+    LDS-patch kernel (conv_small.hip): the
     KH input rows of 128 output pixels staged in LDS, K in runs of KW * Cin
     rounded up to 16 with zero filter rows, pixels past the row and channels
     past Cout not stored."""
     rng = np.random.default_rng(21)
-    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
-                   pad=pad, stride=stride, dilation=dil)
+    xdt = {"bf16": xt.bfloat16, "f16": xt.float16, "i8": xt.int8}[dt]
+    mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xdt, pad=pad, stride=stride, dilation=dil)
     oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
     ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
-    x = rng.normal(0, 0.5, (n, h, w, cin)).astype(np.float32)
-    f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
-    if dt == "bf16":
-        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    if dt == "i8":
+        x = rng.integers(-128, 128, (n, h, w, cin), dtype=np.int8)
+        f = rng.integers(-128, 128, (kh, kw, cin, cout), dtype=np.int8)
     else:
-        x, f = x.astype(np.float16), f.astype(np.float16)
+        x = rng.normal(0, 0.5, (n, h, w, cin)).astype(np.float32)
+        f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+        if dt == "bf16":
+            x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+        else:
+            x, f = x.astype(np.float16), f.astype(np.float16)
     o = np.zeros((n, oh, ow, cout), np.float32)
     got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
                   case=f"conv few channels {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil} {dt}")[2]
     want = run_oracle(mod, [x, f, o], oracle_threads())[2]
-    assert frob_rel(got, want) <= MM_FROB
+    if dt == "i8":  # exact i32 sums rounded to f32 once
+        assert np.array_equal(got, want)
+    else:
+        assert frob_rel(got, want) <= MM_FROB

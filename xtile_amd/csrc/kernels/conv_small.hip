@@ -1,6 +1,7 @@
-// xt.load_conv2d with few input channels (Cin * 2 bytes below 16 or not a
-// multiple of 16: the RGB stem of a CNN, Cin = 1 .. 7) as an implicit GEMM
-// over an input patch staged in LDS, for f16 / bf16 sources and an f32 result.
+// xt.load_conv2d with few input channels (Cin * esize not a multiple of 16:
+// the RGB stem of a CNN, Cin = 1 .. 7 for f16 / bf16, 1 .. 15 for i8) as an
+// implicit GEMM over an input patch staged in LDS, for f16 / bf16 / i8 sources
+// and an f32 result.
 //
 // Semantics (lib/xt/XTOps.cpp:43-90, lib/xt/XTToNova.cpp:110-142,353-437):
 //   out[n, oh, ow, o] = sum_{kh,kw,c} src[n, oh*sh - pad_t + kh*dh,
@@ -13,18 +14,22 @@
 //   * For a fixed kh, the (kw, c) terms of a pixel are KW * Cin consecutive
 //     source elements of one input row (column dilation 1), and f[kh] is
 //     KW * Cin consecutive filter rows (HWIO).  So K runs kh by kh in runs of
-//     KP = KW * Cin rounded up to 16 (one v_mfma_f32_32x32x16 step each 16);
-//     the padding positions take zero filter rows and zeroed source values.
+//     KP = KW * Cin rounded up to the MFMA depth KS (16 for
+//     v_mfma_f32_32x32x16_{f16,bf16}, 32 for v_mfma_i32_32x32x32_i8); the
+//     padding positions take zero filter rows and zeroed source values.
 //   * A workgroup computes 128 consecutive output pixels of one output row
 //     against 64 output channels, four waves of 32 pixels x 64 channels (two
-//     32 x 32 tiles).  It stages the KH input rows its pixels read (128 sw +
-//     KW - 1 columns of Cin channels, zeros outside the image) and the filter's
+//     32 x 32 tiles).  It stages the KH input rows its pixels read (127 sw +
+//     KW columns of Cin channels, zeros outside the image) and the filter's
 //     64 columns (KH * KP rows, zero past each kh's KW * Cin) in LDS once, then
-//     runs every K step from LDS: source fragments as 2-byte reads at the
-//     pixel's patch position, filter fragments by ds_read_b64_tr_b16.
+//     runs every K step from LDS: source fragments as element reads at the
+//     pixel's patch position, filter fragments by ds_read_b64_tr_b16 / _b8.
+//   * i8: exact i32 sums, rounded to f32 once at the store.
 //   * Results: a half-wave stores one 128-byte run of 32 channels per
 //     accumulator register (non-temporal); pixels past the row and channels
 //     past Cout are not stored.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -32,26 +37,35 @@ namespace xtk {
 namespace {
 
 typedef float sc_f16v __attribute__((ext_vector_type(16)));
+typedef int sc_i16v __attribute__((ext_vector_type(16)));
+
+enum { kScF16 = 0, kScBF16 = 1, kScI8 = 2 };
 
 struct ScArgs {
-  const unsigned short* src;  // NHWC input
-  const unsigned short* filt; // [KH*KW*C][CO]
+  const unsigned char* src;   // NHWC input
+  const unsigned char* filt;  // [KH*KW*C][CO]
   float* out;                 // [N][OH][OW][CO]
   unsigned src_bytes, filt_bytes;
   int H, W, C, KH, KW, CO;
   int OH, OW;
   int pad_t, pad_l, sh, sw, dh;
   int run;      // KW * C: consecutive source elements of one kh
-  int kp;       // run rounded up to 16
+  int K;        // KH * run: the reduction length
+  int kp;       // K rounded up to the MFMA depth
   int pw;       // patch columns: 127 * sw + KW
+  int npr;      // 256-element pieces a patch row
   int chunks;   // 128-pixel chunks per output row
   int ntiles;   // 64-channel tiles
-  Div31 d_prow; // / patch row pitch (pw * C rounded up to 8)
-  Div31 d_kp;   // / kp
 };
 
-template <bool BF16, bool BIG>
-__global__ __launch_bounds__(256) void conv2d_small_kernel(ScArgs p) {
+template <int ELEM, bool BIG>
+__global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p) {
+  constexpr bool I8 = ELEM == kScI8;
+  constexpr int ES = I8 ? 1 : 2;       // element bytes
+  constexpr int KS = I8 ? 32 : 16;     // MFMA depth
+  constexpr int FR = 64 * ES;          // filter tile row bytes
+  constexpr int PPR = FR / 16;         // 16-byte pieces a filter row
+  constexpr int RPR = 256 / PPR;       // filter rows a round of one piece a thread
   extern __shared__ __attribute__((aligned(16))) unsigned char sm[];
   typedef __attribute__((address_space(3))) unsigned char lds_t;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -64,117 +78,177 @@ __global__ __launch_bounds__(256) void conv2d_small_kernel(ScArgs p) {
   const int n = L / p.OH;
   const int ow0 = ch * 128, n0 = nt * 64;
 
-  // patch [KH rows][pw * C elements] of f16 / bf16, then the filter tile
-  // [KH * kp rows][64 channels] (128-byte rows, chunk c of row k at
-  // c ^ 2 ((k / 2) % 2) so a transposing read's four rows hit distinct banks).
-  // Each thread issues U loads before it writes any of them to LDS, so that
-  // their latencies overlap.
-  const int prow = p.pw * p.C;                       // elements per patch row
-  const int prow_pad = (prow + 7) & ~7;              // 16-byte multiple
-  unsigned short* patch = reinterpret_cast<unsigned short*>(sm);
-  unsigned char* ftile = sm + (size_t)p.KH * prow_pad * 2;
+  // LDS: the patch [KH rows][pw * C elements], the filter tile [kp rows][64
+  // channels] (K = (kh, kw, c) in HWIO row order, zero rows past K; FR-byte
+  // rows, 16-byte chunk c of row k at c ^ fsw(k) so that a transposing read's
+  // rows hit distinct banks: 128-byte rows XOR 2 ((k / 2) % 2), 64-byte rows
+  // XOR (k / 4) % 2), and T[k], the byte offset of K index k in a pixel's
+  // patch window (kh * row pitch + (k - kh * run)) * esize.
+  auto fsw = [](int k) { return I8 ? (k >> 2) & 1 : 2 * ((k >> 1) & 1); };
+  const int prow = p.pw * p.C;                                 // elements per patch row
+  const int prow_pad = (prow + 16 / ES - 1) & ~(16 / ES - 1);  // 16-byte multiple
+  unsigned char* const patch = sm;
+  unsigned char* const ftile = sm + p.KH * prow_pad * ES;
+  unsigned short* const T = reinterpret_cast<unsigned short*>(ftile + p.kp * FR);
+  for (int k = tid; k < p.kp; k += 256) {
+    const int kh = k / p.run;
+    T[k] = k < p.K ? (unsigned short)((kh * prow_pad + k - kh * p.run) * ES) : 0;
+  }
   const int iw_lo = ow0 * p.sw - p.pad_l;
   // a patch row's elements inside the image: columns [0, W), a range of j
   const int jlo = max(0, -iw_lo) * p.C, jhi = min(prow, (p.W - iw_lo) * p.C);
-  const long long img = (long long)n * p.H;
-  const int total = p.KH * prow_pad;
+  const int nrow = p.KH * p.npr;       // 256-element patch pieces
   // buffer loads: an offset at or past the buffer's size (kOor) reads zero,
-  // so no load sits behind a branch and all U are in flight together
+  // so no load sits behind a branch and a round's loads are in flight together
   constexpr unsigned kOor = 0x80000000u;  // both buffers are below 2 GiB
   const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(p.src), (short)0, (int)p.src_bytes, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(p.src), (short)0, (int)p.src_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rf =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(p.filt), (short)0, (int)p.filt_bytes, 0x00020000);
-  // rounds of U patch elements and UF filter pieces a thread, every load of a
-  // round issued before the round's LDS writes (BIG: one round for the
-  // 7 x 7 stem, where the LDS already holds the workgroups a CU to four)
-  constexpr int U = BIG ? 24 : 8, UF = BIG ? 8 : 2;
-  const int ftotal = p.KH * p.kp * 8;  // 16-byte pieces: 8 per 64-channel row
-  for (int r = 0; r * 256 * U < total || r * 256 * UF < ftotal; ++r) {
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(p.filt), (short)0, (int)p.filt_bytes, 0x00020000);
+  // rounds of U patch pieces and UF filter pieces a thread, every load of a
+  // round issued before the round's LDS writes (BIG: one round for the 7 x 7
+  // stem, where the LDS already holds the workgroups a CU to four).  Piece t
+  // of the patch is row t / npr, elements 256 (t % npr) + tid: the row's
+  // image row and offset are the same for every thread.
+  constexpr int U = BIG ? 28 : 12, UF = BIG ? 5 : 2;
+  const int fq = tid % PPR, fk0 = tid / PPR;  // this thread's filter piece column, first row
+  int kh_t = 0, i_t = 0;                      // piece t's row and position, t = r U + u
+  for (int r = 0; r * U < nrow || r * UF * RPR < p.kp; ++r) {
     unsigned short v[U];
+    int dst[U];
     uint4v w[UF];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int e = tid + 256 * (r * U + u);
-      const int kh = (int)p.d_prow((unsigned)e), j = e - kh * prow_pad;
-      const int ih = oh * p.sh - p.pad_t + kh * p.dh;
-      const bool in = e < total && j >= jlo && j < jhi && (unsigned)ih < (unsigned)p.H;
-      v[u] = __builtin_amdgcn_raw_buffer_load_b16(
-          rs, in ? (unsigned)(((img + ih) * p.W + iw_lo) * p.C + j) * 2u : kOor, 0, 0);
+      const int ih = oh * p.sh - p.pad_t + kh_t * p.dh;
+      const int j = tid + 256 * i_t;
+      const int rowoff = ((n * p.H + ih) * p.W + iw_lo) * p.C;
+      const bool in = r * U + u < nrow && (unsigned)ih < (unsigned)p.H && j >= jlo && j < jhi;
+      const unsigned off = in ? (unsigned)(rowoff + j) * ES : kOor;
+      if constexpr (I8)
+        v[u] = __builtin_amdgcn_raw_buffer_load_b8(rs, off, 0, 0);
+      else
+        v[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+      dst[u] = r * U + u < nrow && j < prow_pad ? kh_t * prow_pad + j : -1;
+      if (++i_t == p.npr) {
+        i_t = 0;
+        ++kh_t;
+      }
     }
 #pragma unroll
     for (int u = 0; u < UF; ++u) {
-      const int e = tid + 256 * (r * UF + u), k = e >> 3, q = e & 7;
-      const int kh = (int)p.d_kp((unsigned)k), j = k - kh * p.kp;
-      const bool in = e < ftotal && j < p.run && n0 + 8 * q < p.CO;
-      w[u] = __builtin_amdgcn_raw_buffer_load_b128(rf, in ? (unsigned)((kh * p.run + j) * p.CO + n0 + 8 * q) * 2u : kOor,
+      const int k = fk0 + RPR * (r * UF + u);
+      const bool in = k < p.K && n0 + fq * (16 / ES) < p.CO;
+      w[u] = __builtin_amdgcn_raw_buffer_load_b128(rf, in ? (unsigned)(k * p.CO + n0 + fq * (16 / ES)) * ES : kOor,
                                                    0, 0);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int e = tid + 256 * (r * U + u);
-      if (e < total) patch[e] = v[u];
+      if (dst[u] >= 0) {
+        if constexpr (I8)
+          patch[dst[u]] = (unsigned char)v[u];
+        else
+          reinterpret_cast<unsigned short*>(patch)[dst[u]] = v[u];
+      }
     }
 #pragma unroll
     for (int u = 0; u < UF; ++u) {
-      const int e = tid + 256 * (r * UF + u), k = e >> 3, q = e & 7;
-      if (e < ftotal) *reinterpret_cast<uint4v*>(ftile + k * 128 + ((q ^ (2 * ((k >> 1) & 1))) << 4)) = w[u];
+      const int k = fk0 + RPR * (r * UF + u);
+      if (k < p.kp) *reinterpret_cast<uint4v*>(ftile + k * FR + ((fq ^ fsw(k)) << 4)) = w[u];
     }
   }
   __syncthreads();
 
-  // this wave's 32 pixels: lane l % 32; K positions 8 (l / 32) .. + 7 of a step
+  // this wave's 32 pixels: lane l % 32; K positions (KS / 2) (l / 32) .. + KS / 2 - 1 of a step
   const int lr = lane & 31, hi = lane >> 5;
   const int g = lane >> 4, li = lane & 15;
-  sc_f16v acc[2];
+  typedef typename std::conditional<I8, sc_i16v, sc_f16v>::type acc_t;
+  acc_t acc[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[t][v] = 0.f;
-  const int px = wave * 32 + lr;                  // pixel within the chunk
-  const int pbase = px * p.sw * p.C;              // its first element in a patch row
-  // filter fragment offsets (N tile j, read h) in a step's first row block
+    for (int v = 0; v < 16; ++v) acc[t][v] = 0;
+  const int px = wave * 32 + lr;                                // pixel within the chunk
+  const unsigned char* const pwin = patch + px * p.sw * p.C * ES;  // its patch window
+  // filter fragment offsets (N tile t, read h) in a step's first row block
   int boff[2][2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int k = 8 * (g >> 1) + 4 * h + (li >> 2);
-      const int cb = (t * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
-      boff[t][h] = k * 128 + (((cb >> 4) ^ (2 * ((k >> 1) & 1))) << 4) + (cb & 15);
+      int k, cb;
+      if constexpr (I8) {
+        k = 16 * (g >> 1) + 8 * h + (li >> 1);
+        cb = t * 32 + 16 * (g & 1) + 8 * (li & 1);
+      } else {
+        k = 8 * (g >> 1) + 4 * h + (li >> 2);
+        cb = (t * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
+      }
+      boff[t][h] = k * FR + (((cb >> 4) ^ fsw(k)) << 4) + (cb & 15);
     }
-  for (int kh = 0; kh < p.KH; ++kh) {
-    const unsigned short* prow_p = patch + kh * prow_pad + pbase;
-    for (int j0 = 0; j0 < p.kp; j0 += 16) {
-      // source fragment: 8 consecutive elements of the run (zero past it)
-      unsigned a32[4];
+  const int nsteps = p.kp / KS;
+  // one K step: the lane's KS / 2 source elements through T (GUARD: the last
+  // step, whose positions past K read as zero), two MFMAs
+  auto step = [&](int s, auto guard) {
+    constexpr bool G = decltype(guard)::value;
+    const int k0 = s * KS + (KS / 2) * hi;
+    unsigned a32[4];
+    if constexpr (I8) {
+      const uint4v t0 = *reinterpret_cast<const uint4v*>(T + k0);
+      const uint4v t1 = *reinterpret_cast<const uint4v*>(T + k0 + 8);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int j = j0 + 8 * hi + 2 * e;
-        const unsigned lo = j < p.run ? prow_p[j] : 0u;
-        const unsigned up = j + 1 < p.run ? prow_p[j + 1] : 0u;
+        const unsigned tw0 = e < 2 ? t0[2 * e] : t1[2 * e - 4], tw1 = e < 2 ? t0[2 * e + 1] : t1[2 * e - 3];
+        const unsigned o[4] = {tw0 & 0xffffu, tw0 >> 16, tw1 & 0xffffu, tw1 >> 16};
+        unsigned word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          unsigned x = pwin[o[b]];
+          if (G && k0 + 4 * e + b >= p.K) x = 0;
+          word |= x << (8 * b);
+        }
+        a32[e] = word;
+      }
+    } else {
+      const uint4v t0 = *reinterpret_cast<const uint4v*>(T + k0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        unsigned lo = *reinterpret_cast<const unsigned short*>(pwin + (t0[e] & 0xffffu));
+        unsigned up = *reinterpret_cast<const unsigned short*>(pwin + (t0[e] >> 16));
+        if (G && k0 + 2 * e >= p.K) lo = 0;
+        if (G && k0 + 2 * e + 1 >= p.K) up = 0;
         a32[e] = lo | (up << 16);
       }
-      const uint4v a = {a32[0], a32[1], a32[2], a32[3]};
-      lds_t* const f = (lds_t*)(ftile + (kh * p.kp + j0) * 128);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint2v l2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                         reinterpret_cast<short4v __attribute__((address_space(3)))*>(
-                                                             f + boff[t][0])));
-        const uint2v h2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                         reinterpret_cast<short4v __attribute__((address_space(3)))*>(
-                                                             f + boff[t][1])));
-        const uint4v b = {l2[0], l2[1], h2[0], h2[1]};
-        if constexpr (BF16)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                           acc[t], 0, 0, 0);
-        else
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b),
-                                                          acc[t], 0, 0, 0);
-      }
     }
-  }
+    const uint4v a = {a32[0], a32[1], a32[2], a32[3]};
+    lds_t* const f = (lds_t*)(ftile + s * KS * FR);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      uint2v l2, h2;
+      if constexpr (I8) {
+        l2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                            reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[t][0])));
+        h2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                            reinterpret_cast<int2v __attribute__((address_space(3)))*>(f + boff[t][1])));
+      } else {
+        l2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                            reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[t][0])));
+        h2 = __builtin_bit_cast(uint2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                            reinterpret_cast<short4v __attribute__((address_space(3)))*>(f + boff[t][1])));
+      }
+      const uint4v b = {l2[0], l2[1], h2[0], h2[1]};
+      if constexpr (I8)
+        acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b),
+                                                       acc[t], 0, 0, 0);
+      else if constexpr (ELEM == kScBF16)
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                         acc[t], 0, 0, 0);
+      else
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), __builtin_bit_cast(half8, b),
+                                                        acc[t], 0, 0, 0);
+    }
+  };
+  for (int s = 0; s + 1 < nsteps; ++s) step(s, std::false_type{});
+  step(nsteps - 1, std::true_type{});
 
   // D = A x B: lane l holds channel 32 t + l % 32 of N tile t, register v
   // pixel 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's 32
@@ -191,12 +265,21 @@ __global__ __launch_bounds__(256) void conv2d_small_kernel(ScArgs p) {
   }
 }
 
+template <int E>
+void launch_sc(bool big, long long wgs, size_t lds, hipStream_t s, const ScArgs& a) {
+  auto kern = big ? conv2d_small_kernel<E, true> : conv2d_small_kernel<E, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(256), lds, s, a);
+}
+
 }  // namespace
 
 bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
   const xt::ConvPlan& c = p.conv;
-  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16) return false;
-  if (c.out_elem != xt::Elem::F32 || c.TC != c.CO || c.dil_w != 1 || c.C * 2 % 16 == 0 || c.CO % 8) return false;
+  const bool i8 = c.elem == xt::Elem::I8;
+  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16 && !i8) return false;
+  const long long es = i8 ? 1 : 2, ks = i8 ? 32 : 16, fr = 64 * es;
+  // 16-byte filter pieces: Cout * esize a multiple of 16
+  if (c.out_elem != xt::Elem::F32 || c.TC != c.CO || c.dil_w != 1 || c.C * es % 16 == 0 || c.CO * es % 16) return false;
   if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
       c.ch.axis == c.cw.axis)
     return false;
@@ -210,21 +293,23 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
       (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
-  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || c.filt_addr.c0 % 8) return false;
+  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || c.filt_addr.c0 * es % 16) return false;
   const long long images = gB * c.TB;
-  const long long run = c.KW * c.C, kp = (run + 15) / 16 * 16;
+  const long long run = c.KW * c.C, K = c.KH * run, kp = (K + ks - 1) / ks * ks;
   const long long pw = 127 * c.stride_w + c.KW;
-  const long long prow_pad = (pw * c.C + 7) / 8 * 8;
-  const size_t lds = (size_t)(c.KH * prow_pad * 2 + c.KH * kp * 128);
+  const long long prow_pad = (pw * c.C * es + 15) / 16 * 16 / es;
+  // patch, filter tile and the K table (16-bit byte offsets into the patch)
+  const size_t lds = (size_t)(c.KH * prow_pad * es + kp * fr + kp * 2);
+  if (c.KH * prow_pad * es >= 65536) return false;
   if (lds > size_t(kMaxLds) || images > c.N) return false;
   const long long chunks = (c.out_W + 127) / 128, ntiles = (c.CO + 63) / 64;
   const long long wgs = images * c.out_H * chunks * ntiles;
-  const long long src_bytes = images * c.H * c.W * c.C * 2, filt_bytes = c.KH * run * c.CO * 2;
+  const long long src_bytes = images * c.H * c.W * c.C * es, filt_bytes = c.KH * run * c.CO * es;
   if (!grid_fits(wgs, 256) || src_bytes >= (1LL << 31) || filt_bytes >= (1LL << 31)) return false;
-  const unsigned short* src = static_cast<const unsigned short*>(bufs[c.src_arg]);
-  const unsigned short* filt = static_cast<const unsigned short*>(bufs[c.filt_arg]) + c.filt_addr.c0;
+  const unsigned char* src = static_cast<const unsigned char*>(bufs[c.src_arg]);
+  const unsigned char* filt = static_cast<const unsigned char*>(bufs[c.filt_arg]) + c.filt_addr.c0 * es;
   float* out = static_cast<float*>(bufs[c.out_arg]);
-  if (reinterpret_cast<uintptr_t>(filt) % 16) return false;
+  if (reinterpret_cast<uintptr_t>(filt) % 16 || reinterpret_cast<uintptr_t>(src) % es) return false;
   ScArgs a;
   a.src = src;
   a.filt = filt;
@@ -245,18 +330,20 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.sw = (int)c.stride_w;
   a.dh = (int)c.dil_h;
   a.run = (int)run;
+  a.K = (int)K;
   a.kp = (int)kp;
   a.pw = (int)pw;
+  a.npr = (int)((prow_pad + 255) / 256);
   a.chunks = (int)chunks;
   a.ntiles = (int)ntiles;
-  a.d_prow = div31((unsigned)prow_pad);
-  a.d_kp = div31((unsigned)kp);
   // four workgroups a CU or fewer by LDS: the register-heavy one-round staging
   const bool big = lds * 5 > size_t(kMaxLds);
-  const bool bf = c.elem == xt::Elem::BF16;
-  auto k = bf ? (big ? conv2d_small_kernel<true, true> : conv2d_small_kernel<true, false>)
-              : (big ? conv2d_small_kernel<false, true> : conv2d_small_kernel<false, false>);
-  hipLaunchKernelGGL(k, dim3((unsigned)wgs), dim3(256), lds, s, a);
+  if (i8)
+    launch_sc<kScI8>(big, wgs, lds, s, a);
+  else if (c.elem == xt::Elem::BF16)
+    launch_sc<kScBF16>(big, wgs, lds, s, a);
+  else
+    launch_sc<kScF16>(big, wgs, lds, s, a);
   e = hipGetLastError();
   return true;
 }
