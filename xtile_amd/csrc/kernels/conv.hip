@@ -35,8 +35,8 @@
 // Kernel choice (launch_conv2d): the band kernel below when the Blocks tile
 // the whole output and filter + halo fit in LDS; else, for the same tiling
 // with Cin * esize and Cout * esize multiples of 16, the implicit GEMM with
-// DMA operands (conv_igemm.hip); for that tiling with f16 / bf16 Cin * 2 not
-// a multiple of 16 (the RGB stem), Cout % 8 == 0 and column dilation 1, the
+// DMA operands (conv_igemm.hip); for that tiling with Cin * esize not a
+// multiple of 16 (the RGB stem), Cout * esize a multiple of 16 and column dilation 1, the
 // LDS-patch kernel (conv_small.hip); else the persistent kernel above for f16 / bf16
 // with Cin % 32 == 0, Cout % 16 == 0 (<= 128), one image per Block, every
 // output channel and an f32 result; else the generic kernel
