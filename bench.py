@@ -1,6 +1,6 @@
 """Benchmark of the xtile_amd HIP path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c7]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|c1|..|c9]
 
 One step = one launch of the tile program over one batch of synthetic input
 (numpy PCG64, seed = config index, shapes of BASELINE.json's configs).  The
@@ -136,6 +136,30 @@ def make_config(name: str):
                         "1x4x56x64 Block tiles, filter shared=2, grid (32,14,1)",
             "unit": "TFLOP/s", "bound": "hbm", "dtype": "f16", "check": ("frob", 1e-3),
             "data": "synthetic: numpy PCG64 seed=4, normal(0,0.1) -> f16",
+        }
+    if name == "c8":
+        rng = np.random.default_rng(8)
+        x = rng.normal(0, 0.5, (32, 224, 224, 3)).astype(np.float16)
+        f = rng.normal(0, 0.1, (7, 7, 3, 64)).astype(np.float16)
+        return K.conv2d(32, 224, 224, 3, 64, 7, 7, 4, 112, pad=(3, 3, 3, 3), stride=(2, 2)), [
+            x, f, np.zeros((32, 112, 112, 64), np.float32)], ["f16", "f16", "f32"], 2, {
+            "workload": "c8_conv2d_stem_f16 (outside the five reference configurations: a 3-channel stem): NHWC "
+                        "32x224x224x3 * 7x7x3x64, stride 2, pad 3, f16 in, f32 out, 1x4x112x64 Block tiles, filter "
+                        "shared=2, grid (32,28,1)",
+            "unit": "TFLOP/s", "bound": "hbm", "dtype": "f16", "check": ("frob", 1e-3),
+            "data": "synthetic: numpy PCG64 seed=8, input normal(0,0.5), filter normal(0,0.1) -> f16",
+        }
+    if name == "c9":
+        rng = np.random.default_rng(9)
+        x = rng.normal(0, 0.1, (32, 14, 14, 256)).astype(np.float16)
+        f = rng.normal(0, 0.1, (3, 3, 256, 256)).astype(np.float16)
+        return K.conv2d(32, 14, 14, 256, 256, 3, 3, 2, 14), [
+            x, f, np.zeros((32, 14, 14, 256), np.float32)], ["f16", "f16", "f32"], 2, {
+            "workload": "c9_conv2d_deep_f16 (outside the five reference configurations: a deep layer whose filter "
+                        "exceeds the band kernel's LDS): NHWC 32x14x14x256 * 3x3x256x256, stride 1, pad 1, f16 in, "
+                        "f32 out, 1x2x14x256 Block tiles, filter shared=2, grid (32,7,1)",
+            "unit": "TFLOP/s", "bound": "mfma", "dtype": "f16", "check": ("frob", 1e-3),
+            "data": "synthetic: numpy PCG64 seed=9, normal(0,0.1) -> f16",
         }
     if name == "c5":
         rng = np.random.default_rng(5)
@@ -491,7 +515,7 @@ def gpu_leg(name: str, cfg, sets: list, steps: int, warmup: int, use_graph: bool
         roof = {"bound": "mfma", "achieved": achieved, "peak": peak,
                 "unit": "TOP/s" if meta["dtype"] == "i8" else "TFLOP/s",
                 "frac": achieved / peak, "traffic": _traffic(name)}
-    if name == "c4":  # report against the MFMA peak as well
+    if name in ("c4", "c8"):  # report against the MFMA peak as well
         tf = plan["flops"] / sec / 1e12
         roof["mfma_tflops"] = tf
         roof["mfma_frac"] = tf / MFMA_PEAK_TFLOPS["f16"]
@@ -728,7 +752,9 @@ def main(argv=None) -> int:
     # 2000 launches keep every timed region >= 7 ms (C1) and the clock settled
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", default="all", help="all, or a comma-separated list of c1..c7")
+    ap.add_argument("--config", default="all",
+                    help="all (c1..c7), or a comma-separated list of c1..c9 (c8, c9: conv layers outside the "
+                         "reference configurations, run only when named)")
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="oracle time per configuration; 0 skips the CPU leg (and the oracle check)")
     ap.add_argument("--no-graph", action="store_true")
