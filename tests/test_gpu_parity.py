@@ -261,6 +261,7 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
         (2, 16, 16, 16, 40, 3, 3, 4, 8, (1, 1, 1, 1), (2, 2), (1, 1), "bf16"),     # Cin 16, Cout 40, stride 2
         (3, 9, 9, 1024, 48, 1, 1, 3, 9, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),      # 1 x 1, Cout 48
         (1, 11, 13, 24, 200, 5, 5, 11, 13, (2, 2, 2, 2), (1, 1), (1, 1), "bf16"),  # Cin 24, Cout 200 (4 tiles, last 8 wide)
+        (24, 14, 14, 512, 512, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # 148 tiles, 144 stages: K in halves
     ],
 )
 def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
