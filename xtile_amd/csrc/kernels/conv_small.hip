@@ -56,6 +56,7 @@ struct ScArgs {
   int npr;      // 256-element pieces a patch row
   int chunks;   // 128-pixel chunks per output row
   int ntiles;   // 64-channel tiles
+  int nwg;      // workgroups
 };
 
 template <int ELEM, bool BIG>
@@ -69,7 +70,11 @@ __global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p
   extern __shared__ __attribute__((aligned(16))) unsigned char sm[];
   typedef __attribute__((address_space(3))) unsigned char lds_t;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // workgroup -> (image, output row, pixel chunk, channel tile); with a
+  // multiple of 8 workgroups the 8 XCDs (dispatched round-robin) receive
+  // contiguous runs of output rows, which share their input rows in one L2
   int L = blockIdx.x;
+  if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
   const int nt = L % p.ntiles;
   L /= p.ntiles;
   const int ch = L % p.chunks;
@@ -336,6 +341,7 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.npr = (int)((prow_pad + 255) / 256);
   a.chunks = (int)chunks;
   a.ntiles = (int)ntiles;
+  a.nwg = (int)wgs;
   // four workgroups a CU or fewer by LDS: the register-heavy one-round staging
   const bool big = lds * 5 > size_t(kMaxLds);
   if (i8)
