@@ -36,7 +36,17 @@ check fails the run: no JSON line is printed and the exit status is 1.
 
 roofline.achieved = algorithmic bytes (or FLOPs) of one launch / per-step
 time; roofline.traffic = measured HBM bytes per launch from the rocprofv3
-FETCH_SIZE / WRITE_SIZE summaries under profiles/ (null when absent).
+FETCH_SIZE / WRITE_SIZE summaries under profiles/ (null when absent);
+roofline.ceiling = what this GPU attains for the same bound in the same run
+(the ceiling kernels: C1 against a copy of its own 12.6 MB, the other
+bandwidth-bound configurations against a 256 MiB streaming copy, matrix-bound
+ones against the MFMA loop of their element type) and roofline.frac_of_ceiling
+= achieved / ceiling.
+
+Output: one JSON line on stdout, short enough to survive a tail of a few KB
+(per_config holds numbers only); one human-readable line per configuration on
+stderr before it; --detail PATH writes every configuration's full record
+(timing protocol, CPU sample, ceiling notes).
 
 cpu_baseline = the oracle (oracle/xt_oracle.c, the loop-lowered C executor of
 the same xt program) timed on this host's cores over whole repetitions of the
@@ -746,6 +756,82 @@ def cpu_leg(name: str, cfg, result: dict, cpu_seconds: float) -> None:
     }
 
 
+# -- the printed line ------------------------------------------------------------
+
+
+def ceiling_of(result: dict, ceil: dict) -> None:
+    """Adds roofline.ceiling (what this GPU attains for the configuration's
+    bound, measured in the same run by the kernels of include/xt_ceiling.h)
+    and roofline.frac_of_ceiling = achieved / ceiling.  C1's ceiling is a copy
+    of C1's own byte count (the launch floor of a 12.6 MB program); the other
+    bandwidth-bound configurations take the 256 MiB streaming copy; matrix-bound
+    ones the MFMA loop of their element type."""
+    roof = result["roofline"]
+    if roof["bound"] == "hbm":
+        if result["config"] == "c1":
+            c, what = ceil["c1_size_copy_GBs"], "copy of C1's 12.6 MB"
+        else:
+            c, what = ceil["hbm_copy_GBs"], "256 MiB streaming copy"
+    else:
+        key = {"f16": "mfma_f16_TFLOPs", "bf16": "mfma_bf16_TFLOPs", "i8": "mfma_i8_TOPs"}[result["dtype"]]
+        c, what = ceil[key], f"{result['dtype']} MFMA loop"
+    roof["ceiling"] = c
+    roof["ceiling_kind"] = what
+    roof["frac_of_ceiling"] = roof["achieved"] / c
+
+
+def _r(x, digits=4):
+    """Round a float to `digits` significant digits for the printed line."""
+    if isinstance(x, float) and math.isfinite(x) and x != 0.0:
+        return float(f"{x:.{digits}g}")
+    return x
+
+
+def compact(d):
+    """Numbers of a ceiling / vendor record, without its prose note."""
+    if d is None:
+        return None
+    return {k: _r(v) for k, v in d.items() if k not in ("note",) and not k.endswith("_error")}
+
+
+def compact_config(r: dict) -> dict:
+    roof = r["roofline"]
+    chk = r["check"]
+    out = {
+        "kernel": r["kernel"],
+        "value": _r(r["value"]),
+        "unit": r["unit"],
+        "us_per_step": _r(r["ms_per_step"] * 1e3),
+        "bound": roof["bound"],
+        "frac": _r(roof["frac"], 3),
+        "frac_of_ceiling": _r(roof.get("frac_of_ceiling"), 3),
+        "traffic": roof.get("traffic"),
+        "check": {"replay_equals_eager": chk["replay_equals_eager"], **(
+            {"vs_oracle": chk["vs_oracle"], "error": _r(chk["error"], 3), "bar": chk["bar"], "ok": chk["ok"]}
+            if "ok" in chk else {})},
+    }
+    if "mfma_frac" in roof:
+        out["mfma_frac"] = _r(roof["mfma_frac"], 3)
+    cpu = r.get("cpu_baseline")
+    if cpu:
+        out["cpu"] = {"value": _r(cpu["value"]), "cores": cpu["cores"], "value_1thread": _r(cpu["value_1thread"])}
+    return out
+
+
+def summary_line(r: dict) -> str:
+    roof = r["roofline"]
+    s = (f"{r['config']}: {r['ms_per_step'] * 1e3:8.2f} us/launch  {r['value']:9.1f} {r['unit']:7s} "
+         f"{roof['frac']:.3f} of peak")
+    if roof.get("frac_of_ceiling") is not None:
+        s += f", {roof['frac_of_ceiling']:.3f} of the {roof['ceiling_kind']}"
+    if "mfma_frac" in roof:
+        s += f", {roof['mfma_frac']:.3f} of f16 MFMA peak"
+    chk = r["check"]
+    if "ok" in chk:
+        s += f"; {chk['vs_oracle']} error {chk['error']:.2e} (bar {chk['bar']:g}) {'ok' if chk['ok'] else 'FAILED'}"
+    return s + f"  [{r['kernel']}]"
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -758,6 +844,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=5.0,
                     help="oracle time per configuration; 0 skips the CPU leg (and the oracle check)")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--detail", default=None, metavar="PATH",
+                    help="also write every configuration's full record (timing protocol, CPU sample) as JSON")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the ceiling and vendor legs")
     ap.add_argument("--no-precondition", action="store_true",
                     help="time from whatever clock the GPU is at (no pre-conditioning; no ceilings)")
@@ -810,6 +898,14 @@ def main(argv=None) -> int:
         for n in failed:
             print(f"[bench] {n}: output check failed: {json.dumps(results[n]['check'])}", file=sys.stderr)
         return 1
+    if ceil is not None:
+        for r in results.values():
+            ceiling_of(r, ceil)
+    if args.detail:
+        Path(args.detail).write_text(json.dumps({"attainable": ceil, "vendor": vend,
+                                                 "per_config": [results[n] for n in names]}, indent=1))
+    for n in names:
+        print("[bench] " + summary_line(results[n]), file=sys.stderr)
     h = results[headline]
     line = {
         "metric": METRIC,
@@ -824,13 +920,14 @@ def main(argv=None) -> int:
         "vs_baseline": None,
         "dtype": h["dtype"],
         "data": h["data"],
-        "config": {"workload": h["workload"], "kernel": h["kernel"], "timing": h["timing"]},
+        "config": {"workload": h["workload"], "kernel": h["kernel"]},
         "roofline": h["roofline"],
         "cpu_baseline": h.get("cpu_baseline"),
         "check": h["check"],
-        "attainable": ceil,
-        "vendor": vend,
-        "per_config": [results[n] for n in names],
+        "timing": h["timing"],
+        "attainable": compact(ceil),
+        "vendor": compact(vend),
+        "per_config": {n: compact_config(results[n]) for n in names},
     }
     print(json.dumps(line), flush=True)
     return 0

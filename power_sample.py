@@ -1,7 +1,7 @@
 """Clock and power of the GPU while one benchmark configuration runs back to back.
 
-    python -m xtile_amd.power_sample --config c3 [--seconds 3] > out.json
-    python -m xtile_amd.power_sample --config ceiling_mfma_f16   (bench.py's MFMA loop;
+    python power_sample.py --config c3 [--seconds 3] > out.json
+    python power_sample.py --config ceiling_mfma_f16   (bench.py's MFMA loop;
         also ceiling_mfma_bf16, ceiling_mfma_i8, ceiling_copy)
 
 Runs the configuration's launch (bench.py's inputs, rotating input sets)
@@ -10,7 +10,8 @@ and replayed back to back for --seconds, two replays queued at a time, while
 the host samples the driver's GPU metrics table (amdsmi gpu_metrics: current
 graphics clock per XCD, socket power, throttle status) every ~5 ms; the first
 0.5 s (the clock's ramp) are left out of the medians.
-Prints one JSON line.  Measurement tooling: the tile programs never use it.
+Prints one JSON line.  Measurement tooling beside bench.py: the xtile_amd
+package never imports it.
 """
 
 from __future__ import annotations
@@ -23,7 +24,7 @@ import sys
 import time
 from pathlib import Path
 
-ROOT = Path(__file__).resolve().parents[1]
+ROOT = Path(__file__).resolve().parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 

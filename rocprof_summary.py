@@ -1,25 +1,34 @@
 """Summarise rocprofv3 (rocpd SQLite) output for xtile_amd kernels.
 
-    python -m xtile_amd.rocprof_summary --trace T.db [--fetch F.db --write W.db
+    python rocprof_summary.py --trace T.db [--fetch F.db --write W.db
         --copy-fetch CF.db --copy-write CW.db --copy-mib 256] [--pmc P.db ...]
-        [--kernel REGEX] [--command "..."] > profiles/<config>_<kernel>.txt
+        [--kernel REGEX] [--power P.json] [--command "..."] > profiles/<config>_<kernel>.txt
 
-Kernel-trace databases give per-kernel dispatch counts and durations.  The
-FETCH_SIZE / WRITE_SIZE databases (one counter per pass) give KiB per
-dispatch; each counter is scaled by the factor that makes it read the true
-byte count of a plain device copy of --copy-mib MiB (which reads and writes
-exactly that many bytes).  The scaled bytes are printed as `fetch_bytes` /
-`write_bytes` lines, which bench.py reads as roofline.traffic.
+Measurement tooling beside bench.py; the xtile_amd package never imports it.
+
+Kernel-trace databases give per-kernel dispatch counts and durations, and for
+the selected kernel the span of its longest run of back-to-back dispatches
+divided by their count (the rate a stream of launches sustains under the
+tracer, comparable with bench.py's per-step time).  The FETCH_SIZE /
+WRITE_SIZE databases (one counter per pass) give KiB per dispatch; each
+counter is scaled by the factor that makes it read the true byte count of a
+plain device copy of --copy-mib MiB (which reads and writes exactly that many
+bytes).  The scaled bytes are printed as `fetch_bytes` / `write_bytes` lines,
+which bench.py reads as roofline.traffic.
 
 Each --pmc database (any other counters, one pass each) is reduced per
-dispatch of the selected kernel - SQ_* counters summed over their instances
-(shader engines), GRBM_* counters as the maximum over theirs (XCDs) - and
-averaged over the dispatches.  With SQ_VALU_MFMA_BUSY_CYCLES and
-GRBM_GUI_ACTIVE it also prints the matrix-core busy fraction,
-busy / (GUI-active cycles x 1024 SIMDs), and the clock the GUI-active count
-implies over the dispatch's duration; under counter collection dispatches
-run one at a time, so that clock is the one of a serialised launch, not of a
-back-to-back stream.
+dispatch of the selected kernel - counters summed over their instances - and
+averaged over the dispatches.  SQ_BUSY_CYCLES is counted by each of the 32
+shader engines (8 XCDs x 4) while it has work, so SQ_BUSY_CYCLES / 32 is the
+dispatch's length in shader-clock cycles.  From it:
+  - sq_busy_clock_GHz = (SQ_BUSY_CYCLES / 32) / traced dispatch duration
+    (dispatches run one at a time under counter collection; a lower bound of
+    the clock, since the traced duration includes the launch and drain);
+  - counter_duration_us = (SQ_BUSY_CYCLES / 32) / the clock sampled while
+    the kernel runs back to back (--power, power_sample.py);
+  - mfma_busy_fraction = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x
+    SQ_BUSY_CYCLES / 32), the share of the dispatch's cycles in which an
+    average SIMD's matrix pipe is busy.
 """
 
 from __future__ import annotations
@@ -34,12 +43,39 @@ import statistics
 SIMDS = 1024  # 256 CUs x 4 SIMDs on MI355X
 
 
+SHADER_ENGINES = 32  # 8 XCDs x 4 shader engines; each counts its own SQ_BUSY_CYCLES
+
+
 def _kernels(db_path: str, pattern: str | None):
     db = sqlite3.connect(db_path)
     rows = db.execute("select name, duration, grid_x, workgroup_x, dispatch_id from kernels").fetchall()
     if pattern:
         rows = [r for r in rows if re.search(pattern, r[0])]
     return rows
+
+
+def _span_rate(db_path: str, pattern: str):
+    """(us per dispatch, count) over the longest run of consecutive dispatches
+    (in dispatch order, no other kernel between them) of the selected kernel:
+    (end of the last - start of the first) / count."""
+    db = sqlite3.connect(db_path)
+    try:
+        rows = db.execute("select name, start, end from kernels order by start").fetchall()
+    except sqlite3.Error:
+        return None
+    best, first, n = (0, 0, 0), 0, 0  # (count, start of the first, end of the last)
+    for name, st, en in rows:
+        if re.search(pattern, name):
+            if n == 0:
+                first = st
+            n += 1
+            if n > best[0]:
+                best = (n, first, en)
+        else:
+            n = 0
+    if best[0] < 2:
+        return None
+    return (best[2] - best[1]) / 1000.0 / best[0], best[0]
 
 
 def _per_dispatch(db_path: str, pattern: str | None):
@@ -55,7 +91,7 @@ def _per_dispatch(db_path: str, pattern: str | None):
         dur[d] = du
     out = {}
     for d, cs in vals.items():
-        out[d] = ({cn: (max(v) if cn.startswith("GRBM_") else sum(v)) for cn, v in cs.items()}, dur[d])
+        out[d] = ({cn: sum(v) for cn, v in cs.items()}, dur[d])
     return out
 
 
@@ -76,9 +112,10 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel", default=None, help="regex selecting the kernel of interest")
     ap.add_argument("--command", action="append", default=[], help="command lines to record")
     ap.add_argument("--bench-log", default=None, help="stdout of the traced bench.py run")
-    ap.add_argument("--power", default=None, help="JSON line written by xtile_amd.power_sample for this config")
+    ap.add_argument("--power", default=None, help="JSON line written by power_sample.py for this config")
     args = ap.parse_args(argv)
 
+    power = json.loads(open(args.power).read().strip().splitlines()[-1]) if args.power else None
     out = []
     for c in args.command:
         out.append(f"# command: {c}")
@@ -101,6 +138,10 @@ def main(argv=None) -> int:
             out.append(f"selected_kernel: {args.kernel}")
             out.append(f"selected_avg_us: {statistics.mean(sel):.3f}")
             out.append(f"selected_median_us: {statistics.median(sel):.3f}")
+            span = _span_rate(args.trace, args.kernel)
+            if span:
+                out.append(f"selected_back_to_back_us_per_dispatch: {span[0]:.3f}  (span of the longest run of "
+                           f"{span[1]} consecutive dispatches / count)")
     if args.bench_log:
         lines = [ln for ln in open(args.bench_log).read().splitlines() if ln.startswith('{"metric"')]
         if lines:
@@ -140,20 +181,28 @@ def main(argv=None) -> int:
         for cn in names:
             vals = [cs[cn] for cs, _ in per.values() if cn in cs]
             out.append(f"{cn}: {statistics.mean(vals):.0f}")
-        busy = [cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (cs["GRBM_GUI_ACTIVE"] * SIMDS)
-                for cs, _ in per.values() if "SQ_VALU_MFMA_BUSY_CYCLES" in cs and cs.get("GRBM_GUI_ACTIVE")]
-        clk = [cs["GRBM_GUI_ACTIVE"] / d for cs, d in per.values() if cs.get("GRBM_GUI_ACTIVE") and d]
         durs = [d / 1000.0 for _, d in per.values()]
         out.append(f"pmc_dispatch_avg_us: {statistics.mean(durs):.3f}")
-        if busy:
-            out.append(f"mfma_busy_fraction: {statistics.mean(busy):.3f}  "
-                       "(SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs))")
-        if clk:
-            out.append(f"gui_active_clock_GHz: {statistics.mean(clk):.3f}  (GRBM_GUI_ACTIVE / dispatch duration, "
-                       "serialised dispatches)")
-    if args.power:
-        rec = json.loads(open(args.power).read().strip().splitlines()[-1])
-        out.append("# clock and power while the kernel runs back to back (xtile_amd.power_sample)")
+        cyc = [(cs["SQ_BUSY_CYCLES"] / SHADER_ENGINES, cs, d) for cs, d in per.values() if cs.get("SQ_BUSY_CYCLES")]
+        if cyc:
+            out.append(f"sq_busy_cycles_per_engine: {statistics.mean(c for c, _, _ in cyc):.0f}  "
+                       f"(SQ_BUSY_CYCLES / {SHADER_ENGINES} shader engines)")
+            clk = [c / d for c, _, d in cyc if d]
+            if clk:
+                out.append(f"sq_busy_clock_GHz: {statistics.mean(clk):.3f}  ((SQ_BUSY_CYCLES / {SHADER_ENGINES}) / "
+                           "traced duration of the serialised dispatch)")
+            if power and power.get("gfxclk_MHz_median"):
+                ghz = power["gfxclk_MHz_median"] / 1000.0
+                out.append(f"counter_duration_us: {statistics.mean(c for c, _, _ in cyc) / ghz / 1000.0:.3f}  "
+                           f"((SQ_BUSY_CYCLES / {SHADER_ENGINES}) / the sampled {ghz:.3f} GHz)")
+            busy = [cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (c * SIMDS) for c, cs, _ in cyc
+                    if "SQ_VALU_MFMA_BUSY_CYCLES" in cs]
+            if busy:
+                out.append(f"mfma_busy_fraction: {statistics.mean(busy):.3f}  (SQ_VALU_MFMA_BUSY_CYCLES / "
+                           f"(1024 SIMDs x SQ_BUSY_CYCLES / {SHADER_ENGINES}))")
+    if power:
+        rec = power
+        out.append("# clock and power while the kernel runs back to back (power_sample.py)")
         for k in ("launches", "us_per_launch", "gfxclk_MHz_median", "gfxclk_MHz_per_xcd", "socket_power_W_median",
                   "throttle_status", "samples"):
             if k in rec:

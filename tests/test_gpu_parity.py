@@ -622,7 +622,9 @@ def test_matmul_epilogue_variants(cuda, dt, scale, bias, ftoi):
     "dt,m_,n_,k_",
     [("f16", 1024, 1024, 4096),   # 64 tiles of 128 x 128: K in 4 ranges of 32 stages
      ("bf16", 1024, 2048, 2048),  # 128 tiles: 2 ranges
-     ("f16", 512, 768, 1536)],    # 24 tiles: K 1536 = 48 stages, 3 ranges
+     ("f16", 512, 768, 1536),     # 24 tiles: K 1536 = 48 stages, 3 ranges
+     ("f16", 256, 256, 9280),     # 4 tiles: 290 stages in 18 ranges of 16-17 (even spread)
+     ("bf16", 256, 256, 8768)],   # 274 stages in 17 ranges of 16-17
 )
 def test_matmul_k_split(cuda, dt, m_, n_, k_):
     """f32 GEMMs without an epilogue whose 256 x 256 tiles would fill at most
@@ -638,6 +640,47 @@ def test_matmul_k_split(cuda, dt, m_, n_, k_):
     got = run_gpu(mod, [a, b, c], [dt, dt, "f32"], cuda, case=f"mm k-split {dt} {m_}x{n_}x{k_}")[2]
     want = run_oracle(mod, [a, b, np.zeros_like(c)], oracle_threads())[2]
     assert frob_rel(got, want) <= MM_FROB
+
+
+def test_k_split_opt_out_is_reproducible(cuda, monkeypatch):
+    """XTILE_AMD_KSPLIT=0 keeps the tiles of a GEMM and of an implicit-GEMM
+    conv that would split K whole: no atomic partial sums, so repeated
+    launches give the same bits, within the bar of the oracle."""
+    import torch
+
+    monkeypatch.setenv("XTILE_AMD_KSPLIT", "0")
+    rng = np.random.default_rng(15)
+    dev = torch.device("cuda:0")
+    m_, n_, k_ = 1024, 1024, 4096  # 64 tiles of 128 x 128: split in 4 unless opted out
+    mod = K.matmul_f16(m_, n_, k_, 128, 128)
+    a = rng.normal(0, 1, (m_, k_)).astype(np.float16)
+    b = rng.normal(0, 1, (k_, n_)).astype(np.float16)
+    bufs = [torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), torch.zeros((m_, n_), device=dev)]
+    outs = []
+    for i in range(3):
+        print(f"[gpu] mm k-split opted out, launch {i}", flush=True)
+        bufs[2].fill_(7.0)
+        xt.launch(mod, *bufs)
+        torch.cuda.synchronize()
+        outs.append(bufs[2].cpu().numpy())
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs)
+    want = run_oracle(mod, [a, b, np.zeros((m_, n_), np.float32)], oracle_threads())[2]
+    assert frob_rel(outs[0], want) <= MM_FROB
+    # a conv whose 52 tiles would split K in 4
+    mod = K.conv2d(32, 7, 7, 512, 512, 3, 3, 7, 7)
+    x = rng.normal(0, 0.1, (32, 7, 7, 512)).astype(np.float16)
+    f = rng.normal(0, 0.1, (3, 3, 512, 512)).astype(np.float16)
+    bufs = [torch.from_numpy(x).to(dev), torch.from_numpy(f).to(dev), torch.zeros((32, 7, 7, 512), device=dev)]
+    outs = []
+    for i in range(3):
+        print(f"[gpu] conv igemm k-split opted out, launch {i}", flush=True)
+        bufs[2].fill_(7.0)
+        xt.launch(mod, *bufs)
+        torch.cuda.synchronize()
+        outs.append(bufs[2].cpu().numpy())
+    assert all(np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)) for o in outs)
+    want = run_oracle(mod, [x, f, np.zeros((32, 7, 7, 512), np.float32)], oracle_threads())[2]
+    assert frob_rel(outs[0], want) <= MM_FROB
 
 
 @pytest.mark.parametrize(
@@ -740,6 +783,11 @@ def test_reference_traced_matmul_program(cuda):
         (2, 20, 150, 5, 48, 3, 3, 4, 150, (1, 1, 1, 1), (1, 1), (1, 1), "i8"),
         (1, 17, 33, 12, 16, 5, 5, 13, 17, (2, 1, 2, 3), (1, 2), (2, 1), "i8"),
         (1, 30, 40, 15, 32, 7, 7, 5, 20, (3, 3, 3, 3), (2, 2), (1, 1), "i8"),   # one staging round
+        (2, 33, 47, 12, 64, 3, 3, 17, 12, (1, 1, 1, 1), (2, 2), (1, 1), "f16"),  # Cin past 8: wider patch rows
+        (2, 33, 47, 12, 64, 3, 3, 17, 12, (1, 1, 1, 1), (2, 2), (1, 1), "bf16"),
+        (1, 29, 35, 20, 32, 3, 3, 5, 18, (1, 1, 1, 1), (2, 2), (1, 1), "f16"),
+        (1, 29, 35, 20, 32, 3, 3, 5, 18, (1, 1, 1, 1), (2, 2), (1, 1), "bf16"),
+        (1, 24, 30, 13, 48, 5, 5, 6, 15, (2, 2, 2, 2), (1, 1), (1, 1), "f16"),   # odd Cin, 5 x 5
     ],
 )
 def test_conv2d_few_input_channels(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):

@@ -477,10 +477,12 @@ struct BandArgs {
   int rb_shift;          // log2(bytes per filter row)
   int fsw_unit, fsw_shift, fsw_mask;  // filter chunk swizzle: unit * ((k >> shift) & mask)
   int pitch;             // LDS bytes per halo pixel: 2*Cin (+16 to make the chunk count odd)
+  int rpitch;            // LDS bytes per halo row: rf_w * pitch + a pad of whole chunks (see try_band)
   int nch;               // 16-byte data chunks per halo pixel: Cin * esize / 16
   int nchp;              // pitch / 16
   int ppi;               // halo pixels per DMA instruction: 64 / nchp
-  Magic m_nchp, m_rfw, m_ow;
+  int ipr;               // DMA instructions per halo row: ceil(rf_w / ppi)
+  Magic m_nchp, m_ipr, m_ow;
   int filt_instr;        // 1 KB DMA runs of the filter
   unsigned filt_bytes;   // K*CO*esize (LDS offset of the halo)
   unsigned image_bytes;  // H*W*C*esize
@@ -559,7 +561,7 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
   for (int t = 0; t < MI; ++t) {
     const int q = min(q0 + t * tstride + lr, qend - 1);
     const int r = (int)udiv((unsigned)q, p.m_ow), c = q - r * p.OW;
-    pa[t] = (r * p.sh * p.rf_w + c * p.sw) * p.pitch + hi * 16;
+    pa[t] = r * p.sh * p.rpitch + c * p.sw * p.pitch + hi * 16;
   }
   typedef short8 __attribute__((address_space(3))) lds_s8;
   auto read = [&](const int (&ra)[MI], const int (&rb)[2], int c, short8 (&a)[MI], short8& b) {
@@ -594,7 +596,7 @@ __device__ __forceinline__ void band_tiles(const BandArgs& p, const band_lds_t* 
   // the pair index, so a tap of CS / 2 pairs starts on set PAR.
   short8 a00[MI], a01[MI], a10[MI], a11[MI], b00, b01, b10, b11;
   const int dcol = p.dw * p.pitch;                                // next tap in the filter row
-  const int drow = (p.dh * p.rf_w - (p.KW - 1) * p.dw) * p.pitch;  // first tap of the next row
+  const int drow = p.dh * p.rpitch - (p.KW - 1) * p.dw * p.pitch;  // first tap of the next row
   const int taps = p.KH * p.KW;
   int tap = 0, kw = 0;
   read(pa, pb, 0, a00, b00);
@@ -698,7 +700,6 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
   const int r0 = (band - n * p.bands_per_image) * p.R;
   const int rows = min(p.R, p.OH - r0);
   const int hrows = (rows - 1) * p.sh + (p.KH - 1) * p.dh + 1;
-  const int hpix = hrows * p.rf_w;
   // -- DMA: filter, then halo --------------------------------------------
   {
     const __amdgpu_buffer_rsrc_t fr = buffer_of(p.filt, p.filt_bytes);
@@ -712,25 +713,27 @@ __global__ __launch_bounds__(BWG, 1) void conv2d_band_kernel(BandArgs p) {
     }
     // Halo pixels are `pitch` bytes apart in LDS (an odd number of 16-byte
     // chunks, so sixteen consecutive pixels fall in sixteen distinct bank
-    // groups).  One DMA instruction writes ppi whole pixels: lane l carries
-    // chunk l % nchp of pixel l / nchp; the pad chunk reads zero and lanes past
-    // ppi * nchp are masked off.
+    // groups) and halo rows `rpitch` bytes apart (padded so that a group of
+    // sixteen output pixels that crosses an output row still does).  One DMA
+    // instruction writes ppi whole pixels of one halo row: lane l carries
+    // chunk l % nchp of pixel l / nchp; the pad chunk reads zero, and lanes
+    // past ppi * nchp or past the row are masked off (no LDS write).
     const __amdgpu_buffer_rsrc_t ir = buffer_of(p.src + (size_t)n * p.image_bytes, p.image_bytes);
     const int ih0 = r0 * p.sh - p.pad_t, iw0 = -p.pad_l;
     const int lp = (int)udiv((unsigned)lane, p.m_nchp);
     const int lc = lane - lp * p.nchp;
-    const bool lane_on = lp < p.ppi;
     const int nch = p.nch;
-    const int hinstr = (hpix + p.ppi - 1) / p.ppi;
+    const int hinstr = hrows * p.ipr;
     for (int i = wave; i < hinstr; i += BWG / 64) {
-      const int q = i * p.ppi + lp;
-      const int hr = (int)udiv((unsigned)q, p.m_rfw), hc = q - hr * p.rf_w;
+      const int hr = (int)udiv((unsigned)i, p.m_ipr), piece = i - hr * p.ipr;
+      const int hc = piece * p.ppi + lp;
       const int ih = ih0 + hr, iw = iw0 + hc;
-      const bool inside = lc < nch && q < hpix && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+      const bool inside = lc < nch && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
       const unsigned off = inside ? (unsigned)((ih * p.W + iw) * nch + lc) * 16u : kOutOfRange;
-      if (lane_on)
+      if (lp < p.ppi && hc < p.rf_w)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ir, (void __attribute__((address_space(3)))*)(Hs + i * p.ppi * p.pitch), 16, off, 0, 0, 0);
+            ir, (void __attribute__((address_space(3)))*)(Hs + hr * p.rpitch + piece * p.ppi * p.pitch), 16, off,
+            0, 0, 0);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA has landed
@@ -811,15 +814,30 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   const long long rf_w = (c.out_W - 1) * c.stride_w + (c.KW - 1) * c.dil_w + 1;
   const long long image_bytes = c.H * c.W * PB;
   if (image_bytes >= (1LL << 31) || filt_bytes >= (1LL << 31)) return false;
+  // Halo rows are rpitch bytes apart: rf_w pixels plus g pad chunks, g the
+  // smallest in [0, 16) for which a step to the next output row moves the
+  // pixel address by OW * sw pixels modulo 16 chunks (sh * rpitch = OW * sw *
+  // pitch mod 256 bytes), as a step along a row does.  Then the sixteen
+  // consecutive output pixels of a fragment read hit sixteen distinct 16-byte
+  // bank groups even where they cross an output row (with an unpadded row the
+  // address jumps by (rf_w - OW) pixels there: C4's 2-pixel jump cost about
+  // one bank-conflict cycle per LDS instruction).  No such g: no pad.
+  long long gpad = 0;
+  for (long long g = 0; g < 16; ++g)
+    if ((c.stride_h * (rf_w * nchp + g) - c.out_W * c.stride_w * nchp) % 16 == 0) {
+      gpad = g;
+      break;
+    }
+  const long long rpitch = rf_w * pitch + 16 * gpad;
+  const long long ipr = (rf_w + ppi - 1) / ppi;
   // rows per band: spread gB * OH rows over the CUs, shrink until LDS fits
   const long long total_rows = gB * c.out_H;
   long long R = std::min<long long>(c.out_H, (total_rows + cus - 1) / std::max(cus, 1));
   size_t lds = 0;
-  long long hpix_max = 0;
+  long long hrows_max = 0;
   for (; R >= 1; --R) {
-    const long long hrows = (R - 1) * c.stride_h + (c.KH - 1) * c.dil_h + 1;
-    hpix_max = hrows * rf_w;
-    const long long halo = ((hpix_max + ppi - 1) / ppi) * ppi * pitch;
+    hrows_max = (R - 1) * c.stride_h + (c.KH - 1) * c.dil_h + 1;
+    const long long halo = hrows_max * rpitch;
     if (filt_bytes + halo <= max_lds) {
       lds = static_cast<size_t>(filt_bytes + halo);
       break;
@@ -827,7 +845,7 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   }
   if (R < 1) return false;
   // the kernel divides pixel indices below 2^16 by multiply-high reciprocals
-  if (hpix_max + ppi >= 65536 || R * c.out_W >= 65536 || rf_w >= 65536 || c.out_W >= 65536) return false;
+  if (hrows_max * ipr >= 65536 || R * c.out_W >= 65536 || rf_w >= 65536 || c.out_W >= 65536) return false;
   if (R * c.out_W * c.CO * 4 >= (1LL << 31)) return false;
   BandArgs a;
   a.src = static_cast<const unsigned char*>(bufs[c.src_arg]);
@@ -866,10 +884,12 @@ bool try_band(const xt::Plan& p, void* const* bufs, hipStream_t s, int max_lds, 
   a.fsw_mask = RB / blk - 1;
   a.nch = (int)(PB / 16);
   a.pitch = (int)pitch;
+  a.rpitch = (int)rpitch;
   a.nchp = (int)nchp;
   a.ppi = (int)ppi;
+  a.ipr = (int)ipr;
   a.m_nchp = udiv_magic((unsigned)nchp);
-  a.m_rfw = udiv_magic((unsigned)rf_w);
+  a.m_ipr = udiv_magic((unsigned)ipr);
   a.m_ow = udiv_magic((unsigned)c.out_W);
   a.filt_instr = (int)(filt_bytes / 1024);
   a.filt_bytes = (unsigned)filt_bytes;

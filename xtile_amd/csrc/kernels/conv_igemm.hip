@@ -76,7 +76,7 @@ struct IgArgs {
   int ntiles;   // channel tiles: CO / BN
   int tiles;    // ceil(M / BM) * ntiles
   int ksplit;   // K ranges per tile (1: one workgroup per tile)
-  int kstages;  // stages per K range (the last may have fewer)
+  int kstages;  // the shortest K range: range r covers stages [r S / ksplit, (r + 1) S / ksplit)
   int nwg;      // tiles * ksplit
   Div31 d_ohw, d_ow;
 };
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
 
   // tap state of the next stage to load
   // this workgroup's stages [s_begin, s_begin + ns)
-  const int s_begin = kr * p.kstages;
+  const int s_begin = (int)((long long)kr * p.stages / p.ksplit);
   int lkt = s_begin, lcc = s_begin % p.cs, lkh = 0, lkw = s_begin / p.cs;
   lkh = lkw / p.KW;
   lkw -= lkh * p.KW;
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // is done with stage s - 1, whose buffer then receives stage s + NS - 1.
   // The barriers are bare s_barriers: __syncthreads' release fence would wait
   // for every DMA in flight.
-  const int ns = min(p.kstages, p.stages - s_begin);
+  const int ns = (int)((long long)(kr + 1) * p.stages / p.ksplit) - s_begin;
 #pragma unroll
   for (int q = 0; q < NS - 1; ++q)
     if (q < ns) dma_stage(buf(q));
@@ -444,13 +444,15 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
     cus = 256;
+  // (XTILE_AMD_KSPLIT=0 keeps every tile whole.)  Ranges are spread evenly:
+  // their lengths differ by at most one stage.
   long long ksplit = 1;
-  if (!i8 && tiles * 2 <= cus) ksplit = std::max(1LL, std::min<long long>(cus / tiles, a.stages / 16));
+  const bool split_ok = !i8 && ksplit_allowed();
+  if (split_ok && tiles * 2 <= cus) ksplit = std::max(1LL, std::min<long long>(cus / tiles, a.stages / 16));
   // up to one round of tiles with a long K: two halves of >= 64 stages
   // (14 x 14 x 512 -> 512, 196 tiles, 144 stages: 63.7 us whole, 56.9 split)
-  else if (!i8 && tiles <= cus && a.stages >= 128) ksplit = 2;
-  a.kstages = (int)((a.stages + ksplit - 1) / ksplit);
-  ksplit = (a.stages + a.kstages - 1) / a.kstages;
+  else if (split_ok && tiles <= cus && a.stages >= 128) ksplit = 2;
+  a.kstages = (int)(a.stages / ksplit);
   const long long nwg = tiles * ksplit;
   if (!grid_fits(nwg, 256) || M * c.CO % 4) return false;
   a.tiles = (int)tiles;

@@ -1,5 +1,6 @@
 // xt.load_conv2d with few input channels (Cin * esize not a multiple of 16:
-// the RGB stem of a CNN, Cin = 1 .. 7 for f16 / bf16, 1 .. 15 for i8) as an
+// the RGB stem of a CNN; any Cin whose row of channels is not a whole number
+// of 16-byte pieces: 3, 5, 12, 20 ... for f16 / bf16, 3, 12, 15 ... for i8) as an
 // implicit GEMM over an input patch staged in LDS, for f16 / bf16 / i8 sources
 // and an f32 result.
 //
@@ -271,9 +272,12 @@ __global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p
 }
 
 template <int E>
-void launch_sc(bool big, long long wgs, size_t lds, hipStream_t s, const ScArgs& a) {
+hipError_t launch_sc(bool big, long long wgs, size_t lds, hipStream_t s, const ScArgs& a) {
   auto kern = big ? conv2d_small_kernel<E, true> : conv2d_small_kernel<E, false>;
+  const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(kern));
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(256), lds, s, a);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -345,12 +349,11 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   // four workgroups a CU or fewer by LDS: the register-heavy one-round staging
   const bool big = lds * 5 > size_t(kMaxLds);
   if (i8)
-    launch_sc<kScI8>(big, wgs, lds, s, a);
+    e = launch_sc<kScI8>(big, wgs, lds, s, a);
   else if (c.elem == xt::Elem::BF16)
-    launch_sc<kScBF16>(big, wgs, lds, s, a);
+    e = launch_sc<kScBF16>(big, wgs, lds, s, a);
   else
-    launch_sc<kScF16>(big, wgs, lds, s, a);
-  e = hipGetLastError();
+    e = launch_sc<kScF16>(big, wgs, lds, s, a);
   return true;
 }
 

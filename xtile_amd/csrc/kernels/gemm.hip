@@ -93,8 +93,9 @@ struct GemmArgs {
   int group;
   int has_scale, has_bias;
   // K split (DMA kernel, f32 results without an epilogue): nwg = tiles *
-  // ksplit workgroups, K range r covering stages [r kstages, (r + 1)
-  // kstages) of 64 K bytes; ksplit = 1, tiles = nwg otherwise
+  // ksplit workgroups, K range r covering stages [r S / ksplit, (r + 1) S /
+  // ksplit) of the S = 2 nk stages of 64 K bytes (ranges differ by at most
+  // one stage; kstages = the shortest); ksplit = 1, tiles = nwg otherwise
   int tiles, ksplit, kstages;
 };
 
@@ -508,8 +509,9 @@ __global__ __launch_bounds__(64 * NW, BMT * BNT <= 128 * 128 ? 2 : 1) void gemm_
   const i32x4 ra = raw_rsrc(t.A), rb = raw_rsrc(t.B);
   const unsigned lda = (unsigned)(p.lda * ES), ldb = (unsigned)(p.ldb * ES);
   // this workgroup's stages of 64 K bytes: [kbase, kbase + nk)
-  const int kbase = KS ? (gemm_lin(p) / p.tiles) * p.kstages : 0;
-  const int nk = KS ? min(p.kstages, p.nk * 2 - kbase) : p.nk * 2;
+  const int krange = KS ? gemm_lin(p) / p.tiles : 0;
+  const int kbase = KS ? (int)((long long)krange * (p.nk * 2) / p.ksplit) : 0;
+  const int nk = KS ? (int)((long long)(krange + 1) * (p.nk * 2) / p.ksplit) - kbase : p.nk * 2;
 
   // B row k keeps its 16-byte chunk c at c ^ bsw(k) (rows of 128-byte i8:
   // (k / 2) % 4, so the eight rows a half-wave's tr_b8 read covers still
@@ -982,7 +984,7 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   const bool out_i8 = p.c.elem == xt::Elem::I8;
   long long M = 0, N = 0;
   float* const cbase = static_cast<float*>(bufs[p.c.arg]) + p.c.addr.c0;
-  const bool can_split = !i8 && !out_i8 && !p.gemm_scale && !p.gemm_bias && c_region(p, M, N) && N % 4 == 0 &&
+  const bool can_split = ksplit_allowed() && !i8 && !out_i8 && !p.gemm_scale && !p.gemm_bias && c_region(p, M, N) && N % 4 == 0 &&
                          p.c.ld % 4 == 0 && reinterpret_cast<uintptr_t>(cbase) % 16 == 0 && M < (1LL << 31);
   // Workgroup tile, all on the DMA kernel: 256 x 256 when the Blocks map onto
   // it and its tiles fill the CUs, or are few enough for the K split below;
@@ -1064,18 +1066,19 @@ hipError_t launch_gemm(const xt::Plan& p, void* const* bufs, hipStream_t s, std:
   a.kstages = a.nk * 2;
   // K split: when the 256 x 256 tiles fill at most an eighth of the CUs, f32
   // results of f16 / bf16 products without an epilogue split K into ranges
-  // of at least 16 stages, one workgroup each, adding their partial sums
-  // atomically into the zero-filled output (the f32 addition order, and so
-  // the last bits, vary between runs; i8 sums stay exact and whole).
+  // of at least 16 stages (spread evenly: lengths differ by at most one),
+  // one workgroup each, adding their partial sums atomically into the
+  // zero-filled output (the f32 addition order, and so the last bits, vary
+  // between runs; i8 sums stay exact and whole).  XTILE_AMD_KSPLIT=0 turns
+  // the split off (run-to-run reproducible results).
   // Measured (f16, 30 launches): 1024 x 1024 x 4096 (16 tiles) 79.2 us whole,
   // 42.8 in 8 ranges; 2048^3 (64 tiles) 47.3 whole, 71.4 in 4; 1024 x 8192 x
   // 8192 (128 tiles) 155.9 whole, 164.4 in 2.
   if (can_split && ((bm == 256 && bn == 256 && nwg * 8 <= cus) || (tiny && bm == 128 && bn == 128 && nwg * 2 <= cus))) {
     const long long nk2 = a.nk * 2LL;
-    long long ks = std::min<long long>(cus / nwg, nk2 / 16);
+    const long long ks = std::min<long long>(cus / nwg, nk2 / 16);
     if (ks > 1) {
-      a.kstages = (int)((nk2 + ks - 1) / ks);
-      ks = (nk2 + a.kstages - 1) / a.kstages;
+      a.kstages = (int)(nk2 / ks);
       a.ksplit = (int)ks;
       a.nwg = (int)(nwg * ks);
       const long long n4 = M * (N / 4);

@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <mutex>
 #include <set>
 #include <string>
@@ -40,6 +41,16 @@ inline hipError_t allow_full_lds(const void* kernel) {
   e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
   if (e == hipSuccess) done.insert({kernel, dev});
   return e;
+}
+
+// Whether the GEMM and implicit-GEMM conv launchers may split K across
+// workgroups whose f32 partial sums are added atomically (faster on launches
+// of few tiles; the addition order, and so the last bits, vary between runs).
+// XTILE_AMD_KSPLIT=0 in the environment turns it off (read at each launch,
+// so a process may switch it between launches).
+inline bool ksplit_allowed() {
+  const char* v = std::getenv("XTILE_AMD_KSPLIT");
+  return !(v && v[0] == '0' && v[1] == '\0');
 }
 
 // Blocks of the plan's grid, in 64 bits (three int32 axes).
