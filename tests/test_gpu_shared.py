@@ -269,10 +269,13 @@ def test_scale_rows_shared_moving_index(cuda, monkeypatch, fuse, k):
     _check(cuda, text, host, ["f32"] * 4, 3, "exact", kernel, _plants(text, k), f"{kernel} shared={k}")
 
 
+@pytest.mark.parametrize("stage", ["1", "0"])
 @pytest.mark.parametrize("k", [1, 2])
-def test_tile_vm_matmul_shared_moving_index(cuda, k):
-    """An f32 matmul of 16x16 tiles (the tile interpreter's matmul) whose
-    left operand's index (bid0, bid1) is shared=k."""
+def test_tile_vm_matmul_shared_moving_index(cuda, monkeypatch, stage, k):
+    """An f32 matmul of 16x16 tiles whose left operand's index (bid0, bid1)
+    is shared=k: on the staged kernel (f32 MFMA) and on the tile interpreter
+    (XTILE_AMD_STAGE=0)."""
+    monkeypatch.setenv("XTILE_AMD_STAGE", stage)
     mr = "memref<64x64xf32>"
     t = "tensor<16x16xf32>"
     body = (
@@ -286,7 +289,8 @@ def test_tile_vm_matmul_shared_moving_index(cuda, k):
     a = rng.normal(size=(64, 64)).astype(np.float32)
     b = rng.normal(size=(64, 64)).astype(np.float32)
     host = [a, b, np.zeros_like(a)]
-    _check(cuda, text, host, ["f32"] * 3, 2, "close", "tile_vm", _plants(text, k), f"tile_vm matmul shared={k}")
+    kernel = "staged" if stage == "1" else "tile_vm"
+    _check(cuda, text, host, ["f32"] * 3, 2, "close", kernel, _plants(text, k), f"{kernel} matmul shared={k}")
 
 
 def test_conv_filter_at_a_constant_index_of_a_stack(cuda):

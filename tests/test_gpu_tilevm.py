@@ -1,4 +1,5 @@
-"""GPU parity of the tile interpreter (kernels/tilevm.hip) against the oracle.
+"""GPU parity of the tile interpreter (kernels/tilevm.hip) and of the staged
+kernel that compiles the same lowering (csrc/staged.cpp) against the oracle.
 
 Programs: the reference DSL test programs that are neither one of the four
 benchmark families nor conv (unary ops, reshape, transpose, column reduce,
@@ -26,6 +27,16 @@ from tests.gpu_util import frob_rel, run_gpu, run_oracle
 from xtile_amd import kernels as K
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, params=["staged", "interpreter"])
+def vm_path(request, monkeypatch):
+    """Every program here runs twice: compiled (the staged kernel, for the
+    programs the fused layout declines) and on the interpreter itself
+    (XTILE_AMD_STAGE=0)."""
+    if request.param == "interpreter":
+        monkeypatch.setenv("XTILE_AMD_STAGE", "0")
+    return request.param
 
 
 def _golden(name):
@@ -195,7 +206,7 @@ def test_attention_block(cuda):
     np.testing.assert_allclose(want, (p / p.sum(axis=1, keepdims=True)) @ v, rtol=0, atol=1e-5)
 
 
-def test_small_tile_i8_matmul_epilogue_is_bit_exact(cuda):
+def test_small_tile_i8_matmul_epilogue_is_bit_exact(cuda, vm_path):
     """kernels/matmul.py's program with 16 x 8 tiles (below the MFMA GEMM's
     64 x 64): i8 x i8, * scale + bias, astype(int8)."""
     from tests.golden.dsl_programs import programs
@@ -206,7 +217,7 @@ def test_small_tile_i8_matmul_epilogue_is_bit_exact(cuda):
     m = xt.convert(kern, args=(xt.Array((M, Kd), xt.int8), xt.Array((Kd, N), xt.int8), xt.Array((M, N), xt.int8),
                                xt.Array((1, N), xt.float32), xt.Array((1, N), xt.float32), tm, tn, Kd),
                    grid=(M // tm, N // tn, 1), double_buffering=True)
-    assert xt.plan(m)["kernel"].startswith("tile_vm")
+    assert xt.plan(m)["kernel"].startswith("staged" if vm_path == "staged" else "tile_vm")
     rng = np.random.default_rng(30)
     a = rng.integers(-128, 128, (M, Kd), dtype=np.int8)
     b = rng.integers(-128, 128, (Kd, N), dtype=np.int8)

@@ -116,24 +116,42 @@ def test_conv_inside_a_larger_program_gives_the_conv_form():
 
 
 @pytest.mark.parametrize(
-    "name,kernel",
+    "name,kernel,interp",
     [
-        ("unary_and_shape", "tile_vm f32 insts=12 loads=2 stores=3 lds="),
-        ("column_reduce", "fused f32 tile=8x8 threads=8x2 vw=4 insts=3 "),
-        ("divide_kernel", "fused f32 tile=8x8 threads=8x2 vw=4 insts=5 "),
-        ("compute_ops", "tile_vm f32 insts=5 loads=3 stores=1 lds="),
+        ("unary_and_shape", "staged f32 threads=256 lds=", "tile_vm f32 insts=12 loads=2 stores=3 lds="),
+        ("column_reduce", "fused f32 tile=8x8 threads=8x2 vw=4 insts=3 ", "fused f32 tile=8x8 threads=8x2 vw=4 insts=3 "),
+        ("divide_kernel", "fused f32 tile=8x8 threads=8x2 vw=4 insts=5 ", "fused f32 tile=8x8 threads=8x2 vw=4 insts=5 "),
+        ("compute_ops", "staged f32 threads=256 lds=4864B mfma=i8 insts=5", "tile_vm f32 insts=5 loads=3 stores=1 lds="),
     ],
 )
-def test_general_programs_plan_onto_the_tile_interpreter(name, kernel):
+def test_general_programs_plan_onto_compiled_kernels(monkeypatch, name, kernel, interp):
     """Programs of loads, stores, unary / binary ops and reductions over one
     [R, C] tile and its broadcasts are compiled into a fused kernel; the rest
-    (rank-3 tiles, matmul, transposes) run on the interpreter."""
+    (rank-3 tiles, matmul / mma, transposes) into a staged kernel, or run on
+    the interpreter with XTILE_AMD_STAGE=0."""
     from tests.golden.dsl_programs import programs
     from xtile_amd import dsl
 
     k, args, grid, db = programs(dsl)[name]
     m = xt.convert(k, args=args, grid=grid, double_buffering=db)
     assert xt.plan(m)["kernel"].startswith(kernel)
+    monkeypatch.setenv("XTILE_AMD_STAGE", "0")
+    m = xt.convert(k, args=args, grid=grid, double_buffering=db)
+    assert xt.plan(m)["kernel"].startswith(interp)
+
+
+def test_staged_plans():
+    """The staged kernel's choices: f16 operands as loaded take the f16 MFMA,
+    the f32 probabilities the f32 MFMA; algorithmic bytes count a head's
+    shared K and V tiles once."""
+    m = K.attention(512, 128, 128, 64, 64)
+    p = xt.plan(m)
+    assert p["kernel"].startswith("staged f32 threads=256 lds=") and "mfma=f32,f16" in p["kernel"]
+    q = 512 * 128 * 64 * 2
+    assert p["bytes"] == q + q + 2 * (512 * 128 * 64 * 4)  # Q, K (f16), V, O (f32): each tile once
+    assert p["flops"] == 2 * (2 * 512 * 128 * 128 * 64)
+    m = K.attention(2, 48, 33, 20, 16, qk=xt.float32)
+    assert "mfma=f32 " in xt.plan(m)["kernel"]
 
 
 def test_interpreter_programs_and_lds_budget(monkeypatch):
@@ -181,7 +199,11 @@ def _mm_exp(m, k, n):
     return xt.parse(_MM_EXP.replace("MxK", f"{m}x{k}").replace("KxN", f"{k}x{n}").replace("MxN", f"{m}x{n}"))
 
 
-def test_matmul_outside_the_gemm_forms_runs_on_the_tile_interpreter():
+def test_matmul_outside_the_gemm_forms_runs_compiled(monkeypatch):
+    """A matmul followed by another op: the staged kernel (f16 MFMA on the
+    operands as loaded), or the interpreter with XTILE_AMD_STAGE=0."""
+    assert xt.plan(_mm_exp(64, 64, 64))["kernel"].startswith("staged f32 threads=256 lds=51200B mfma=f16 insts=5")
+    monkeypatch.setenv("XTILE_AMD_STAGE", "0")
     assert xt.plan(_mm_exp(64, 64, 64))["kernel"].startswith("tile_vm f32 insts=5 loads=2 stores=1")
 
 

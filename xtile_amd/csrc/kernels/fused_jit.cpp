@@ -147,7 +147,8 @@ const xt::FusedPlan* scalar_variant(const xt::Plan& p, std::string& err) {
   std::lock_guard<std::mutex> lock(g_scalar_mu);
   if (!fp->scalar) {
     auto sp = std::make_shared<xt::FusedPlan>();
-    if (!xt::fuse_vm(p.vm, p.grid, *sp, err, 1) || !compile_fused(*sp, err)) return nullptr;
+    const bool built = fp->staged ? xt::stage_vm(p.vm, p.grid, *sp, err, 1) : xt::fuse_vm(p.vm, p.grid, *sp, err, 1);
+    if (!built || !compile_fused(*sp, err)) return nullptr;
     fp->scalar = std::move(sp);
   }
   return fp->scalar.get();

@@ -743,7 +743,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       small_int.insert(o->results[0]);
   }
   VmPlan vm;
-  double bytes = 0, once_bytes = 0, flops = 0;
+  double once_bytes = 0, flops = 0;
   for (int i = 0; i < nops; ++i) {
     const Op* o = an.compute[i];
     const std::string& n = o->name;
@@ -773,10 +773,16 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
       in.op = is_load ? VmOp::Load : VmOp::Store;
       in.kind = static_cast<int16_t>(vm.access.size());
       vm.access.push_back(acc);
-      // a tile at the same place in every Block (weights, scalars) moves from HBM once
+      // algorithmic traffic: each distinct tile once.  The tile origin moves
+      // only along the grid axes with a nonzero step (a shared load's leader
+      // rule has already zeroed the axes below k), so Blocks that differ only
+      // along the other axes read the same tile: a tile at the same place in
+      // every Block (weights, scalars) moves from HBM once, a shared=k tile
+      // once per sharing group.
       const double tb = double(ten.numel()) * elem_bytes(mem.elem);
-      if (acc.addr.sx == 0 && acc.addr.sy == 0 && acc.addr.sz == 0) once_bytes += tb;
-      else bytes += tb;
+      const double distinct = (acc.addr.sx ? double(p.grid[0]) : 1.0) * (acc.addr.sy ? double(p.grid[1]) : 1.0) *
+                              (acc.addr.sz ? double(p.grid[2]) : 1.0);
+      once_bytes += tb * distinct;
       if (is_load) {
         auto sl = alloc(static_cast<int>(ten.numel()));
         slot[o->results[0]] = sl;
@@ -879,7 +885,7 @@ bool match_vm(const Analysis& an, Plan& p, std::string& err) {
   p.kind = PlanKind::TileVM;
   p.vm = std::move(vm);
   const double blocks = double(p.grid[0]) * p.grid[1] * p.grid[2];
-  p.algo_bytes = blocks * bytes + once_bytes;
+  p.algo_bytes = once_bytes;
   p.algo_flops = blocks * flops;
   return true;
 }
@@ -1017,17 +1023,25 @@ bool build_plan(const Module& m, const std::string& func, Plan& p, std::string& 
     if (first.empty()) first = why;
   }
   if (match_vm(an, p, err)) {
-    // compiled for itself when it fits the fused layout (XTILE_AMD_FUSE=0 keeps the interpreter)
+    // compiled for itself: the register-resident fused kernel when every
+    // value fits its layout, else the LDS-staged kernel (XTILE_AMD_FUSE=0
+    // keeps the interpreter; XTILE_AMD_STAGE=0 keeps it for what the fused
+    // layout declines)
     const char* env = std::getenv("XTILE_AMD_FUSE");
+    const char* stage_env = std::getenv("XTILE_AMD_STAGE");
+    const bool fuse_off = env && std::string(env) == "0";
     FusedPlan fp;
-    std::string why;
-    if (!(env && std::string(env) == "0") && fuse_vm(p.vm, p.grid, fp, why)) {
+    std::string why, why_staged;
+    if (!fuse_off && (fuse_vm(p.vm, p.grid, fp, why) ||
+                      (!(stage_env && std::string(stage_env) == "0") && stage_vm(p.vm, p.grid, fp, why_staged)))) {
       p.kind = PlanKind::Fused;
       p.fused = std::make_shared<FusedPlan>(std::move(fp));
       p.vm_fallback = vm_fits_interpreter(p.vm, p.vm_fallback_why);
       return true;
     }
-    p.unfused = env && std::string(env) == "0" ? "XTILE_AMD_FUSE=0" : why;
+    if (fuse_off) p.unfused = "XTILE_AMD_FUSE=0";
+    else if (stage_env && std::string(stage_env) == "0") p.unfused = why + "; XTILE_AMD_STAGE=0";
+    else p.unfused = why + "; not staged: " + why_staged;
     if (vm_fits_interpreter(p.vm, err)) return true;
     err += " (not fused: " + p.unfused + ")";
   }

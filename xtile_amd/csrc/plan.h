@@ -107,6 +107,7 @@ struct FusedPlan {
   // the same program with scalar row accesses (vw = 1), built and compiled by
   // the first launch whose buffers are not aligned to the vw-element vectors
   std::shared_ptr<FusedPlan> scalar;
+  bool staged = false;       // written by stage_vm (values in LDS), not fuse_vm
 };
 
 struct Plan {
@@ -147,6 +148,13 @@ struct Plan {
 // Returns false, with `why` set, when the program does not fit.
 // max_vw caps the row vector width (4, 2 or 1 elements)
 bool fuse_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why, int max_vw = 4);
+
+// The staged kernel for a tile-interpreter plan the fused layout declines
+// (staged.cpp): every instruction compiled, values in LDS, matmul / mma on
+// MFMA.  Returns false, with `why` set, when the program does not fit
+// (LDS beyond 160 KB, more than 8 accesses, an exact matmul of values that
+// are not i8 tiles, a load of a memref the program stored to).
+bool stage_vm(const VmPlan& vm, const int32_t grid[3], FusedPlan& out, std::string& why, int max_vw = 4);
 
 // Builds the plan of function `func` (empty name: the only function).
 // Returns false and sets `error` when the program is not one the HIP

@@ -35,9 +35,11 @@ from . import (
     mul as tile_mul,
     reciprocal,
     rsqrt,
+    reshape,
     store,
     sub as tile_sub,
     sum as tile_sum,
+    transpose,
 )
 
 
@@ -289,6 +291,37 @@ def bias_add(rows: int, cols: int, trow: int = 32, tcol: int = 64):
     a = Array(shape=(rows, cols), dtype=float32)
     v = Array(shape=(1, cols), dtype=float32)
     return convert(bias_add_kernel, args=(a, v, a, trow, tcol), grid=(rows // trow, cols // tcol, 1))
+
+
+@kernel
+def attention_kernel(q, k, v, o, tq, d, nk):
+    """softmax(Q K^T) V for one query tile of one head: Q, V and the result
+    are [heads, rows, d], K is [heads, nk, d].  The head's K and V tiles are
+    shared by its query tiles (`shared = 1`); K^T comes from the DSL's rank-3
+    transpose (xtile/dsl.py:426-438); P V multiplies the f32 probabilities by
+    an f32 V, since matmul operands share a dtype (xtile/dsl.py:369-374)."""
+    i = bid(0)
+    h = bid(1)
+    qt = reshape(load(q, index=(h, i, 0), shape=(1, tq, d)), shape=(tq, d))
+    kt = load(k, index=(h, 0, 0), shape=(1, nk, d), shared=1)
+    vt = reshape(load(v, index=(h, 0, 0), shape=(1, nk, d), shared=1), shape=(nk, d))
+    ktt = reshape(transpose(kt), shape=(d, nk))
+    s = matmul(qt, ktt)
+    p = exp(tile_sub(s, tile_max(s, axis=1)))
+    p = tile_mul(p, reciprocal(tile_sum(p, axis=1)))
+    store(o, index=(h, i, 0), tile=reshape(matmul(p, vt), shape=(1, tq, d)))
+
+
+def attention(heads: int, nq: int, nk: int, d: int, tq: int = 64, qk=float16):
+    """Grid (nq / tq, heads, 1).  `qk` is the element type of Q and K (f16,
+    bf16 or f32: their product is f32); V and the result are f32."""
+    if nq % tq:
+        raise ValueError("tq must divide nq")
+    qa = Array(shape=(heads, nq, d), dtype=qk)
+    ka = Array(shape=(heads, nk, d), dtype=qk)
+    va = Array(shape=(heads, nk, d), dtype=float32)
+    oa = Array(shape=(heads, nq, d), dtype=float32)
+    return convert(attention_kernel, args=(qa, ka, va, oa, tq, d, nk), grid=(nq // tq, heads, 1))
 
 
 CONFIGS = {
