@@ -5,34 +5,48 @@
 // launches it like a fused kernel.
 //
 // Execution.  One 256-thread workgroup (four waves) runs one Block.  Values
-// live in LDS as f32, as the interpreter and the oracle hold them; every
-// instruction is straight-line code with its shapes, strides and tile origins
-// as compile-time constants, and a barrier separates an instruction from the
-// next one that reads what it wrote or writes where it read.  A run of loads
-// issues every global read before its first LDS write.
+// live in LDS, as f32 (as the interpreter and the oracle hold them) or, for
+// f16 / bf16 tiles as loaded whose every reader is an MFMA operand, as their
+// 16-bit patterns; every instruction is straight-line code with its shapes,
+// strides and tile origins as compile-time constants, and a barrier separates
+// an instruction from the next one that reads what it wrote or writes where
+// it read.  The global reads of a run of loads are issued together; the LDS
+// write of a load whose first reader comes later waits in registers until
+// that reader (so its LDS is not held meanwhile).
 //   * matmul / mma: 32 x 32 output tiles dealt over the four waves, K in MFMA
 //     steps: v_mfma_f32_32x32x16_f16 / _bf16 when both operands are f16 / bf16
 //     tiles as loaded (or transposed / permuted: the values are then exact in
 //     that type), v_mfma_i32_32x32x32_i8 with exact i32 sums for the
 //     interpreter's exact i8 x i8 products, v_mfma_f32_32x32x2_f32 otherwise;
-//     fragments are read from LDS and converted (exactly) in registers.  The
-//     mma accumulator is added to the finished sum, as the interpreter does.
+//     two accumulators (even and odd steps), a ring of fragment sets read
+//     ahead of the MFMAs.  The mma accumulator is added to the finished sum,
+//     as the interpreter does.  A result whose only reader is a store goes
+//     from the accumulators straight to global memory.
+//   * a transpose / permute whose every reader is a matmul operand is a view:
+//     the matmul reads its source through the permutation.  Other permutes
+//     copy, one thread per output element.
 //   * reductions along a row: a power-of-two group of lanes per row with a
 //     shuffle butterfly; along a column: one thread per column.
-//   * permute / transpose: one thread per output element.
+//   * elementwise ops: every LDS read of a chunk of elements before its
+//     writes, four elements at a time where the layouts allow.
 //
 // LDS layout.  The generator allocates its own slots (liveness, first fit,
 // 16-byte granules): a value of n elements is stored as rows of `krow`
 // elements `pitch` apart in the value's row-major element order, so reshapes
 // keep their meaning.  krow = pitch = the innermost dim, except for
-//   * matmul operands: A[M, K] with krow = K, pitch = K rounded up to 4 mod 8
-//     (f16 / bf16 / i8: the 16-byte fragment reads of sixteen rows fall in
-//     sixteen distinct bank groups) or to 2 mod 4 (f32: 32 rows of single
-//     floats in distinct banks); B[K, N] with krow = N, pitch 4 mod 8 for the
-//     narrow types (the two half-waves' rows, 8 or 16 apart, in distinct banks);
-//   * the source of a permute: an odd pitch (a column read is conflict-free).
+//   * matmul operands: rows that the lanes of a fragment read side by side
+//     (A's rows; the source rows of a transposed view) get a pitch of 4 mod 8
+//     floats or 8 mod 16 halves for the 16-byte reads of the narrow types
+//     (sixteen rows in sixteen distinct bank groups) and 2 mod 4 floats for
+//     f32 (32 rows of single floats in distinct banks); B[K, N] read across
+//     columns gets 4 mod 8 floats / 8 mod 16 halves for the narrow types (the
+//     two half-waves' rows, 8 apart, in distinct banks);
+//   * the source of a copying permute: an odd pitch (a column read is
+//     conflict-free).
 // The first consumer in program order decides.
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <functional>
 #include <map>
 #include <sstream>
@@ -54,11 +68,21 @@ enum VType { kVF32 = 0, kVF16 = 1, kVBF16 = 2, kVI8 = 3 };
 struct Val {
   int def = -1, last = -1;  // producing instruction, last reader
   long long numel = 0;
-  int d2 = 1;               // innermost dim at the definition
-  int krow = 0, pitch = 0;  // layout (0: not chosen yet)
-  int off = -1;             // LDS float offset
+  int dims[3] = {1, 1, 1};  // dims at the definition
+  int krow = 0, pitch = 0;  // layout (0: not chosen yet), in elements
+  int off = -1;             // LDS offset in floats (-1: no storage)
   int vt = kVF32;
-  long long floats() const { return numel / krow * pitch; }
+  bool h16 = false;         // held as 16-bit patterns (pitch and offsets in halves)
+  int src = -1;             // a view: element (j0, j1, j2) is src's element with index perm[d] = j_d
+  int perm[3] = {0, 1, 2};
+  int alloc_at = -1;        // the instruction from which it holds LDS (a deferred load: its first reader)
+  int gstore = -1;          // a matmul result its only reader, this store, takes from the accumulators
+  int alias = -1;           // written in place over this value (an elementwise operand that dies there)
+  std::vector<int> users;   // instructions that read it
+  long long floats() const {
+    const long long e = numel / krow * pitch;
+    return h16 ? (e + 1) / 2 : e;
+  }
 };
 
 struct Reads {
@@ -70,6 +94,13 @@ int pad_to(int k, int mod, int rem) { return k + ((rem - k % mod) % mod + mod) %
 
 std::string S(long long v) { return std::to_string(v); }
 
+// phys index = base + sr * r + sc * c of a matmul operand viewed as [R, C]
+struct Aff {
+  bool ok = false;
+  int store = -1;  // the value holding the data
+  long long base = 0, sr = 0, sc = 0;
+};
+
 class StagedGen {
  public:
   StagedGen(const VmPlan& vm, const int32_t grid[3], int max_vw) : vm_(vm), max_vw_(max_vw) {
@@ -77,47 +108,73 @@ class StagedGen {
   }
 
   bool run(FusedPlan& out, std::string& why) {
-    if (!analyze(why) || !layouts(why) || !allocate(why)) return false;
+    if (!analyze(why) || !views() || !layouts(why) || !plan_loads() || !allocate(why)) return false;
+    if (std::getenv("XTILE_AMD_STAGE_DUMP"))
+      for (size_t v = 0; v < vals_.size(); ++v) {
+        const Val& w = vals_[v];
+        std::fprintf(stderr, "v%zu def=%d last=%d alloc=%d dims=%dx%dx%d krow=%d pitch=%d off=%d h16=%d src=%d alias=%d gstore=%d\n",
+                     v, w.def, w.last, w.alloc_at, w.dims[0], w.dims[1], w.dims[2], w.krow, w.pitch, w.off, (int)w.h16,
+                     w.src, w.alias, w.gstore);
+      }
     std::ostringstream b;
-    const size_t n = vm_.inst.size();
-    size_t i = 0;
+    const int n = static_cast<int>(vm_.inst.size());
     bool any_mm[4] = {false, false, false, false};
+    int prev = -1;  // the last instruction that emitted code
+    int i = 0;
+    auto barrier_before = [&](int next) {
+      if (prev < 0) return;
+      if (vm_.inst[prev].op == VmOp::Store && vm_.inst[next].op == VmOp::Store) return;
+      b << "  __syncthreads();\n";
+    };
     while (i < n) {
       const VmInst& in = vm_.inst[i];
       if (in.op == VmOp::Load) {
-        // a run of loads: every global read, then every LDS write
-        size_t j = i;
-        int regs = 0;
+        // a run of loads: every global read, then the LDS writes that are not deferred
+        int j = i, regs = 0;
         while (j < n && vm_.inst[j].op == VmOp::Load) {
-          const int r = load_regs(static_cast<int>(j));
-          if (j > i && regs + r > 128) break;
+          const int r = load_regs(j);
+          if (j > i && regs + r > 160) break;
           regs += r;
           ++j;
         }
-        for (size_t k = i; k < j; ++k) emit_load_read(b, static_cast<int>(k));
-        for (size_t k = i; k < j; ++k) emit_load_write(b, static_cast<int>(k));
+        barrier_before(i);
+        for (int k = i; k < j; ++k) emit_load_read(b, k);
+        for (int k = i; k < j; ++k)
+          if (!deferred(k)) emit_load_write(b, k);
+        prev = j - 1;
         i = j;
-      } else {
-        switch (in.op) {
-          case VmOp::Store: emit_store(b, static_cast<int>(i)); break;
-          case VmOp::Unary:
-          case VmOp::Binary: emit_elementwise(b, static_cast<int>(i)); break;
-          case VmOp::Reduce: emit_reduce(b, static_cast<int>(i)); break;
-          case VmOp::Permute: emit_permute(b, static_cast<int>(i)); break;
-          case VmOp::Matmul:
-            emit_matmul(b, static_cast<int>(i));
-            any_mm[rd_[i].mode] = true;
-            break;
-          default: why = "staged kernels take the interpreter's instructions"; return false;
-        }
+        continue;
+      }
+      const Reads& r = rd_[i];
+      const bool silent = (in.op == VmOp::Permute && vals_[r.dst].src >= 0) ||
+                          (in.op == VmOp::Store && vals_[r.a].gstore == i);
+      if (silent) {
         ++i;
+        continue;
       }
-      if (i < n) {
-        // stores only read LDS and loads write distinct live slots: no
-        // barrier between two of a kind
-        const VmOp prev = vm_.inst[i - 1].op, next = vm_.inst[i].op;
-        if (!((prev == VmOp::Store && next == VmOp::Store))) b << "  __syncthreads();\n";
+      barrier_before(i);
+      // deferred loads whose first reader this is: their LDS write, then a barrier
+      bool wrote = false;
+      for (int k = 0; k < i; ++k)
+        if (vm_.inst[k].op == VmOp::Load && deferred(k) && vals_[rd_[k].dst].alloc_at == i) {
+          emit_load_write(b, k);
+          wrote = true;
+        }
+      if (wrote) b << "  __syncthreads();\n";
+      switch (in.op) {
+        case VmOp::Store: emit_store(b, i); break;
+        case VmOp::Unary:
+        case VmOp::Binary: emit_elementwise(b, i); break;
+        case VmOp::Reduce: emit_reduce(b, i); break;
+        case VmOp::Permute: emit_permute(b, i); break;
+        case VmOp::Matmul:
+          emit_matmul(b, i);
+          any_mm[r.mode] = true;
+          break;
+        default: why = "staged kernels take the interpreter's instructions"; return false;
       }
+      prev = i;
+      ++i;
     }
     std::ostringstream k;
     k << "typedef float xf16v __attribute__((ext_vector_type(16)));\n"
@@ -129,6 +186,7 @@ class StagedGen {
     k << "extern \"C\" __global__ void __launch_bounds__(" << kThreads << ") xt_fused(FusedArgs a) {\n"
       << "#pragma clang fp contract(off)\n"
       << "  __shared__ __attribute__((aligned(16))) float S[" << std::max(4LL, high_) << "];\n"
+      << "  unsigned short* const H = reinterpret_cast<unsigned short*>(S);\n  (void)H;\n"
       << "  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);\n"
       << "  (void)lane; (void)wave;\n"
       << "  const int bid = blockIdx.x;\n"
@@ -167,11 +225,11 @@ class StagedGen {
     return false;
   }
 
-  int new_val(int def, long long numel, int d2, int vt) {
+  int new_val(int def, const int d[3], int vt) {
     Val v;
-    v.def = v.last = def;
-    v.numel = numel;
-    v.d2 = d2;
+    v.def = v.last = v.alloc_at = def;
+    for (int k = 0; k < 3; ++k) v.dims[k] = d[k];
+    v.numel = (long long)d[0] * d[1] * d[2];
     v.vt = vt;
     vals_.push_back(v);
     return static_cast<int>(vals_.size()) - 1;
@@ -190,13 +248,14 @@ class StagedGen {
         if (it == cur.end()) return false;
         out = it->second;
         vals_[out].last = static_cast<int>(i);
+        vals_[out].users.push_back(static_cast<int>(i));
         return true;
       };
       switch (in.op) {
         case VmOp::Load: {
           const Elem e = vm_.access[in.kind].elem;
           const int vt = e == Elem::F16 ? kVF16 : e == Elem::BF16 ? kVBF16 : e == Elem::I8 ? kVI8 : kVF32;
-          r.dst = new_val(static_cast<int>(i), prod(in.dims), in.dims[2], vt);
+          r.dst = new_val(static_cast<int>(i), in.dims, vt);
           break;
         }
         case VmOp::Store:
@@ -204,24 +263,26 @@ class StagedGen {
           break;
         case VmOp::Unary:
           if (!rd(in.a, r.a)) return fail(why, "unary op of an unknown value");
-          r.dst = new_val(static_cast<int>(i), prod(in.dims), in.dims[2],
-                          in.kind == static_cast<int16_t>(VmUnary::Ftoi) ? kVI8 : kVF32);
+          r.dst = new_val(static_cast<int>(i), in.dims, in.kind == static_cast<int16_t>(VmUnary::Ftoi) ? kVI8 : kVF32);
           break;
         case VmOp::Binary:
           if (!rd(in.a, r.a) || !rd(in.b, r.b)) return fail(why, "binary op of an unknown value");
-          r.dst = new_val(static_cast<int>(i), prod(in.dims), in.dims[2], kVF32);
+          r.dst = new_val(static_cast<int>(i), in.dims, kVF32);
           break;
         case VmOp::Reduce: {
           if (!rd(in.a, r.a)) return fail(why, "reduction of an unknown value");
           if (in.dims[0] != 1) return fail(why, "reductions take rank-2 tiles");
           const bool rows = in.aux[0] == 1;
-          r.dst = new_val(static_cast<int>(i), rows ? in.dims[1] : in.dims[2], rows ? 1 : in.dims[2], kVF32);
+          const int d[3] = {1, rows ? in.dims[1] : 1, rows ? 1 : in.dims[2]};
+          r.dst = new_val(static_cast<int>(i), d, kVF32);
           break;
         }
-        case VmOp::Permute:
+        case VmOp::Permute: {
           if (!rd(in.a, r.a)) return fail(why, "permute of an unknown value");
-          r.dst = new_val(static_cast<int>(i), prod(in.dims), in.dims[in.aux[2]], vals_[r.a].vt);
+          const int d[3] = {in.dims[in.aux[0]], in.dims[in.aux[1]], in.dims[in.aux[2]]};
+          r.dst = new_val(static_cast<int>(i), d, vals_[r.a].vt);
           break;
+        }
         case VmOp::Matmul: {
           if (!rd(in.a, r.a) || !rd(in.b, r.b) || (in.c >= 0 && !rd(in.c, r.c)))
             return fail(why, "matmul of an unknown value");
@@ -236,7 +297,8 @@ class StagedGen {
           } else {
             r.mode = kMmF32;
           }
-          r.dst = new_val(static_cast<int>(i), (long long)in.dims[1] * in.dims[2], in.dims[2], kVF32);
+          const int d[3] = {1, in.dims[1], in.dims[2]};
+          r.dst = new_val(static_cast<int>(i), d, kVF32);
           break;
         }
       }
@@ -245,22 +307,82 @@ class StagedGen {
     return true;
   }
 
+  bool is_operand(int inst, int v) const {
+    const VmInst& in = vm_.inst[inst];
+    return in.op == VmOp::Matmul && (rd_[inst].a == v || rd_[inst].b == v) && rd_[inst].c != v;
+  }
+
+  // Permutes read only by matmul operands become views of their source;
+  // matmul results read only by one store go to global memory directly.
+  bool views() {
+    for (size_t i = 0; i < vm_.inst.size(); ++i) {
+      const VmInst& in = vm_.inst[i];
+      const Reads& r = rd_[i];
+      if (in.op == VmOp::Permute) {
+        Val& X = vals_[r.dst];
+        if (X.users.empty() || vals_[r.a].src >= 0) continue;
+        bool all = true;
+        for (int u : X.users) all = all && is_operand(u, r.dst);
+        if (!all) continue;
+        X.src = r.a;
+        for (int d = 0; d < 3; ++d) X.perm[d] = in.aux[d];
+        Val& Y = vals_[r.a];
+        Y.users.erase(std::remove(Y.users.begin(), Y.users.end(), static_cast<int>(i)), Y.users.end());
+        for (int u : X.users) Y.users.push_back(u);
+        Y.last = Y.users.empty() ? Y.def : *std::max_element(Y.users.begin(), Y.users.end());
+      } else if (in.op == VmOp::Matmul) {
+        Val& D = vals_[r.dst];
+        if (D.users.size() == 1 && vm_.inst[D.users[0]].op == VmOp::Store) D.gstore = D.users[0];
+      }
+    }
+    return true;
+  }
+
+  // the value holding v's data (v itself, or a view's source)
+  int storage_of(int v) const { return vals_[v].src >= 0 ? vals_[v].src : v; }
+
   bool layouts(std::string& why) {
+    // 16-bit storage: f16 / bf16 loads read only as operands of f16 / bf16 MFMAs
+    for (size_t i = 0; i < vm_.inst.size(); ++i)
+      if (vm_.inst[i].op == VmOp::Load) {
+        Val& v = vals_[rd_[i].dst];
+        if ((v.vt != kVF16 && v.vt != kVBF16) || v.users.empty()) continue;
+        bool all = true;
+        for (int u : v.users) {
+          const int m = rd_[u].mode;
+          all = all && vm_.inst[u].op == VmOp::Matmul && (m == kMmF16 || m == kMmBF16) &&
+                (storage_of(rd_[u].a) == rd_[i].dst || storage_of(rd_[u].b) == rd_[i].dst) &&
+                rd_[u].c != rd_[i].dst;
+        }
+        v.h16 = all;
+      }
     for (size_t i = 0; i < vm_.inst.size(); ++i) {
       const VmInst& in = vm_.inst[i];
       const Reads& r = rd_[i];
       if (in.op == VmOp::Matmul) {
-        const int K = in.aux[0], N = in.dims[2];
-        Val &A = vals_[r.a], &B = vals_[r.b];
-        if (!A.krow) {
-          A.krow = K;
-          A.pitch = r.mode == kMmF32 ? pad_to(K, 4, 2) : pad_to(K, 8, 4);
+        const int M = in.dims[1], K = in.aux[0], N = in.dims[2];
+        for (int side = 0; side < 2; ++side) {
+          const int vid = side == 0 ? r.a : r.b;
+          Val& st = vals_[storage_of(vid)];
+          if (st.krow) continue;
+          // which storage row the fragment's lanes walk: A's rows (lanes = M),
+          // B's columns (lanes = N); through a view, the permuted dim
+          bool lanes_on_rows;
+          if (vals_[vid].src < 0) {
+            lanes_on_rows = side == 0;
+            st.krow = side == 0 ? K : N;
+          } else {
+            const Val& X = vals_[vid];
+            // the view's dim that the lanes walk: dim 1 (rows) for A, dim 2 for B
+            lanes_on_rows = X.perm[side == 0 ? 1 : 2] == 1;
+            st.krow = st.dims[2];
+          }
+          (void)M;
+          if (st.h16) st.pitch = pad_to(st.krow, 16, 8);
+          else if (r.mode == kMmF32) st.pitch = lanes_on_rows ? pad_to(st.krow, 4, 2) : st.krow;
+          else st.pitch = pad_to(st.krow, 8, 4);
         }
-        if (!B.krow) {
-          B.krow = N;
-          B.pitch = r.mode == kMmF32 ? N : pad_to(N, 8, 4);
-        }
-      } else if (in.op == VmOp::Permute) {
+      } else if (in.op == VmOp::Permute && vals_[r.dst].src < 0) {
         Val& src = vals_[r.a];
         if (!src.krow) {
           src.krow = in.dims[2];
@@ -268,67 +390,211 @@ class StagedGen {
         }
       }
     }
+    coalesce();
     for (Val& v : vals_) {
-      if (!v.krow) v.krow = v.pitch = std::max(1, v.d2);
+      if (v.alias >= 0) continue;
+      if (!v.krow) v.krow = v.pitch = std::max(1, v.dims[2]);
       if (v.numel % v.krow) return fail(why, "staged layout rows do not divide a value");
+    }
+    for (Val& v : vals_)
+      if (v.alias >= 0) {
+        const Val& root = vals_[root_of(static_cast<int>(&v - &vals_[0]))];
+        v.krow = root.krow;
+        v.pitch = root.pitch;
+      }
+    return true;
+  }
+
+  int root_of(int v) const {
+    while (vals_[v].alias >= 0) v = vals_[v].alias;
+    return v;
+  }
+
+  // An elementwise result whose same-shaped operand is last read by that
+  // instruction is written in place over it: each thread reads the elements
+  // it then writes, at the same indices, and no other thread touches them.
+  // The chain of such values shares one slot and one layout (the operand
+  // layouts already chosen for any member, which must agree).
+  void coalesce() {
+    for (size_t i = 0; i < vm_.inst.size(); ++i) {
+      const VmInst& in = vm_.inst[i];
+      if (in.op != VmOp::Unary && in.op != VmOp::Binary) continue;
+      const Reads& r = rd_[i];
+      Val& D = vals_[r.dst];
+      if (D.gstore >= 0 || D.src >= 0) continue;
+      for (int side = 0; side < (in.op == VmOp::Binary ? 2 : 1); ++side) {
+        const int xv = side == 0 ? r.a : r.b;
+        const int* od = in.op == VmOp::Unary ? in.dims : side == 0 ? in.lhs : in.aux;
+        if (od[0] != in.dims[0] || od[1] != in.dims[1] || od[2] != in.dims[2]) continue;  // broadcast
+        Val& X = vals_[xv];
+        if (X.src >= 0 || X.h16 || X.gstore >= 0 || X.last != static_cast<int>(i) || X.numel != D.numel) continue;
+        if (in.op == VmOp::Binary && r.a == r.b) continue;
+        // the chain's layout: X's root's, or D's, whichever is set; both set must agree
+        const int root = root_of(xv);
+        const Val& R = vals_[root];
+        if (R.krow && D.krow && (R.krow != D.krow || R.pitch != D.pitch)) continue;
+        bool member_has = false;  // another member of X's chain carries a layout
+        for (size_t w = 0; w < vals_.size(); ++w)
+          if (vals_[w].alias >= 0 && root_of(static_cast<int>(w)) == root && vals_[w].krow &&
+              D.krow && (vals_[w].krow != D.krow || vals_[w].pitch != D.pitch))
+            member_has = true;
+        if (member_has) continue;
+        if (!vals_[root].krow && D.krow) {
+          vals_[root].krow = D.krow;
+          vals_[root].pitch = D.pitch;
+        }
+        D.alias = xv;
+        break;
+      }
+    }
+  }
+
+  bool deferred(int load_inst) const {
+    const Val& v = vals_[rd_[load_inst].dst];
+    return v.alloc_at > load_inst;
+  }
+
+  // A load whose first reader is not the first instruction to run after its
+  // run of loads keeps its data in registers until that reader.
+  bool plan_loads() {
+    const int n = static_cast<int>(vm_.inst.size());
+    for (int i = 0; i < n; ++i) {
+      if (vm_.inst[i].op != VmOp::Load) continue;
+      Val& v = vals_[rd_[i].dst];
+      int end = i;
+      while (end + 1 < n && vm_.inst[end + 1].op == VmOp::Load) ++end;
+      // the first instruction after the run that emits code
+      int next = end + 1;
+      while (next < n && silent(next)) ++next;
+      if (v.users.empty()) {
+        // never read: its slot stays reserved until the run's writes are ordered
+        v.last = std::min(n - 1, end + 1);
+        continue;
+      }
+      const int first = *std::min_element(v.users.begin(), v.users.end());
+      if (first > next) v.alloc_at = first;
     }
     return true;
   }
 
+  bool silent(int i) const {
+    const VmInst& in = vm_.inst[i];
+    const Reads& r = rd_[i];
+    return (in.op == VmOp::Permute && vals_[r.dst].src >= 0) || (in.op == VmOp::Store && vals_[r.a].gstore == i);
+  }
+
   bool allocate(std::string& why) {
-    // a load whose value is never read keeps its slot until the run of loads
-    // it belongs to has ended: the run's LDS writes are not ordered among
-    // themselves
     const int n = static_cast<int>(vm_.inst.size());
-    for (Val& v : vals_)
-      if (v.last == v.def && vm_.inst[v.def].op == VmOp::Load) {
-        int e = v.def;
-        while (e + 1 < n && vm_.inst[e + 1].op == VmOp::Load) ++e;
-        v.last = std::min(n - 1, e + 1);
+    // a chain of in-place values holds its root's slot until its last member's last read
+    for (size_t v = 0; v < vals_.size(); ++v)
+      if (vals_[v].alias >= 0) {
+        Val& root = vals_[root_of(static_cast<int>(v))];
+        root.last = std::max(root.last, vals_[v].last);
       }
-    std::vector<std::pair<long long, long long>> used;  // (offset, floats) of live values
-    std::vector<int> at_def(vm_.inst.size(), -1);
-    for (size_t v = 0; v < vals_.size(); ++v) at_def[vals_[v].def] = static_cast<int>(v);
-    for (size_t i = 0; i < vm_.inst.size(); ++i) {
-      const int v = at_def[i];
-      if (v >= 0) {
-        const long long fl = (vals_[v].floats() + 3) & ~3LL;
-        long long at = 0;
-        for (bool clash = true; clash;) {
-          clash = false;
-          for (auto& u : used)
-            if (at < u.first + u.second && u.first < at + fl) {
-              at = (u.first + u.second + 3) & ~3LL;
-              clash = true;
-            }
-        }
-        used.push_back({at, fl});
-        vals_[v].off = static_cast<int>(at);
-        high_ = std::max(high_, at + fl);
-      }
-      // values whose last use is this instruction (their slot is reused from the next one on)
-      for (size_t w = 0; w < vals_.size(); ++w)
-        if (vals_[w].last == static_cast<int>(i) && vals_[w].off >= 0)
-          for (size_t k = 0; k < used.size(); ++k)
-            if (used[k].first == vals_[w].off) {
-              used.erase(used.begin() + k);
-              break;
-            }
+    // Every slot's life [alloc_at, last] is known, so two packings are
+    // tried and the smaller kept: first fit in program order, and largest
+    // first at the lowest offset clear of every placed slot whose life
+    // overlaps (first fit leaves holes that a later, larger slot cannot use).
+    std::vector<int> items;
+    for (size_t v = 0; v < vals_.size(); ++v) {
+      const Val& w = vals_[v];
+      if (w.src < 0 && w.gstore < 0 && w.alias < 0 && w.alloc_at >= 0 && w.alloc_at < n) items.push_back(static_cast<int>(v));
     }
+    auto size_of = [&](int v) { return (vals_[v].floats() + 3) & ~3LL; };
+    auto overlap = [&](int a, int b) { return vals_[a].alloc_at <= vals_[b].last && vals_[b].alloc_at <= vals_[a].last; };
+    auto pack = [&](std::vector<int> order, std::vector<long long>& off) {
+      off.assign(vals_.size(), -1);
+      long long high = 0;
+      std::vector<int> placed;
+      for (int v : order) {
+        const long long fl = size_of(v);
+        std::vector<long long> cand = {0};
+        for (int p : placed) cand.push_back(off[p] + size_of(p));
+        std::sort(cand.begin(), cand.end());
+        for (long long at : cand) {
+          bool clash = false;
+          for (int p : placed)
+            if (overlap(v, p) && at < off[p] + size_of(p) && off[p] < at + fl) clash = true;
+          if (!clash) {
+            off[v] = at;
+            break;
+          }
+        }
+        placed.push_back(v);
+        high = std::max(high, off[v] + fl);
+      }
+      return high;
+    };
+    std::vector<int> by_time = items, by_size = items;
+    std::stable_sort(by_time.begin(), by_time.end(), [&](int a, int b) { return vals_[a].alloc_at < vals_[b].alloc_at; });
+    std::stable_sort(by_size.begin(), by_size.end(), [&](int a, int b) {
+      return size_of(a) != size_of(b) ? size_of(a) > size_of(b) : vals_[a].alloc_at < vals_[b].alloc_at;
+    });
+    std::vector<long long> off_t, off_s;
+    const long long high_t = pack(by_time, off_t), high_s = pack(by_size, off_s);
+    const std::vector<long long>& off = high_s < high_t ? off_s : off_t;
+    high_ = std::min(high_t, high_s);
+    for (int v : items) vals_[v].off = static_cast<int>(off[v]);
+    for (size_t v = 0; v < vals_.size(); ++v)
+      if (vals_[v].alias >= 0) vals_[v].off = vals_[root_of(static_cast<int>(v))].off;
     if (high_ > kMaxLdsFloats)
       return fail(why, "staged kernel needs " + S((high_ * 4 + 1023) / 1024) + " KB of LDS (at most 160 KB)");
     return true;
   }
 
-  // LDS float index of logical element `lin` of value v
+  // LDS index (floats, or halves for 16-bit values) of logical element `lin` of a stored value
   std::string phys(const Val& v, const std::string& lin) const {
-    if (v.krow == v.pitch) return "(" + S(v.off) + " + (" + lin + "))";
-    return "(" + S(v.off) + " + (" + lin + ") / " + S(v.krow) + " * " + S(v.pitch) + " + (" + lin + ") % " +
+    const long long base = v.h16 ? 2LL * v.off : v.off;
+    if (v.krow == v.pitch) return "(" + S(base) + " + (" + lin + "))";
+    return "(" + S(base) + " + (" + lin + ") / " + S(v.krow) + " * " + S(v.pitch) + " + (" + lin + ") % " +
            S(v.krow) + ")";
   }
 
-  // four consecutive elements from a multiple of 4 stay contiguous and aligned
-  static bool vec4(const Val& v) { return v.krow % 4 == 0 && v.pitch % 4 == 0 && v.off % 4 == 0; }
+  // the f32 value of element `lin` of value v (through a view, from its source)
+  std::string elem(int vid, const std::string& lin) const {
+    const Val& v = vals_[vid];
+    if (v.src >= 0) {
+      const Val& y = vals_[v.src];
+      // lin -> (j0, j1, j2) in v.dims; source index iv[perm[d]] = j_d
+      const std::string j[3] = {"((" + lin + ") / " + S((long long)v.dims[1] * v.dims[2]) + ")",
+                                "(((" + lin + ") / " + S(v.dims[2]) + ") % " + S(v.dims[1]) + ")",
+                                "((" + lin + ") % " + S(v.dims[2]) + ")"};
+      std::string iv[3];
+      for (int d = 0; d < 3; ++d) iv[v.perm[d]] = j[d];
+      return elem(v.src, "(" + iv[0] + " * " + S(y.dims[1]) + " + " + iv[1] + ") * " + S(y.dims[2]) + " + " + iv[2]);
+    }
+    if (v.h16)
+      return v.vt == kVBF16 ? "xbf(H[" + phys(v, lin) + "])"
+                            : "(float)__builtin_bit_cast(_Float16, H[" + phys(v, lin) + "])";
+    return "S[" + phys(v, lin) + "]";
+  }
+
+  // element (r, c) of operand vid viewed as [R, C], as an affine LDS index
+  Aff affine(int vid, int R, int C) const {
+    Aff f;
+    const Val& v = vals_[vid];
+    if (v.src < 0) {
+      if (v.krow != C) return f;
+      f.ok = true;
+      f.store = vid;
+      f.base = v.h16 ? 2LL * v.off : v.off;
+      f.sr = v.pitch;
+      f.sc = 1;
+      return f;
+    }
+    const Val& y = vals_[v.src];
+    if (v.dims[0] != 1 || v.dims[1] != R || v.dims[2] != C || y.krow != y.dims[2]) return f;
+    const long long st[3] = {(long long)y.dims[1] * y.pitch, y.pitch, 1};
+    f.ok = true;
+    f.store = v.src;
+    f.base = y.h16 ? 2LL * y.off : y.off;
+    f.sr = st[v.perm[1]];
+    f.sc = st[v.perm[2]];
+    return f;
+  }
+
+  // four consecutive f32 elements from a multiple of 4 stay contiguous and aligned
+  static bool vec4(const Val& v) { return !v.h16 && v.krow % 4 == 0 && v.pitch % 4 == 0 && v.off % 4 == 0; }
 
   std::string origin(const TileAddr& o) const {
     std::ostringstream s;
@@ -372,25 +638,25 @@ class StagedGen {
   // with one wave per SIMD every group then waits out the LDS latency.)
   // `regs` floats a group; `read` / `write` emit a group's code given e,
   // i0, i1, i2 and j.
+  long long chunk(long long n, int vw, int regs) const {
+    const long long iters = (n / vw + kThreads - 1) / kThreads;
+    return std::max(1LL, std::min(iters, (long long)(64 / std::max(1, regs))));
+  }
   void two_phase(std::ostringstream& b, long long n, int vw, const int d[3], int regs,
-                 const std::function<void(std::ostringstream&)>& decl,
                  const std::function<void(std::ostringstream&)>& read,
-                 const std::function<void(std::ostringstream&)>& write, int& CH) const {
+                 const std::function<void(std::ostringstream&)>& write) const {
     const long long groups = n / vw, iters = (groups + kThreads - 1) / kThreads;
-    CH = static_cast<int>(std::max(1LL, std::min(iters, (long long)(64 / std::max(1, regs)))));
-    decl(b);
+    const long long CH = chunk(n, vw, regs);
     const long long chunks = (iters + CH - 1) / CH;
-    auto guard = [&]() {
-      std::string g;
-      if (iters % CH) g = "q < " + S(iters);
-      if (groups % kThreads) g += std::string(g.empty() ? "" : " && ") + "e < " + S(n);
-      return g.empty() ? std::string("true") : g;
-    };
+    std::string g;
+    if (iters % CH) g = "q < " + S(iters);
+    if (groups % kThreads) g += std::string(g.empty() ? "" : " && ") + "e < " + S(n);
+    if (g.empty()) g = "true";
     b << "#pragma unroll " << (chunks <= 4 ? chunks : 1) << "\n  for (int q0 = 0; q0 < " << iters << "; q0 += " << CH
       << ") {\n";
     for (int phase = 0; phase < 2; ++phase) {
       b << "#pragma unroll\n    for (int j = 0; j < " << CH << "; ++j) {\n      const int q = q0 + j;\n"
-        << "      const int e = (t + q * " << kThreads << ") * " << vw << ";\n      if (" << guard() << ") {\n"
+        << "      const int e = (t + q * " << kThreads << ") * " << vw << ";\n      if (" << g << ") {\n"
         << "      const int i2 = e % " << d[2] << ", i1 = (e / " << d[2] << ") % " << d[1] << ", i0 = e / "
         << (long long)d[1] * d[2] << ";\n      (void)i0; (void)i1; (void)i2;\n";
       (phase == 0 ? read : write)(b);
@@ -424,28 +690,35 @@ class StagedGen {
     return o.sx != 0 || o.sy != 0 || o.sz != 0;
   }
 
+  // global reads of load i into registers r<i>: f32 values, or the 16-bit
+  // patterns of a value held as 16 bits
   void emit_load_read(std::ostringstream& b, int i) {
     const VmInst& in = vm_.inst[i];
     const VmAccess& acc = vm_.access[in.kind];
+    const bool h16 = vals_[rd_[i].dst].h16;
     const int w = gvw(in);
     gvw_max_ = std::max(gvw_max_, w);
     const long long n = prod(in.dims);
     const long long iters = (n / w + kThreads - 1) / kThreads;
     const std::string R = "r" + S(i);
     b << "  // load " << i << ": [" << in.dims[0] << "," << in.dims[1] << "," << in.dims[2] << "] of a.p["
-      << in.kind << "]\n";
-    b << "  float " << R << "[" << iters * w << "];\n  {\n    const long long org = " << origin(acc.addr) << ";\n";
+      << in.kind << "]" << (h16 ? ", held as 16 bits" : "") << (deferred(i) ? ", written to LDS at its first reader" : "")
+      << "\n";
+    b << "  " << (h16 ? "unsigned short " : "float ") << R << "[" << iters * w << "];\n  {\n    const long long org = "
+      << origin(acc.addr) << ";\n";
     loop_open(b, n, w, in.dims);
     b << "    const long long off = org + (long long)i0 * " << acc.stride[0] << "LL + (long long)i1 * "
       << acc.stride[1] << "LL + (long long)i2 * " << acc.stride[2] << "LL;\n";
-    const char* ty = gtype(acc.elem, w);
+    const Elem le = h16 ? Elem::BF16 : acc.elem;  // 16-bit patterns load as unsigned short vectors
+    const char* ty = gtype(le, w);
     b << "    const " << ty << " qv = " << (streamed(in.kind) ? "__builtin_nontemporal_load(" : "*(")
-      << "reinterpret_cast<const " << ty << "*>(static_cast<const " << gbase(acc.elem) << "*>(a.p[" << in.kind
+      << "reinterpret_cast<const " << ty << "*>(static_cast<const " << gbase(le) << "*>(a.p[" << in.kind
       << "]) + off));\n";
-    if (w == 1) b << "    " << R << "[q] = " << to_f32(acc.elem, "qv") << ";\n";
+    const std::string conv = h16 ? "qv" : "";
+    if (w == 1) b << "    " << R << "[q] = " << (h16 ? "qv" : to_f32(acc.elem, "qv")) << ";\n";
     else
       b << "#pragma unroll\n    for (int c = 0; c < " << w << "; ++c) " << R << "[q * " << w << " + c] = "
-        << to_f32(acc.elem, "qv[c]") << ";\n";
+        << (h16 ? "qv[c]" : to_f32(acc.elem, "qv[c]")) << ";\n";
     loop_close(b);
     b << "  }\n";
   }
@@ -461,17 +734,30 @@ class StagedGen {
     if (w == 4 && vec4(v))
       b << "    *reinterpret_cast<xf4*>(&S[" << phys(v, "e") << "]) = xf4{" << R << "[q * 4], " << R
         << "[q * 4 + 1], " << R << "[q * 4 + 2], " << R << "[q * 4 + 3]};\n";
+    else if (w == 4 && v.h16 && v.krow % 4 == 0 && v.pitch % 4 == 0)
+      b << "    *reinterpret_cast<xu4*>(&H[" << phys(v, "e") << "]) = xu4{" << R << "[q * 4], " << R
+        << "[q * 4 + 1], " << R << "[q * 4 + 2], " << R << "[q * 4 + 3]};\n";
     else
-      b << "#pragma unroll\n    for (int c = 0; c < " << w << "; ++c) S[" << phys(v, "e + c") << "] = " << R
-        << "[q * " << w << " + c];\n";
+      b << "#pragma unroll\n    for (int c = 0; c < " << w << "; ++c) " << (v.h16 ? "H[" : "S[") << phys(v, "e + c")
+        << "] = " << R << "[q * " << w << " + c];\n";
     loop_close(b);
     b << "  }\n";
+  }
+
+  static std::string store_conv(Elem e, const std::string& f) {
+    switch (e) {
+      case Elem::F32: return f;
+      case Elem::F16: return "xto_f16(" + f + ")";
+      case Elem::BF16: return "xto_bf16(" + f + ")";
+      default: return "(signed char)xto_i8(" + f + ")";
+    }
   }
 
   void emit_store(std::ostringstream& b, int i) {
     const VmInst& in = vm_.inst[i];
     const VmAccess& acc = vm_.access[in.kind];
-    const Val& v = vals_[rd_[i].a];
+    const int vid = rd_[i].a;
+    const Val& v = vals_[vid];
     const int w = gvw(in);
     gvw_max_ = std::max(gvw_max_, w);
     const long long n = prod(in.dims);
@@ -480,18 +766,13 @@ class StagedGen {
     loop_open(b, n, w, in.dims);
     b << "    const long long off = org + (long long)i0 * " << acc.stride[0] << "LL + (long long)i1 * "
       << acc.stride[1] << "LL + (long long)i2 * " << acc.stride[2] << "LL;\n";
-    if (w == 4 && vec4(v)) b << "    const xf4 f = *reinterpret_cast<const xf4*>(&S[" << phys(v, "e") << "]);\n";
+    if (w == 4 && v.src < 0 && vec4(v))
+      b << "    const xf4 f = *reinterpret_cast<const xf4*>(&S[" << phys(v, "e") << "]);\n";
     else {
       b << "    float f[" << w << "];\n";
-      b << "#pragma unroll\n    for (int c = 0; c < " << w << "; ++c) f[c] = S[" << phys(v, "e + c") << "];\n";
+      b << "#pragma unroll\n    for (int c = 0; c < " << w << "; ++c) f[c] = " << elem(vid, "e + c") << ";\n";
     }
-    std::string conv;
-    switch (acc.elem) {
-      case Elem::F32: conv = "f[c]"; break;
-      case Elem::F16: conv = "xto_f16(f[c])"; break;
-      case Elem::BF16: conv = "xto_bf16(f[c])"; break;
-      default: conv = "(signed char)xto_i8(f[c])"; break;
-    }
+    const std::string conv = store_conv(acc.elem, "f[c]");
     const char* base = acc.elem == Elem::F32 ? "float" : acc.elem == Elem::I8 ? "signed char" : "unsigned short";
     const char* ty = acc.elem == Elem::F32 ? gtype(Elem::F32, w) : acc.elem == Elem::I8 ? gtype(Elem::I8, w)
                                                                                           : gtype(Elem::BF16, w);
@@ -532,20 +813,19 @@ class StagedGen {
       }
     // four elements at a time when every operand that varies along the
     // innermost dim is contiguous there
-    bool v4 = in.dims[2] % 4 == 0 && n % 4 == 0 && vec4(D) && (ad[2] == 1 || vec4(A)) &&
-              (!bin || bd[2] == 1 || vec4(*B));
+    const bool v4 = in.dims[2] % 4 == 0 && n % 4 == 0 && vec4(D) && (ad[2] == 1 || (A.src < 0 && vec4(A))) &&
+                    (!bin || bd[2] == 1 || (B->src < 0 && vec4(*B)));
     const int w = v4 ? 4 : 1;
     const char* ty = w == 4 ? "xf4" : "float";
     b << "  // " << (bin ? "binary " : "unary ") << i << "\n  {\n";
-    int CH = 1;
-    auto operand = [&](std::ostringstream& o, const Val& v, const int od[3], const std::string& name) {
+    auto operand = [&](std::ostringstream& o, int vid, const int od[3], const std::string& name) {
       const std::string lin = bcast(od);
       if (w == 4 && od[2] != 1)
-        o << "      " << name << "[j] = *reinterpret_cast<const xf4*>(&S[" << phys(v, lin) << "]);\n";
+        o << "      " << name << "[j] = *reinterpret_cast<const xf4*>(&S[" << phys(vals_[vid], lin) << "]);\n";
       else if (w == 4)
-        o << "      { const float s1 = S[" << phys(v, lin) << "]; " << name << "[j] = xf4{s1, s1, s1, s1}; }\n";
+        o << "      { const float s1 = " << elem(vid, lin) << "; " << name << "[j] = xf4{s1, s1, s1, s1}; }\n";
       else
-        o << "      " << name << "[j] = S[" << phys(v, lin) << "];\n";
+        o << "      " << name << "[j] = " << elem(vid, lin) << ";\n";
     };
     std::string expr;
     if (bin) {
@@ -555,17 +835,14 @@ class StagedGen {
       expr = replace_x(unary_expr(in.kind), w == 4 ? "va[j][c]" : "va[j]");
     }
     const int regs = w * (bin ? 2 : 1);
+    const long long ch = chunk(n, w, regs);
+    b << "  " << ty << " va[" << ch << "];\n";
+    if (bin) b << "  " << ty << " vb[" << ch << "];\n";
     two_phase(
         b, n, w, in.dims, regs,
         [&](std::ostringstream& o) {
-          const long long groups = n / w, iters = (groups + kThreads - 1) / kThreads;
-          const long long ch = std::max(1LL, std::min(iters, (long long)(64 / std::max(1, regs))));
-          o << "  " << ty << " va[" << ch << "];\n";
-          if (bin) o << "  " << ty << " vb[" << ch << "];\n";
-        },
-        [&](std::ostringstream& o) {
-          operand(o, A, ad, "va");
-          if (bin) operand(o, *B, bd, "vb");
+          operand(o, r.a, ad, "va");
+          if (bin) operand(o, r.b, bd, "vb");
         },
         [&](std::ostringstream& o) {
           if (w == 4)
@@ -573,8 +850,7 @@ class StagedGen {
               << ";\n      *reinterpret_cast<xf4*>(&S[" << phys(D, "e") << "]) = ov;\n";
           else
             o << "      S[" << phys(D, "e") << "] = " << expr << ";\n";
-        },
-        CH);
+        });
     b << "  }\n";
   }
 
@@ -600,7 +876,7 @@ class StagedGen {
       while (G < 64 && G * 2 <= C && (long long)R * G < kThreads) G *= 2;
       const int rows_per = kThreads / G;
       const long long passes = (R + rows_per - 1) / rows_per;
-      const bool v4 = C % (4 * G) == 0 && vec4(A);
+      const bool v4 = C % (4 * G) == 0 && A.src < 0 && vec4(A);
       const long long per = v4 ? C / (4 * G) : (C + G - 1) / G;
       b << "    const int g = t % " << G << ", r0 = t / " << G << ";\n";
       b << "#pragma unroll " << (passes <= 8 ? passes : 4) << "\n    for (int p = 0; p < " << passes << "; ++p) {\n"
@@ -614,9 +890,8 @@ class StagedGen {
         b << "          m = " << comb(comb(comb(comb("m", "q4[0]"), "q4[1]"), "q4[2]"), "q4[3]") << ";\n";
       } else {
         b << "          const int c = g + j * " << G << ";\n";
-        if (C % G) b << "          if (c < " << C << ") m = " << comb("m", "S[" + phys(A, "r * " + S(C) + " + c") + "]")
-                     << ";\n";
-        else b << "          m = " << comb("m", "S[" + phys(A, "r * " + S(C) + " + c") + "]") << ";\n";
+        if (C % G) b << "          if (c < " << C << ") m = " << comb("m", elem(r.a, "r * " + S(C) + " + c")) << ";\n";
+        else b << "          m = " << comb("m", elem(r.a, "r * " + S(C) + " + c")) << ";\n";
       }
       b << "        }\n      }\n";
       for (int o = G / 2; o > 0; o /= 2)
@@ -630,8 +905,8 @@ class StagedGen {
       if (C % kThreads) b << "      if (c < " << C << ") {\n";
       else b << "      {\n";
       b << "        float m = " << init << ";\n#pragma unroll 8\n        for (int rr = 0; rr < " << R
-        << "; ++rr) m = " << comb("m", "S[" + phys(A, "rr * " + S(C) + " + c") + "]") << ";\n        S["
-        << phys(D, "c") << "] = m;\n      }\n    }\n";
+        << "; ++rr) m = " << comb("m", elem(r.a, "rr * " + S(C) + " + c")) << ";\n        S[" << phys(D, "c")
+        << "] = m;\n      }\n    }\n";
     }
     b << "  }\n";
   }
@@ -639,85 +914,113 @@ class StagedGen {
   void emit_permute(std::ostringstream& b, int i) {
     const VmInst& in = vm_.inst[i];
     const Reads& r = rd_[i];
-    const Val &A = vals_[r.a], &D = vals_[r.dst];
+    const Val& D = vals_[r.dst];
     const int od[3] = {in.dims[in.aux[0]], in.dims[in.aux[1]], in.dims[in.aux[2]]};
     const long long n = prod(in.dims);
     b << "  // permute " << i << "\n  {\n";
-    int CH = 1;
     // output (i0, i1, i2) = input index with dim perm[d] at i_d
     const std::string src = "(iv[0] * " + S(in.dims[1]) + " + iv[1]) * " + S(in.dims[2]) + " + iv[2]";
+    b << "  float pv[" << chunk(n, 1, 1) << "];\n";
     two_phase(
         b, n, 1, od, 1,
         [&](std::ostringstream& o) {
-          const long long iters = (n + kThreads - 1) / kThreads;
-          o << "  float pv[" << std::max(1LL, std::min(iters, 64LL)) << "];\n";
-        },
-        [&](std::ostringstream& o) {
           o << "      int iv[3];\n      iv[" << in.aux[0] << "] = i0;\n      iv[" << in.aux[1] << "] = i1;\n      iv["
-            << in.aux[2] << "] = i2;\n      pv[j] = S[" << phys(A, src) << "];\n";
+            << in.aux[2] << "] = i2;\n      pv[j] = " << elem(r.a, src) << ";\n";
         },
-        [&](std::ostringstream& o) { o << "      S[" << phys(D, "e") << "] = pv[j];\n"; }, CH);
+        [&](std::ostringstream& o) { o << "      S[" << phys(D, "e") << "] = pv[j];\n"; });
     b << "  }\n";
   }
 
   void emit_matmul(std::ostringstream& b, int i) {
     const VmInst& in = vm_.inst[i];
     const Reads& r = rd_[i];
-    const Val &A = vals_[r.a], &B = vals_[r.b], &D = vals_[r.dst];
-    const Val* C = r.c >= 0 ? &vals_[r.c] : nullptr;
+    const Val& D = vals_[r.dst];
     const int M = in.dims[1], N = in.dims[2], K = in.aux[0];
     const int mode = r.mode;
     // K elements per MFMA and per lane
     const int KB = mode == kMmF32 ? 2 : mode == kMmI8 ? 32 : 16, KL = KB / 2;
     const int MT = (M + 31) / 32, NT = (N + 31) / 32, steps = (K + KB - 1) / KB;
     const bool mg = M % 32 != 0, ng = N % 32 != 0, kg = K % KB != 0;
-    b << "  // matmul " << i << ": [" << M << "," << K << "] x [" << K << "," << N << "]"
-      << (C ? " + acc" : "") << ", " << (mode == kMmF32 ? "f32" : mode == kMmF16 ? "f16" : mode == kMmBF16 ? "bf16" : "i8")
-      << " MFMA\n  {\n";
+    const bool narrow = mode == kMmF16 || mode == kMmBF16;
+    b << "  // matmul " << i << ": [" << M << "," << K << "] x [" << K << "," << N << "]" << (r.c >= 0 ? " + acc" : "")
+      << ", " << (mode == kMmF32 ? "f32" : mode == kMmF16 ? "f16" : mode == kMmBF16 ? "bf16" : "i8") << " MFMA"
+      << (D.gstore >= 0 ? ", result stored to global memory" : "") << "\n  {\n";
     b << "    const int l32 = lane & 31, h = lane >> 5;\n";
     b << "    for (int u = wave; u < " << MT * NT << "; u += 4) {\n"
       << "      const int row = (u / " << NT << ") * 32 + l32, col = (u % " << NT << ") * 32 + l32;\n";
     // two accumulators, even and odd K steps: consecutive MFMAs are then
-    // independent and issue back to back (a dependent chain waits out each
-    // MFMA's latency); their sum is the tile's (exact for i8)
+    // independent and issue back to back; their sum is the tile's (exact for i8)
     b << "      " << (mode == kMmI8 ? "xi16v" : "xf16v") << " acc0 = {}, acc1 = {};\n";
-    // fragments of K step `st` into set `p` (fa<p>, fb<p>)
-    const bool avec = KL >= 4 && A.krow == K && vec4(A) && !kg;
+    // Operand fragments of K step `st` into set p: a lane takes KL elements
+    // along K at its row of A (lane = row) / its column of B (lane = column).
+    // Narrow modes keep the 16-bit patterns (fa<p> / fb<p> as xs8), the
+    // others f32 values.
+    const Aff fa = affine(r.a, M, K), fb = affine(r.b, K, N);
+    auto frag = [&](int vid, const Aff& af, bool is_a, const std::string& name) -> std::string {
+      std::ostringstream o;
+      const std::string lanev = is_a ? "row" : "col";  // the lane's row of A / column of B
+      const int lim = is_a ? M : N;
+      const bool lg = is_a ? mg : ng;
+      std::string cond;
+      if (lg) cond = lanev + " < " + S(lim);
+      const Val& st = vals_[af.ok ? af.store : storage_of(vid)];
+      // contiguous along K: one vector read of KL elements
+      const long long sk = af.ok ? (is_a ? af.sc : af.sr) : 0, sl = af.ok ? (is_a ? af.sr : af.sc) : 0;
+      const int esz = st.h16 ? 2 : 4;
+      const bool vec = af.ok && sk == 1 && !kg && (af.base * esz) % 16 == 0 && (sl * esz) % 16 == 0 &&
+                       (KL * esz) % 16 == 0 && (narrow ? st.h16 || KL % 4 == 0 : KL % 4 == 0) &&
+                       (mode != kMmI8 && mode != kMmF32 ? true : !st.h16);
+      const std::string idx0 = S(af.base) + " + " + S(sl) + " * " + lanev + " + " + S(sk) + " * k0";
+      if (vec && st.h16) {
+        o << "            " << name << " = " << (cond.empty() ? "" : "(" + cond + ") ? ")
+          << "*reinterpret_cast<const xs8*>(&H[" << idx0 << "])" << (cond.empty() ? "" : " : xs8{}") << ";\n";
+        return o.str();
+      }
+      if (vec) {  // f32 storage, KL a multiple of 4
+        o << "            {\n";
+        for (int q = 0; q < KL / 4; ++q)
+          o << "              const xf4 q" << q << " = " << (cond.empty() ? "" : "(" + cond + ") ? ")
+            << "*reinterpret_cast<const xf4*>(&S[" << idx0 << " + " << 4 * q << "])"
+            << (cond.empty() ? "" : " : xf4{}") << ";\n";
+        for (int j = 0; j < KL; ++j) {
+          const std::string f = "q" + S(j / 4) + "[" + S(j % 4) + "]";
+          if (mode == kMmF16)
+            o << "              " << name << "[" << j << "] = __builtin_bit_cast(short, (_Float16)" << f << ");\n";
+          else if (mode == kMmBF16)
+            o << "              " << name << "[" << j << "] = (short)(__float_as_uint(" << f << ") >> 16);\n";
+          else
+            o << "              " << name << "[" << j << "] = " << f << ";\n";
+        }
+        o << "            }\n";
+        return o.str();
+      }
+      // element by element (a view or layout that is not affine, a partial K step)
+      std::string c2 = cond;
+      if (kg) c2 += (c2.empty() ? "" : " && ") + std::string("k < ") + S(K);
+      o << "#pragma unroll\n            for (int j = 0; j < " << KL << "; ++j) {\n              const int k = k0 + j;\n";
+      const std::string lin = is_a ? "row * " + S(K) + " + k" : "k * " + S(N) + " + col";
+      std::string val;
+      const bool raw16 = af.ok && st.h16;  // val is a 16-bit pattern, not an f32 value
+      if (raw16) val = "H[" + S(af.base) + " + " + S(sl) + " * " + lanev + " + " + S(sk) + " * k]";
+      else if (af.ok) val = "S[" + S(af.base) + " + " + S(sl) + " * " + lanev + " + " + S(sk) + " * k]";
+      else val = elem(vid, lin);
+      if (narrow) {
+        std::string bits;
+        if (raw16) bits = "(short)" + val;
+        else if (mode == kMmF16) bits = "__builtin_bit_cast(short, (_Float16)" + val + ")";
+        else bits = "(short)(__float_as_uint(" + val + ") >> 16)";
+        o << "              " << name << "[j] = " << (c2.empty() ? bits : "(" + c2 + ") ? " + bits + " : (short)0")
+          << ";\n";
+      } else {
+        o << "              " << name << "[j] = " << (c2.empty() ? val : "(" + c2 + ") ? " + val + " : 0.0f") << ";\n";
+      }
+      o << "            }\n";
+      return o.str();
+    };
     auto read = [&](const std::string& st, int p) -> std::string {
       std::ostringstream o;
-      const std::string FA = "fa" + S(p), FB = "fb" + S(p);
-      o << "        {\n          const int k0 = (" << st << ") * " << KB << " + h * " << KL << ";\n";
-      if (avec) {
-        o << (mg ? "          if (row < " + S(M) + ") {\n" : "          {\n");
-        o << "#pragma unroll\n            for (int j = 0; j < " << KL / 4 << "; ++j) {\n"
-          << "              const xf4 q4 = *reinterpret_cast<const xf4*>(&S["
-          << phys(A, "row * " + S(K) + " + k0 + 4 * j") << "]);\n              " << FA << "[4 * j] = q4[0]; " << FA
-          << "[4 * j + 1] = q4[1]; " << FA << "[4 * j + 2] = q4[2]; " << FA << "[4 * j + 3] = q4[3];\n"
-          << "            }\n          }\n";
-        if (mg)
-          o << "          else {\n#pragma unroll\n            for (int j = 0; j < " << KL << "; ++j) " << FA
-            << "[j] = 0.0f;\n          }\n";
-      } else {
-        std::string cond;
-        if (mg) cond = "row < " + S(M);
-        if (kg) cond += (cond.empty() ? "" : " && ") + std::string("k < ") + S(K);
-        o << "#pragma unroll\n          for (int j = 0; j < " << KL << "; ++j) {\n            const int k = k0 + j;\n"
-          << "            " << FA << "[j] = ";
-        if (!cond.empty()) o << "(" << cond << ") ? S[" << phys(A, "row * " + S(K) + " + k") << "] : 0.0f;\n";
-        else o << "S[" << phys(A, "row * " + S(K) + " + k") << "];\n";
-        o << "          }\n";
-      }
-      {
-        std::string cond;
-        if (ng) cond = "col < " + S(N);
-        if (kg) cond += (cond.empty() ? "" : " && ") + std::string("k < ") + S(K);
-        o << "#pragma unroll\n          for (int j = 0; j < " << KL << "; ++j) {\n            const int k = k0 + j;\n"
-          << "            " << FB << "[j] = ";
-        if (!cond.empty()) o << "(" << cond << ") ? S[" << phys(B, "k * " + S(N) + " + col") << "] : 0.0f;\n";
-        else o << "S[" << phys(B, "k * " + S(N) + " + col") << "];\n";
-        o << "          }\n";
-      }
-      o << "        }\n";
+      o << "        {\n          const int k0 = (" << st << ") * " << KB << " + h * " << KL << ";\n"
+        << frag(r.a, fa, true, "fa" + S(p)) << frag(r.b, fb, false, "fb" + S(p)) << "        }\n";
       return o.str();
     };
     auto mfma = [&](int p) -> std::string {
@@ -730,16 +1033,12 @@ class StagedGen {
             << ", 0, 0, 0);\n";
           break;
         case kMmF16:
-          o << "        {\n          xh8 ha, hb;\n#pragma unroll\n          for (int j = 0; j < 8; ++j) { ha[j] = "
-               "(_Float16)" << FA << "[j]; hb[j] = (_Float16)" << FB << "[j]; }\n"
-            << "          " << acc << " = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, hb, " << acc << ", 0, 0, 0);\n        }\n";
+          o << "        " << acc << " = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(xh8, " << FA
+            << "), __builtin_bit_cast(xh8, " << FB << "), " << acc << ", 0, 0, 0);\n";
           break;
         case kMmBF16:
-          o << "        {\n          xs8 ha, hb;\n#pragma unroll\n          for (int j = 0; j < 8; ++j) { ha[j] = "
-               "(short)(__float_as_uint(" << FA << "[j]) >> 16); hb[j] = (short)(__float_as_uint(" << FB
-            << "[j]) >> 16); }\n"
-            << "          " << acc << " = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(xb8, ha), "
-               "__builtin_bit_cast(xb8, hb), " << acc << ", 0, 0, 0);\n        }\n";
+          o << "        " << acc << " = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(xb8, " << FA
+            << "), __builtin_bit_cast(xb8, " << FB << "), " << acc << ", 0, 0, 0);\n";
           break;
         default:
           o << "        {\n          xi4v ia, ib;\n#pragma unroll\n          for (int j = 0; j < 4; ++j) {\n";
@@ -749,8 +1048,8 @@ class StagedGen {
               << X << "[4 * j + 1] & 255) << 8) | ((unsigned)((int)" << X << "[4 * j + 2] & 255) << 16) | "
               << "((unsigned)((int)" << X << "[4 * j + 3] & 255) << 24));\n";
           }
-          o << "          }\n          " << acc << " = __builtin_amdgcn_mfma_i32_32x32x32_i8(ia, ib, " << acc << ", 0, 0, 0);\n"
-            << "        }\n";
+          o << "          }\n          " << acc << " = __builtin_amdgcn_mfma_i32_32x32x32_i8(ia, ib, " << acc
+            << ", 0, 0, 0);\n        }\n";
           break;
       }
       return o.str();
@@ -761,18 +1060,19 @@ class StagedGen {
     // no branch (the compiler waits for every LDS read at a block boundary):
     // look-ahead reads past the last step re-read the last step, and the
     // steps beyond the last whole group run after the loop from the sets the
-    // loop's reads already filled.
+    // loop's reads already filled.  Scheduling fences keep each step's
+    // look-ahead reads ahead of its MFMA (left alone, the compiler sinks them
+    // next to their use).
     int NS = std::max(1, std::min(steps, mode == kMmF32 ? 8 : 4));
     if (NS > 1 && NS % 2) --NS;  // even: set j holds steps of parity j % 2
     const int full = steps / NS * NS, tail = steps - full;
     auto clamp = [&](const std::string& e) { return "min(" + e + ", " + S(steps - 1) + ")"; };
-    b << "      float";
-    for (int q = 0; q < NS; ++q) b << (q ? ", " : " ") << "fa" << q << "[" << KL << "], fb" << q << "[" << KL << "]";
-    b << ";\n";
+    for (int q = 0; q < NS; ++q) {
+      if (narrow) b << "      xs8 fa" << q << ", fb" << q << ";\n";
+      else b << "      float fa" << q << "[" << KL << "], fb" << q << "[" << KL << "];\n";
+    }
     for (int q = 0; q + 1 < NS; ++q) b << read(S(std::min(q, steps - 1)), q);
     b << "#pragma unroll 1\n      for (int s = 0; s < " << full << "; s += " << NS << ") {\n";
-    // scheduling fences keep each step's look-ahead reads ahead of its MFMA
-    // (left alone, the compiler sinks them next to their use)
     for (int j = 0; j < NS; ++j) {
       if (NS > 1) b << read(clamp("s + " + S(j + NS - 1)), (j + NS - 1) % NS);
       else b << read("s", 0);
@@ -789,8 +1089,24 @@ class StagedGen {
     if (ng) cond += (cond.empty() ? "" : " && ") + std::string("col < ") + S(N);
     b << "        " << (cond.empty() ? "{" : "if (" + cond + ") {") << "\n";
     b << "          float o = " << (mode == kMmI8 ? "(float)acc[v]" : "acc[v]") << ";\n";
-    if (C) b << "          o = o + S[" << phys(*C, "rr * " + S(N) + " + col") << "];\n";
-    b << "          S[" << phys(D, "rr * " + S(N) + " + col") << "] = o;\n        }\n      }\n    }\n  }\n";
+    if (r.c >= 0) b << "          o = o + " << elem(r.c, "rr * " + S(N) + " + col") << ";\n";
+    if (D.gstore >= 0) {
+      // element (rr, col) is the store's element rr * N + col of its own dims
+      const VmInst& st = vm_.inst[D.gstore];
+      const VmAccess& acc = vm_.access[st.kind];
+      const char* base = acc.elem == Elem::F32 ? "float" : acc.elem == Elem::I8 ? "signed char" : "unsigned short";
+      b << "          const int e = rr * " << N << " + col;\n"
+        << "          const int i2 = e % " << st.dims[2] << ", i1 = (e / " << st.dims[2] << ") % " << st.dims[1]
+        << ", i0 = e / " << (long long)st.dims[1] * st.dims[2] << ";\n"
+        << "          const long long off = " << origin(acc.addr) << " + (long long)i0 * " << acc.stride[0]
+        << "LL + (long long)i1 * " << acc.stride[1] << "LL + (long long)i2 * " << acc.stride[2] << "LL;\n";
+      const std::string dst = "static_cast<" + std::string(base) + "*>(a.p[" + S(st.kind) + "]) + off";
+      if (streamed(st.kind)) b << "          __builtin_nontemporal_store(" << store_conv(acc.elem, "o") << ", " << dst << ");\n";
+      else b << "          *(" << dst << ") = " << store_conv(acc.elem, "o") << ";\n";
+    } else {
+      b << "          S[" << phys(D, "rr * " + S(N) + " + col") << "] = o;\n";
+    }
+    b << "        }\n      }\n    }\n  }\n";
   }
 };
 
