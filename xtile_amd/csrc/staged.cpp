@@ -36,11 +36,12 @@
 // keep their meaning.  krow = pitch = the innermost dim, except for
 //   * matmul operands: rows that the lanes of a fragment read side by side
 //     (A's rows; the source rows of a transposed view) get a pitch of 4 mod 8
-//     floats or 8 mod 16 halves for the 16-byte reads of the narrow types
-//     (sixteen rows in sixteen distinct bank groups) and 2 mod 4 floats for
-//     f32 (32 rows of single floats in distinct banks); B[K, N] read across
-//     columns gets 4 mod 8 floats / 8 mod 16 halves for the narrow types (the
-//     two half-waves' rows, 8 apart, in distinct banks);
+//     floats or 8 mod 16 halves: the 16-byte reads of the narrow types put
+//     sixteen rows in sixteen distinct bank groups, and f32's single floats
+//     of 32 rows meet at most two to a bank while rows stay float4-aligned
+//     for the elementwise ops that write them; B[K, N] read across columns
+//     gets 4 mod 8 floats / 8 mod 16 halves for the narrow types (the two
+//     half-waves' rows, 8 apart, in distinct banks);
 //   * the source of a copying permute: an odd pitch (a column read is
 //     conflict-free).
 // The first consumer in program order decides.
@@ -164,7 +165,12 @@ class StagedGen {
       switch (in.op) {
         case VmOp::Store: emit_store(b, i); break;
         case VmOp::Unary:
-        case VmOp::Binary: emit_elementwise(b, i); break;
+        case VmOp::Binary: {
+          const int end = ew_chain_end(i);
+          emit_elementwise(b, i, end);
+          i = end;  // the run's later instructions are done
+          break;
+        }
         case VmOp::Reduce: emit_reduce(b, i); break;
         case VmOp::Permute: emit_permute(b, i); break;
         case VmOp::Matmul:
@@ -379,7 +385,7 @@ class StagedGen {
           }
           (void)M;
           if (st.h16) st.pitch = pad_to(st.krow, 16, 8);
-          else if (r.mode == kMmF32) st.pitch = lanes_on_rows ? pad_to(st.krow, 4, 2) : st.krow;
+          else if (r.mode == kMmF32) st.pitch = lanes_on_rows ? pad_to(st.krow, 8, 4) : st.krow;
           else st.pitch = pad_to(st.krow, 8, 4);
         }
       } else if (in.op == VmOp::Permute && vals_[r.dst].src < 0) {
@@ -797,7 +803,35 @@ class StagedGen {
     return "((" + i0 + " * " + S(od[1]) + " + " + i1 + ") * " + S(od[2]) + " + " + i2 + ")";
   }
 
-  void emit_elementwise(std::ostringstream& b, int i) {
+  // The longest run of elementwise instructions from i in which each one
+  // writes in place over the previous one's result (its only reader), with
+  // the same shape and element grouping: one loop computes the run in
+  // registers, reading the other operands (complete before the run's first
+  // barrier) and writing only the last result.
+  int ew_chain_end(int i) const {
+    int j = i;
+    const int w = ew_width(i);
+    while (j + 1 < static_cast<int>(vm_.inst.size())) {
+      const VmInst& nx = vm_.inst[j + 1];
+      if (nx.op != VmOp::Unary && nx.op != VmOp::Binary) break;
+      const Val& D = vals_[rd_[j + 1].dst];
+      if (D.alias != rd_[j].dst || vals_[rd_[j].dst].users.size() != 1) break;
+      if (nx.dims[0] != vm_.inst[i].dims[0] || nx.dims[1] != vm_.inst[i].dims[1] || nx.dims[2] != vm_.inst[i].dims[2])
+        break;
+      if (ew_width(j + 1) != w) break;
+      // a load whose LDS write waits for this reader is written before it, behind a barrier
+      bool waits = false;
+      for (int k = 0; k <= j; ++k)
+        if (vm_.inst[k].op == VmOp::Load && deferred(k) && vals_[rd_[k].dst].alloc_at == j + 1) waits = true;
+      if (waits) break;
+      ++j;
+    }
+    return j;
+  }
+
+  // elements a thread takes at once: four when every operand that varies
+  // along the innermost dim is contiguous there
+  int ew_width(int i) const {
     const VmInst& in = vm_.inst[i];
     const Reads& r = rd_[i];
     const Val& D = vals_[r.dst];
@@ -805,51 +839,102 @@ class StagedGen {
     const bool bin = in.op == VmOp::Binary;
     const Val& A = vals_[r.a];
     const Val* B = bin ? &vals_[r.b] : nullptr;
-    int ad[3] = {in.dims[0], in.dims[1], in.dims[2]}, bd[3] = {1, 1, 1};
-    if (bin)
-      for (int d = 0; d < 3; ++d) {
-        ad[d] = in.lhs[d];
-        bd[d] = in.aux[d];
-      }
-    // four elements at a time when every operand that varies along the
-    // innermost dim is contiguous there
+    const int* ad = bin ? in.lhs : in.dims;
     const bool v4 = in.dims[2] % 4 == 0 && n % 4 == 0 && vec4(D) && (ad[2] == 1 || (A.src < 0 && vec4(A))) &&
-                    (!bin || bd[2] == 1 || (B->src < 0 && vec4(*B)));
-    const int w = v4 ? 4 : 1;
+                    (!bin || in.aux[2] == 1 || (B->src < 0 && vec4(*B)));
+    return v4 ? 4 : 1;
+  }
+
+  // the f32 formula of a unary op; exp is exp2 of x log2(e) on the hardware
+  // exp2 (relative error at most |x| 2^-24 plus one ulp: below 5.3e-6 for
+  // normal results; results below FLT_MIN may flush to 0)
+  static std::string unary_formula(int kind, const std::string& x) {
+    if (kind == static_cast<int>(VmUnary::Exp)) return "__builtin_amdgcn_exp2f((" + x + ") * 1.44269504088896340736f)";
+    return replace_x(unary_expr(kind), x);
+  }
+
+  void emit_elementwise(std::ostringstream& b, int i0, int i1) {
+    const VmInst& first = vm_.inst[i0];
+    const long long n = prod(first.dims);
+    const int w = ew_width(i0);
     const char* ty = w == 4 ? "xf4" : "float";
-    b << "  // " << (bin ? "binary " : "unary ") << i << "\n  {\n";
-    auto operand = [&](std::ostringstream& o, int vid, const int od[3], const std::string& name) {
-      const std::string lin = bcast(od);
-      if (w == 4 && od[2] != 1)
-        o << "      " << name << "[j] = *reinterpret_cast<const xf4*>(&S[" << phys(vals_[vid], lin) << "]);\n";
-      else if (w == 4)
-        o << "      { const float s1 = " << elem(vid, lin) << "; " << name << "[j] = xf4{s1, s1, s1, s1}; }\n";
-      else
-        o << "      " << name << "[j] = " << elem(vid, lin) << ";\n";
+    b << "  // elementwise " << i0;
+    for (int i = i0 + 1; i <= i1; ++i) b << ", " << i;
+    b << (i1 > i0 ? " in registers" : "") << "\n  {\n";
+    // operands read from LDS: both of the first op's, then the other operand of each later one
+    struct Opnd {
+      int vid;
+      int dims[3];
+      std::string name;
     };
-    std::string expr;
-    if (bin) {
-      const char* op = in.kind == 0 ? " + " : in.kind == 1 ? " - " : " * ";
-      expr = w == 4 ? "va[j][c]" + std::string(op) + "vb[j][c]" : "va[j]" + std::string(op) + "vb[j]";
-    } else {
-      expr = replace_x(unary_expr(in.kind), w == 4 ? "va[j][c]" : "va[j]");
+    std::vector<Opnd> ops;
+    std::vector<std::string> a_of(i1 - i0 + 1), b_of(i1 - i0 + 1);
+    for (int i = i0; i <= i1; ++i) {
+      const VmInst& in = vm_.inst[i];
+      const Reads& r = rd_[i];
+      const bool bin = in.op == VmOp::Binary;
+      const int* ad = bin ? in.lhs : in.dims;
+      const int* bd = in.aux;
+      const int k = i - i0;
+      auto add = [&](int vid, const int* d) {
+        Opnd o;
+        o.vid = vid;
+        for (int q = 0; q < 3; ++q) o.dims[q] = d[q];
+        o.name = "v" + S(ops.size());
+        ops.push_back(o);
+        return ops.back().name + "[j]";
+      };
+      const std::string prevv = "t" + S(k - 1);
+      if (k == 0) {
+        a_of[k] = add(r.a, ad);
+        if (bin) b_of[k] = add(r.b, bd);
+      } else {
+        const int chain = rd_[i - 1].dst;
+        a_of[k] = r.a == chain ? prevv : add(r.a, ad);
+        if (bin) b_of[k] = r.b == chain ? prevv : add(r.b, bd);
+      }
     }
-    const int regs = w * (bin ? 2 : 1);
+    const int regs = w * static_cast<int>(ops.size());
     const long long ch = chunk(n, w, regs);
-    b << "  " << ty << " va[" << ch << "];\n";
-    if (bin) b << "  " << ty << " vb[" << ch << "];\n";
+    for (const Opnd& o : ops) b << "  " << ty << " " << o.name << "[" << ch << "];\n";
+    auto operand = [&](std::ostringstream& o, const Opnd& op) {
+      const std::string lin = bcast(op.dims);
+      const Val& v = vals_[op.vid];
+      if (w == 4 && op.dims[2] != 1)
+        o << "      " << op.name << "[j] = *reinterpret_cast<const xf4*>(&S[" << phys(v, lin) << "]);\n";
+      else if (w == 4)
+        o << "      { const float s1 = " << elem(op.vid, lin) << "; " << op.name << "[j] = xf4{s1, s1, s1, s1}; }\n";
+      else
+        o << "      " << op.name << "[j] = " << elem(op.vid, lin) << ";\n";
+    };
+    const Val& D = vals_[rd_[i1].dst];
     two_phase(
-        b, n, w, in.dims, regs,
+        b, n, w, first.dims, regs,
         [&](std::ostringstream& o) {
-          operand(o, r.a, ad, "va");
-          if (bin) operand(o, r.b, bd, "vb");
+          for (const Opnd& op : ops) operand(o, op);
         },
         [&](std::ostringstream& o) {
-          if (w == 4)
-            o << "      xf4 ov;\n#pragma unroll\n      for (int c = 0; c < 4; ++c) ov[c] = " << expr
-              << ";\n      *reinterpret_cast<xf4*>(&S[" << phys(D, "e") << "]) = ov;\n";
-          else
-            o << "      S[" << phys(D, "e") << "] = " << expr << ";\n";
+          const int lanes = w;
+          o << "      " << ty << " ov;\n#pragma unroll\n      for (int c = 0; c < " << lanes << "; ++c) {\n";
+          for (int i = i0; i <= i1; ++i) {
+            const VmInst& in = vm_.inst[i];
+            const int k = i - i0;
+            auto lane = [&](const std::string& x) {
+              if (x.rfind("t", 0) == 0) return x;                   // a chain value, already a lane scalar
+              return w == 4 ? x + "[c]" : x;                        // an operand register
+            };
+            std::string expr;
+            if (in.op == VmOp::Binary) {
+              const char* op = in.kind == 0 ? " + " : in.kind == 1 ? " - " : " * ";
+              expr = lane(a_of[k]) + op + lane(b_of[k]);
+            } else {
+              expr = unary_formula(in.kind, lane(a_of[k]));
+            }
+            o << "        const float t" << k << " = " << expr << ";\n";
+          }
+          o << "        " << (w == 4 ? "ov[c]" : "ov") << " = t" << (i1 - i0) << ";\n      }\n";
+          if (w == 4) o << "      *reinterpret_cast<xf4*>(&S[" << phys(D, "e") << "]) = ov;\n";
+          else o << "      S[" << phys(D, "e") << "] = ov;\n";
         });
     b << "  }\n";
   }
@@ -1056,30 +1141,38 @@ class StagedGen {
     };
     // A ring of NS fragment sets: the reads of steps s + 1 .. s + NS - 1 are
     // in flight while step s's MFMA runs (an f32 step is one 64-cycle MFMA
-    // on two floats a lane, so it reads furthest ahead).  The loop body has
-    // no branch (the compiler waits for every LDS read at a block boundary):
-    // look-ahead reads past the last step re-read the last step, and the
-    // steps beyond the last whole group run after the loop from the sets the
-    // loop's reads already filled.  Scheduling fences keep each step's
-    // look-ahead reads ahead of its MFMA (left alone, the compiler sinks them
-    // next to their use).
+    // on two floats a lane, so it reads furthest ahead).  The loop runs the
+    // groups of NS steps whose look-ahead reads stay within K, with no branch
+    // in its body (the compiler waits for every LDS read at a block
+    // boundary); the last steps follow unrolled, reading ahead only while
+    // steps remain.  Scheduling fences keep each step's look-ahead reads
+    // ahead of its MFMA (left alone, the compiler sinks them next to their
+    // use).  NS is even, so set j always holds steps of parity j % 2.
     int NS = std::max(1, std::min(steps, mode == kMmF32 ? 8 : 4));
-    if (NS > 1 && NS % 2) --NS;  // even: set j holds steps of parity j % 2
-    const int full = steps / NS * NS, tail = steps - full;
-    auto clamp = [&](const std::string& e) { return "min(" + e + ", " + S(steps - 1) + ")"; };
+    if (NS > 1 && NS % 2) --NS;
     for (int q = 0; q < NS; ++q) {
       if (narrow) b << "      xs8 fa" << q << ", fb" << q << ";\n";
       else b << "      float fa" << q << "[" << KL << "], fb" << q << "[" << KL << "];\n";
     }
-    for (int q = 0; q + 1 < NS; ++q) b << read(S(std::min(q, steps - 1)), q);
-    b << "#pragma unroll 1\n      for (int s = 0; s < " << full << "; s += " << NS << ") {\n";
-    for (int j = 0; j < NS; ++j) {
-      if (NS > 1) b << read(clamp("s + " + S(j + NS - 1)), (j + NS - 1) % NS);
-      else b << read("s", 0);
-      b << "        __builtin_amdgcn_sched_barrier(0);\n" << mfma(j) << "        __builtin_amdgcn_sched_barrier(0);\n";
+    const std::string fence = "        __builtin_amdgcn_sched_barrier(0);\n";
+    if (NS == 1) {
+      b << "#pragma unroll 1\n      for (int s = 0; s < " << steps << "; ++s) {\n" << read("s", 0) << fence << mfma(0)
+        << fence << "      }\n";
+    } else {
+      for (int q = 0; q + 1 < NS; ++q) b << read(S(q), q);
+      // groups starting at s read up to step s + 2 NS - 2
+      const int groups = steps >= 2 * NS - 1 ? (steps - (2 * NS - 1)) / NS + 1 : 0;
+      if (groups > 0) {
+        b << "#pragma unroll 1\n      for (int s = 0; s < " << groups * NS << "; s += " << NS << ") {\n";
+        for (int j = 0; j < NS; ++j)
+          b << read("s + " + S(j + NS - 1), (j + NS - 1) % NS) << fence << mfma(j) << fence;
+        b << "      }\n";
+      }
+      for (int t = groups * NS; t < steps; ++t) {
+        if (t + NS - 1 < steps) b << read(S(t + NS - 1), (t + NS - 1) % NS);
+        b << fence << mfma(t % NS) << fence;
+      }
     }
-    b << "      }\n";
-    for (int j = 0; j < tail; ++j) b << mfma(j);
     b << "      const auto acc = acc0 + acc1;\n";
     // D: lane l holds column col; register v holds row 8 (v / 4) + 4 h + v % 4 of the tile
     b << "#pragma unroll\n      for (int v = 0; v < 16; ++v) {\n"
