@@ -5,8 +5,10 @@
 One step = one launch of the tile program over one batch of synthetic input
 (numpy PCG64, seed = config index, shapes of BASELINE.json's configs).  The
 headline line is C2 (row softmax fp32 8192x4096, BASELINE.json configs[1]);
-the six BASELINE.json configurations (C1-C6) and C7, a row layernorm run as a
-fused tile program, are measured and reported under "per_config".
+the six BASELINE.json configurations (C1-C6), C7 (a row layernorm run as a
+fused tile program) and C10 (an attention Block, matmul -> row softmax ->
+matmul, run as a staged tile program) are measured and reported under
+"per_config".
 
 Order of work: every input is generated on the host first; then the GPU
 legs run back to back - the ceiling kernels of include/xt_ceiling.h (an MFMA
@@ -75,7 +77,7 @@ METRIC = "GB/s (add, softmax) & TFLOP/s (matmul, conv2d) on 1 MI355X, % of roofl
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "i8": 5000.0, "f32": 157.3}  # dense; i8 in TOP/s
 ROTATE_BYTES = 1 << 30
-ALL = ["c1", "c2", "c3", "c4", "c5", "c6", "c7"]
+ALL = ["c1", "c2", "c3", "c4", "c5", "c6", "c7", "c10"]
 
 
 def _f32(a):
@@ -173,16 +175,16 @@ def make_config(name: str):
         }
     if name == "c10":
         rng = np.random.default_rng(10)
-        heads, nq, nk, d, tq = 512, 128, 128, 64, 64
+        heads, nq, nk, d, tq = 1024, 64, 64, 64, 64
         q = rng.normal(0, 0.5, (heads, nq, d)).astype(np.float16)
         k = rng.normal(0, 0.5, (heads, nk, d)).astype(np.float16)
         v = _f32(rng.normal(0, 1.0, (heads, nk, d)))
         return K.attention(heads, nq, nk, d, tq), [q, k, v, np.zeros((heads, nq, d), np.float32)], [
             "f16", "f16", "f32", "f32"], 3, {
             "workload": "c10_attention (outside the five reference configurations: a program with matmul, "
-                        "transpose and row softmax in one Block, on the staged kernel): softmax(Q K^T) V, 512 "
-                        "heads x 128 queries x 128 keys, d=64, Q/K f16, V and result f32, 64-query tiles, K/V "
-                        "shared=1, grid (2,512,1)",
+                        "transpose and row softmax in one Block, on the staged kernel): softmax(Q K^T) V, 1024 "
+                        "heads x 64 queries x 64 keys, d=64, Q/K f16, V and result f32, one 64-query tile per "
+                        "head, K/V shared=1, grid (1,1024,1)",
             "unit": "TFLOP/s", "bound": "mixed", "dtype": "f16+f32", "check": ("frob", 1e-5),
             "data": "synthetic: numpy PCG64 seed=10, Q,K normal(0,0.5) -> f16, V normal(0,1)",
             # the f16 product Q K^T and the f32 product P V, in FLOPs per launch

@@ -53,6 +53,15 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, unsigned lds, unsigned voff, u
 // their maxima), n < 64.
 #define XTK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
 
+// The logical index of workgroup `id` of `n` when the 8 XCDs, which receive
+// workgroups round-robin (id % 8), should each take a contiguous run of
+// logical indices (the first n % 8 XCDs one more than the rest): a bijection
+// on [0, n).
+__device__ __forceinline__ int xcd_contiguous(int id, int n) {
+  const int x = id & 7, j = id >> 3, per = n >> 3, rem = n & 7;
+  return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + j;
+}
+
 // Affine element offset of a tile origin: c0 + x*sx + y*sy + z*sz
 // (the host folds tile coordinates, tile shape and memref strides into it).
 struct TileOff {

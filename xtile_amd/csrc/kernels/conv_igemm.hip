@@ -127,7 +127,8 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // that also read each stage's fragments during the previous stage's MFMAs
   // and spread the DMA over them, measured slower on 3 x 3 convs with 128 to
   // 512 channels (e.g. 28 x 28 x 128: 18.3 us with this loop at four stages,
-  // 19.2 at five, 21.1 / 23.2 pipelined)
+  // 19.2 at five, 21.1 / 23.2 pipelined); eight stages (one workgroup a CU)
+  // left 32 x 14^2 x 256 -> 256 unchanged (29.0 / 30.4 us)
   constexpr int NS = 4;
   constexpr int ES = ELEM == kIgI8 ? 1 : 2;  // bytes per element
   // a stage is 64 bytes of K: 32 f16 / bf16 or 64 i8 channels; a K step of
@@ -146,11 +147,13 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
   auto buf = [&](int q) { return smem + (q % NS) * STAGE; };
 
-  // workgroup -> (K range, pixel tile, channel tile); with a multiple of 8
-  // workgroups the 8 XCDs receive contiguous runs, so the channel tiles of
-  // one pixel tile share its input rows in one L2
-  int L = blockIdx.x;
-  if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
+  // workgroup -> (K range, pixel tile, channel tile).  Workgroups are dealt
+  // to the 8 XCDs round-robin (id % 8); each XCD takes a contiguous run of
+  // the logical order (the first nwg % 8 XCDs one more), so the channel tiles
+  // of a pixel tile and neighbouring pixel tiles share input rows and filter
+  // columns in one L2.  (Without it a deep layer's whole input and filter,
+  // 4.4 MB for 32 x 14^2 x 256 -> 256, passed through every XCD's 4 MB L2.)
+  int L = xcd_contiguous(blockIdx.x, p.nwg);
   const int kr = L / p.tiles;
   L -= kr * p.tiles;
   const int mt = L / p.ntiles;

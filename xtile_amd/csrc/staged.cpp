@@ -110,6 +110,7 @@ class StagedGen {
 
   bool run(FusedPlan& out, std::string& why) {
     if (!analyze(why) || !views() || !layouts(why) || !plan_loads() || !allocate(why)) return false;
+    earlier_writes();
     if (std::getenv("XTILE_AMD_STAGE_DUMP"))
       for (size_t v = 0; v < vals_.size(); ++v) {
         const Val& w = vals_[v];
@@ -154,12 +155,14 @@ class StagedGen {
         continue;
       }
       barrier_before(i);
-      // deferred loads whose first reader this is: their LDS write, then a barrier
+      // deferred loads written in this step: before their first reader's
+      // barrier, or (written in the reader's own step) behind one more
       bool wrote = false;
       for (int k = 0; k < i; ++k)
         if (vm_.inst[k].op == VmOp::Load && deferred(k) && vals_[rd_[k].dst].alloc_at == i) {
           emit_load_write(b, k);
-          wrote = true;
+          const auto& us = vals_[rd_[k].dst].users;
+          wrote = wrote || *std::min_element(us.begin(), us.end()) == i;
         }
       if (wrote) b << "  __syncthreads();\n";
       switch (in.op) {
@@ -481,6 +484,37 @@ class StagedGen {
       if (first > next) v.alloc_at = first;
     }
     return true;
+  }
+
+  // A deferred load written at its first reader costs a barrier of its own.
+  // Written during the step before (an instruction that begins a step: not
+  // silent, not a load, not the continuation of an in-place elementwise
+  // chain), the barrier after that step orders it; kept when the packed LDS
+  // does not grow.
+  void earlier_writes() {
+    const int n = static_cast<int>(vm_.inst.size());
+    for (int i = 0; i < n; ++i) {
+      if (vm_.inst[i].op != VmOp::Load || !deferred(i)) continue;
+      Val& v = vals_[rd_[i].dst];
+      const int c = v.alloc_at - 1;
+      if (c <= i || silent(c) || vm_.inst[c].op == VmOp::Load) continue;
+      const VmInst& ci = vm_.inst[c];
+      if ((ci.op == VmOp::Unary || ci.op == VmOp::Binary) && c > 0 &&
+          (vm_.inst[c - 1].op == VmOp::Unary || vm_.inst[c - 1].op == VmOp::Binary) &&
+          vals_[rd_[c].dst].alias == rd_[c - 1].dst)
+        continue;  // c may continue the previous step's chain
+      const long long before = high_;
+      const int keep_at = v.alloc_at;
+      std::vector<int> offs(vals_.size());
+      for (size_t w = 0; w < vals_.size(); ++w) offs[w] = vals_[w].off;
+      v.alloc_at = c;
+      std::string why;
+      if (!allocate(why) || high_ > before) {
+        v.alloc_at = keep_at;
+        for (size_t w = 0; w < vals_.size(); ++w) vals_[w].off = offs[w];
+        high_ = before;
+      }
+    }
   }
 
   bool silent(int i) const {
