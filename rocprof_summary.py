@@ -113,6 +113,8 @@ def main(argv=None) -> int:
     ap.add_argument("--command", action="append", default=[], help="command lines to record")
     ap.add_argument("--bench-log", default=None, help="stdout of the traced bench.py run")
     ap.add_argument("--power", default=None, help="JSON line written by power_sample.py for this config")
+    ap.add_argument("--trace-eager", default=None,
+                    help="a kernel-trace database of bench.py's eager 20-launch protocol (--steps 20 --warmup 5)")
     args = ap.parse_args(argv)
 
     power = json.loads(open(args.power).read().strip().splitlines()[-1]) if args.power else None
@@ -142,6 +144,12 @@ def main(argv=None) -> int:
             if span:
                 out.append(f"selected_back_to_back_us_per_dispatch: {span[0]:.3f}  (span of the longest run of "
                            f"{span[1]} consecutive dispatches / count)")
+    if args.trace_eager and args.kernel:
+        eager = [d / 1000.0 for n, d, *_ in _kernels(args.trace_eager, args.kernel)]
+        if len(eager) >= 20:
+            timed = eager[-20:]  # the timed launches come last
+            out.append(f"eager_protocol_avg_us: {statistics.mean(timed):.3f}  (the last 20 dispatches of the eager "
+                       f"20-launch run: its timed launches)")
     if args.bench_log:
         lines = [ln for ln in open(args.bench_log).read().splitlines() if ln.startswith('{"metric"')]
         if lines:
