@@ -135,6 +135,73 @@ def test_matmul_followed_by_ops(cuda, dt, m_, n_, k_, tm, tn):
     assert frob_rel(got, want) <= 1e-5
 
 
+@xt.kernel
+def _matmul_then_row_norm(a, b, gamma, beta, inv_n, eps, out, rstd, tm, tn, tk):
+    i = xt.bid(0)
+    j = xt.bid(1)
+    x = xt.load(a, index=(i, 0), shape=(tm, tk))
+    w = xt.load(b, index=(0, j), shape=(tk, tn), shared=1)
+    g = xt.load(gamma, index=(0, j), shape=(1, tn), shared=1)
+    be = xt.load(beta, index=(0, j), shape=(1, tn), shared=1)
+    n = xt.load(inv_n, index=(0, 0), shape=(1, 1), shared=1)
+    e = xt.load(eps, index=(0, 0), shape=(1, 1), shared=1)
+    t = xt.matmul(x, w)
+    xc = xt.sub(t, xt.mul(xt.sum(t, axis=1), n))
+    r = xt.rsqrt(xt.add(xt.mul(xt.sum(xt.mul(xc, xc), axis=1), n), e))
+    xt.store(rstd, index=(i, j), tile=r)
+    xt.store(out, index=(i, j), tile=xt.add(xt.mul(xt.mul(xc, r), g), be))
+
+
+@pytest.mark.parametrize(
+    "dt,m_,n_,k_,tm,tn",
+    [("f16", 256, 128, 64, 64, 64),     # 4 lanes a row, one pass
+     ("f32", 64, 48, 40, 32, 24),       # 8 lanes a row of 24: 3 elements a lane, scalar LDS accesses
+     ("bf16", 256, 128, 32, 128, 64),   # 2 lanes a row of 64
+     ("f32", 512, 16, 32, 512, 8),      # 512 rows of 8: a lane a row, two passes
+     ("f16", 64, 256, 32, 16, 256)],    # 16 lanes a row of 256
+)
+def test_matmul_then_row_normalisation(cuda, monkeypatch, dt, m_, n_, k_, tm, tn):
+    """matmul, then a layernorm along the result's rows with gamma / beta
+    column vectors and (1, 1) scalars, storing the rows' 1/std as well: the
+    row reductions and the ops around them run as one register step (a row
+    segment); the staged kernel, the interpreter and the oracle agree."""
+    xdt = {"f16": xt.float16, "bf16": xt.bfloat16, "f32": xt.float32}[dt]
+    nt = n_ // tn
+
+    def build():
+        return xt.convert(_matmul_then_row_norm,
+                          args=(xt.Array((m_, k_), xdt), xt.Array((k_, n_), xdt), xt.Array((1, n_), xt.float32),
+                                xt.Array((1, n_), xt.float32), xt.Array((1, 1), xt.float32),
+                                xt.Array((1, 1), xt.float32), xt.Array((m_, n_), xt.float32),
+                                xt.Array((m_, nt), xt.float32), tm, tn, k_),
+                          grid=(m_ // tm, nt, 1), double_buffering=False)
+
+    m = build()
+    assert xt.plan(m)["kernel"].startswith("staged")
+    rng = np.random.default_rng(37)
+    a = rng.normal(0, 0.3, (m_, k_)).astype(np.float32)
+    b = rng.normal(0, 0.3, (k_, n_)).astype(np.float32)
+    if dt == "f16":
+        a, b = a.astype(np.float16), b.astype(np.float16)
+    elif dt == "bf16":
+        a, b = f32_to_bf16_bits(a), f32_to_bf16_bits(b)
+    gamma = rng.normal(1, 0.2, (1, n_)).astype(np.float32)
+    beta = rng.normal(0, 0.2, (1, n_)).astype(np.float32)
+    bufs = [a, b, gamma, beta, np.full((1, 1), 1.0 / tn, np.float32), np.full((1, 1), 1e-5, np.float32),
+            np.zeros((m_, n_), np.float32), np.zeros((m_, nt), np.float32)]
+    dts = [dt, dt, "f32", "f32", "f32", "f32", "f32", "f32"]
+    got = run_gpu(m, bufs, dts, cuda, case=f"matmul then row norm {dt} {m_}x{n_}x{k_} tiles {tm}x{tn}")
+    want = run_oracle(m, bufs, oracle_threads())
+    assert frob_rel(got[6], want[6]) <= 1e-5
+    assert frob_rel(got[7], want[7]) <= 1e-5
+    monkeypatch.setenv("XTILE_AMD_STAGE", "0")
+    mi = build()
+    assert xt.plan(mi)["kernel"].startswith("tile_vm")
+    interp = run_gpu(mi, bufs, dts, cuda, case="row norm on the interpreter")
+    assert frob_rel(got[6], interp[6]) <= 1e-5
+    assert frob_rel(got[7], interp[7]) <= 1e-5
+
+
 def test_staged_and_interpreter_agree_on_the_i8_epilogue(cuda, monkeypatch):
     """kernels/matmul.py's program with 16 x 8 tiles (below the GEMM
     kernel's 64 x 64) and K = 72 (two i8 MFMA steps of 32, the second part

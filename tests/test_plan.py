@@ -154,6 +154,19 @@ def test_staged_plans():
     assert "mfma=f32 " in xt.plan(m)["kernel"]
 
 
+def test_staged_row_segments(tmp_path, monkeypatch):
+    """The staged generator computes the attention's softmax (row max,
+    subtract, exp, row sum, reciprocal, scale) in registers as one step with
+    four lanes a row, so the kernel has three barriers: after the loads,
+    after Q K^T and after the softmax."""
+    monkeypatch.setenv("XTILE_AMD_JIT_CACHE", str(tmp_path))
+    xt.plan(K.attention(1000, 64, 64, 64, 64))  # a grid no other test plans: compiled here, written here
+    (src,) = [f.read_text() for f in tmp_path.glob("*.hip")]
+    assert "// rows 5-10: 4 lanes a row of [64,64], 16 elements a lane, in registers" in src
+    body = src[src.index("xt_fused(FusedArgs a)"):]
+    assert body.count("xbar();") == 3 and "__syncthreads" not in body
+
+
 def test_interpreter_programs_and_lds_budget(monkeypatch):
     assert xt.plan(K.layernorm(128, 64, 64))["kernel"].startswith("fused f32 tile=64x64 threads=32x16 vw=4 insts=17")
     assert xt.plan(K.layernorm(8192, 4096, 1))["kernel"].startswith("fused f32 tile=1x4096 threads=1x512 vw=4")

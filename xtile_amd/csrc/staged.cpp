@@ -126,7 +126,7 @@ class StagedGen {
     auto barrier_before = [&](int next) {
       if (prev < 0) return;
       if (vm_.inst[prev].op == VmOp::Store && vm_.inst[next].op == VmOp::Store) return;
-      b << "  __syncthreads();\n";
+      b << "  xbar();\n";
     };
     while (i < n) {
       const VmInst& in = vm_.inst[i];
@@ -155,6 +155,11 @@ class StagedGen {
         continue;
       }
       barrier_before(i);
+      // the step: instruction i, or the row segment or elementwise chain that starts there
+      const int seg = row_segment_end(i);
+      const int end = seg > i ? seg
+                      : (in.op == VmOp::Unary || in.op == VmOp::Binary) ? ew_chain_end(i)
+                                                                         : i;
       // deferred loads written in this step: before their first reader's
       // barrier, or (written in the reader's own step) behind one more
       bool wrote = false;
@@ -162,14 +167,19 @@ class StagedGen {
         if (vm_.inst[k].op == VmOp::Load && deferred(k) && vals_[rd_[k].dst].alloc_at == i) {
           emit_load_write(b, k);
           const auto& us = vals_[rd_[k].dst].users;
-          wrote = wrote || *std::min_element(us.begin(), us.end()) == i;
+          wrote = wrote || *std::min_element(us.begin(), us.end()) <= end;
         }
-      if (wrote) b << "  __syncthreads();\n";
+      if (wrote) b << "  xbar();\n";
+      if (seg > i) {
+        emit_rows(b, i, end);
+        prev = end;
+        i = end + 1;
+        continue;
+      }
       switch (in.op) {
         case VmOp::Store: emit_store(b, i); break;
         case VmOp::Unary:
         case VmOp::Binary: {
-          const int end = ew_chain_end(i);
           emit_elementwise(b, i, end);
           i = end;  // the run's later instructions are done
           break;
@@ -191,7 +201,15 @@ class StagedGen {
       << "typedef int xi4v __attribute__((ext_vector_type(4)));\n"
       << "typedef _Float16 xh8 __attribute__((ext_vector_type(8)));\n"
       << "typedef short xs8 __attribute__((ext_vector_type(8)));\n"
-      << "typedef __bf16 xb8 __attribute__((ext_vector_type(8)));\n";
+      << "typedef __bf16 xb8 __attribute__((ext_vector_type(8)));\n"
+      // a workgroup barrier that orders LDS only: the program's global
+      // accesses need no ordering between waves (no memref is loaded after
+      // the program stores to it), and a load still in flight (a deferred
+      // load's registers) is not waited for here
+      << "__device__ __forceinline__ void xbar() {\n"
+      << "  __builtin_amdgcn_fence(__ATOMIC_RELEASE, \"workgroup\", \"local\");\n"
+      << "  __builtin_amdgcn_s_barrier();\n"
+      << "  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"workgroup\", \"local\");\n}\n";
     k << "extern \"C\" __global__ void __launch_bounds__(" << kThreads << ") xt_fused(FusedArgs a) {\n"
       << "#pragma clang fp contract(off)\n"
       << "  __shared__ __attribute__((aligned(16))) float S[" << std::max(4LL, high_) << "];\n"
@@ -971,6 +989,225 @@ class StagedGen {
           else o << "      S[" << phys(D, "e") << "] = ov;\n";
         });
     b << "  }\n";
+  }
+
+  // A row segment: a run of instructions over one [R, C] tile and its row
+  // vectors ([R, 1]), column vectors ([1, C]) and scalars - elementwise ops
+  // and reductions along rows, as in a softmax or a normalisation - computed
+  // in registers with G lanes a row and CPL = C / G contiguous elements a
+  // lane: the segment's inputs are read from LDS once, row reductions
+  // combine a lane's elements in order and then the row's lanes by a
+  // shuffle butterfly, and only values read after the segment are written
+  // back.  One step instead of a barrier-separated step per instruction.
+  //
+  // Kind of an operand of dims d: 0 the tile, 1 a row vector, 2 a column
+  // vector, 3 a scalar, -1 none of them.
+  static int seg_kind(const int d[3], int R, int C) {
+    if (d[0] != 1) return -1;
+    if (d[1] == R && d[2] == C) return 0;
+    if (d[1] == R && d[2] == 1) return 1;
+    if (d[1] == 1 && d[2] == C) return 2;
+    if (d[1] == 1 && d[2] == 1) return 3;
+    return -1;
+  }
+  bool seg_ok(int i, int R, int C) const {
+    const VmInst& in = vm_.inst[i];
+    if (in.op == VmOp::Reduce) return in.aux[0] == 1 && seg_kind(in.dims, R, C) == 0;
+    const int kd = seg_kind(in.dims, R, C);
+    if (kd != 0 && kd != 1) return false;
+    if (in.op == VmOp::Unary) return true;  // its operand has the result's shape
+    if (in.op != VmOp::Binary) return false;
+    const int ka = seg_kind(in.lhs, R, C), kb = seg_kind(in.aux, R, C);
+    if (ka < 0 || kb < 0) return false;
+    return kd == 0 || ((ka == 1 || ka == 3) && (kb == 1 || kb == 3));
+  }
+  // lanes a row: the fewest that give the 256 threads a row each, with at
+  // most 32 elements a lane; 0 when the row does not split evenly
+  static int seg_lanes(int R, int C) {
+    int G = 1;
+    while (G < 64 && ((long long)R * G < kThreads || C / G > 32)) G *= 2;
+    return C % G == 0 ? G : 0;
+  }
+  // The last instruction of the row segment that starts at i (i itself when
+  // none does: a segment holds a row reduction and another instruction).
+  int row_segment_end(int i) const {
+    const VmInst& in = vm_.inst[i];
+    int R, C;
+    if (in.op == VmOp::Reduce) {
+      if (in.aux[0] != 1 || in.dims[0] != 1) return i;
+      R = in.dims[1];
+      C = in.dims[2];
+    } else if ((in.op == VmOp::Unary || in.op == VmOp::Binary) && in.dims[0] == 1) {
+      R = in.dims[1];
+      C = in.dims[2];
+    } else {
+      return i;
+    }
+    if (C < 2 || !seg_ok(i, R, C) || seg_lanes(R, C) == 0) return i;
+    const int n = static_cast<int>(vm_.inst.size());
+    int end = i;
+    while (end + 1 < n && seg_ok(end + 1, R, C)) ++end;
+    // a deferred load written inside the segment must not be read there
+    for (bool again = true; again && end > i;) {
+      again = false;
+      for (int k = 0; k < n; ++k) {
+        if (vm_.inst[k].op != VmOp::Load || !deferred(k)) continue;
+        const Val& v = vals_[rd_[k].dst];
+        const int first = *std::min_element(v.users.begin(), v.users.end());
+        if (v.alloc_at > i && v.alloc_at <= end && first <= end) {
+          end = v.alloc_at - 1;
+          again = true;
+        }
+      }
+    }
+    // registers: every tile value of the segment, CPL floats each
+    const int cpl = C / seg_lanes(R, C);
+    int tiles = 0;
+    std::vector<int> seen;
+    for (int j = i; j <= end; ++j) {
+      for (int v : {rd_[j].a, rd_[j].b, rd_[j].dst})
+        if (v >= 0 && std::find(seen.begin(), seen.end(), v) == seen.end()) {
+          seen.push_back(v);
+          if (vals_[v].numel == (long long)R * C && R > 1) ++tiles;
+        }
+      if (tiles * cpl > 160) {
+        end = j - 1;
+        break;
+      }
+    }
+    bool has_reduce = false;
+    for (int j = i; j <= end; ++j) has_reduce |= vm_.inst[j].op == VmOp::Reduce;
+    return has_reduce && end > i ? end : i;
+  }
+
+  void emit_rows(std::ostringstream& b, int i0, int i1) {
+    const VmInst& first = vm_.inst[i0];
+    const int R = first.dims[1], C = first.dims[2];
+    const int G = seg_lanes(R, C), cpl = C / G, rows_per = kThreads / G;
+    const long long passes = (R + rows_per - 1) / rows_per;
+    b << "  // rows " << i0 << "-" << i1 << ": " << G << " lanes a row of [" << R << "," << C << "], " << cpl
+      << " elements a lane, in registers\n  {\n";
+    b << "    const int g = t % " << G << ", r0 = t / " << G << ", c0 = g * " << cpl << ";\n";
+    b << "#pragma unroll 1\n    for (int p = 0; p < " << passes << "; ++p) {\n      const int r = r0 + p * "
+      << rows_per << ";\n";
+    b << (R % rows_per ? "      if (r < " + S(R) + ") {\n" : "      {\n");
+    // register names: tiles and column vectors arrays of cpl, row vectors and scalars one float
+    std::map<int, std::string> name;
+    std::map<int, int> kind;
+    auto defined_here = [&](int v) { return vals_[v].def >= i0 && vals_[v].def <= i1; };
+    auto in_name = [&](int v, const int* d) -> std::string {
+      auto it = name.find(v);
+      if (it != name.end()) return it->second;
+      const int k = seg_kind(d, R, C);
+      const std::string nm = "w" + S(v);
+      name[v] = nm;
+      kind[v] = k;
+      const Val& V = vals_[v];
+      if (k == 0 || k == 2) {
+        const std::string lin0 = k == 0 ? "r * " + S(C) + " + c0" : "c0";
+        b << "        float " << nm << "[" << cpl << "];\n";
+        if (cpl % 4 == 0 && V.src < 0 && vec4(V))
+          b << "#pragma unroll\n        for (int c = 0; c < " << cpl << "; c += 4) {\n          const xf4 q4 = "
+            << "*reinterpret_cast<const xf4*>(&S[" << phys(V, lin0 + " + c") << "]);\n          " << nm << "[c] = q4[0]; "
+            << nm << "[c + 1] = q4[1]; " << nm << "[c + 2] = q4[2]; " << nm << "[c + 3] = q4[3];\n        }\n";
+        else
+          b << "#pragma unroll\n        for (int c = 0; c < " << cpl << "; ++c) " << nm << "[c] = "
+            << elem(v, lin0 + " + c") << ";\n";
+      } else {
+        b << "        const float " << nm << " = " << elem(v, k == 1 ? "r" : "0") << ";\n";
+      }
+      return nm;
+    };
+    // inputs first: every LDS read of the pass before any write
+    for (int i = i0; i <= i1; ++i) {
+      const VmInst& in = vm_.inst[i];
+      const Reads& r = rd_[i];
+      const int* ad = in.op == VmOp::Binary ? in.lhs : in.dims;
+      if (!defined_here(r.a)) in_name(r.a, ad);
+      if (in.op == VmOp::Binary && !defined_here(r.b)) in_name(r.b, in.aux);
+    }
+    auto at = [&](int v, const std::string& c) {
+      const std::string& nm = name.at(v);
+      return kind.at(v) == 0 || kind.at(v) == 2 ? nm + "[" + c + "]" : nm;
+    };
+    for (int i = i0; i <= i1; ++i) {
+      const VmInst& in = vm_.inst[i];
+      const Reads& r = rd_[i];
+      const std::string nm = "w" + S(r.dst);
+      if (in.op == VmOp::Reduce) {
+        const bool mx = in.kind == 1;
+        auto comb = [&](const std::string& p, const std::string& q) {
+          return mx ? "fmaxf(" + p + ", " + q + ")" : p + " + " + q;
+        };
+        b << "        float " << nm << " = " << (mx ? "-__builtin_huge_valf()" : "0.0f") << ";\n"
+          << "#pragma unroll\n        for (int c = 0; c < " << cpl << "; ++c) " << nm << " = "
+          << comb(nm, at(r.a, "c")) << ";\n";
+        for (int o = G / 2; o > 0; o /= 2)
+          b << "        " << nm << " = " << comb(nm, "__shfl_xor(" + nm + ", " + S(o) + ", " + S(G) + ")") << ";\n";
+        name[r.dst] = nm;
+        kind[r.dst] = 1;
+        continue;
+      }
+      const int kd = seg_kind(in.dims, R, C);
+      std::string expr;
+      auto fx = [&](const std::string& c) {
+        if (in.op == VmOp::Binary) {
+          const char* op = in.kind == 0 ? " + " : in.kind == 1 ? " - " : " * ";
+          return at(r.a, c) + op + at(r.b, c);
+        }
+        return unary_formula(in.kind, at(r.a, c));
+      };
+      if (kd == 0)
+        b << "        float " << nm << "[" << cpl << "];\n#pragma unroll\n        for (int c = 0; c < " << cpl
+          << "; ++c) " << nm << "[c] = " << fx("c") << ";\n";
+      else
+        b << "        const float " << nm << " = " << fx("0") << ";\n";
+      name[r.dst] = nm;
+      kind[r.dst] = kd == 0 ? 0 : 1;
+    }
+    // values read after the segment go back to LDS
+    for (int i = i0; i <= i1; ++i) {
+      const int v = rd_[i].dst;
+      const Val& D = vals_[v];
+      bool later = false;
+      for (int u : D.users) later |= u > i1;
+      if (!later) continue;
+      const std::string& nm = name.at(v);
+      if (kind.at(v) == 0) {
+        const std::string lin0 = "r * " + S(C) + " + c0";
+        if (cpl % 4 == 0 && vec4(D))
+          b << "#pragma unroll\n        for (int c = 0; c < " << cpl << "; c += 4) *reinterpret_cast<xf4*>(&S["
+            << phys(D, lin0 + " + c") << "]) = xf4{" << nm << "[c], " << nm << "[c + 1], " << nm << "[c + 2], " << nm
+            << "[c + 3]};\n";
+        else
+          b << "#pragma unroll\n        for (int c = 0; c < " << cpl << "; ++c) S[" << phys(D, lin0 + " + c") << "] = "
+            << nm << "[c];\n";
+      } else {
+        b << "        if (g == 0) S[" << phys(D, "r") << "] = " << nm << ";\n";
+      }
+    }
+    b << "      }\n    }\n  }\n";
+    // deferred loads whose slot opens inside the segment (their readers come
+    // after it): written now, behind a barrier when the slot overlaps
+    // anything the segment read from LDS
+    bool fenced = false;
+    for (int k = 0; k < i0; ++k) {
+      if (vm_.inst[k].op != VmOp::Load || !deferred(k)) continue;
+      const Val& L = vals_[rd_[k].dst];
+      if (L.alloc_at <= i0 || L.alloc_at > i1) continue;
+      const long long lo = L.off, hi = L.off + L.floats();
+      bool overlap = false;
+      for (const auto& kv : name) {
+        if (defined_here(kv.first)) continue;
+        const Val& V = vals_[storage_of(kv.first)];
+        if (V.off < hi && lo < V.off + V.floats()) overlap = true;
+      }
+      if (overlap && !fenced) {
+        b << "  xbar();\n";
+        fenced = true;
+      }
+      emit_load_write(b, k);
+    }
   }
 
   void emit_reduce(std::ostringstream& b, int i) {
