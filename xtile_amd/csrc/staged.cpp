@@ -8,11 +8,12 @@
 // live in LDS, as f32 (as the interpreter and the oracle hold them) or, for
 // f16 / bf16 tiles as loaded whose every reader is an MFMA operand, as their
 // 16-bit patterns; every instruction is straight-line code with its shapes,
-// strides and tile origins as compile-time constants, and a barrier separates
-// an instruction from the next one that reads what it wrote or writes where
-// it read.  The global reads of a run of loads are issued together; the LDS
-// write of a load whose first reader comes later waits in registers until
-// that reader (so its LDS is not held meanwhile).
+// strides and tile origins as compile-time constants, and a barrier (one
+// that orders LDS only) separates an instruction from the next one that
+// reads what it wrote or writes where it read.  The global reads of a run of
+// loads are issued together; the LDS write of a load whose first reader
+// comes later waits in registers until that reader (so its LDS is not held
+// meanwhile).
 //   * matmul / mma: 32 x 32 output tiles dealt over the four waves, K in MFMA
 //     steps: v_mfma_f32_32x32x16_f16 / _bf16 when both operands are f16 / bf16
 //     tiles as loaded (or transposed / permuted: the values are then exact in
@@ -26,7 +27,10 @@
 //     the matmul reads its source through the permutation.  Other permutes
 //     copy, one thread per output element.
 //   * reductions along a row: a power-of-two group of lanes per row with a
-//     shuffle butterfly; along a column: one thread per column.
+//     shuffle butterfly; along a column: one thread per column.  A run of
+//     row reductions and the elementwise ops around them over one [R, C]
+//     tile (a softmax, a normalisation) is one step in registers (a row
+//     segment, emit_rows).
 //   * elementwise ops: every LDS read of a chunk of elements before its
 //     writes, four elements at a time where the layouts allow.
 //
@@ -1293,8 +1297,12 @@ class StagedGen {
     const Val& D = vals_[r.dst];
     const int M = in.dims[1], N = in.dims[2], K = in.aux[0];
     const int mode = r.mode;
-    // K elements per MFMA and per lane
-    const int KB = mode == kMmF32 ? 2 : mode == kMmI8 ? 32 : 16, KL = KB / 2;
+    // K elements per step and per lane.  An f32 step is four MFMAs of K = 2:
+    // lane half h takes k = 8 s + 4 h + j into MFMA j (the order of the sum
+    // over k is free, and A and B use the same order), so a lane reads its A
+    // row's four floats with one 16-byte read (conflict-free at A's pitch of
+    // 4 mod 8 floats) instead of four single floats.
+    const int KB = mode == kMmF32 ? 8 : mode == kMmI8 ? 32 : 16, KL = KB / 2;
     const int MT = (M + 31) / 32, NT = (N + 31) / 32, steps = (K + KB - 1) / KB;
     const bool mg = M % 32 != 0, ng = N % 32 != 0, kg = K % KB != 0;
     const bool narrow = mode == kMmF16 || mode == kMmBF16;
@@ -1385,8 +1393,9 @@ class StagedGen {
       const std::string acc = "acc" + S(p % 2);
       switch (mode) {
         case kMmF32:
-          o << "        " << acc << " = __builtin_amdgcn_mfma_f32_32x32x2f32(" << FA << "[0], " << FB << "[0], " << acc
-            << ", 0, 0, 0);\n";
+          for (int j = 0; j < KL; ++j)
+            o << "        acc" << j % 2 << " = __builtin_amdgcn_mfma_f32_32x32x2f32(" << FA << "[" << j << "], " << FB
+              << "[" << j << "], acc" << j % 2 << ", 0, 0, 0);\n";
           break;
         case kMmF16:
           o << "        " << acc << " = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(xh8, " << FA
@@ -1411,15 +1420,14 @@ class StagedGen {
       return o.str();
     };
     // A ring of NS fragment sets: the reads of steps s + 1 .. s + NS - 1 are
-    // in flight while step s's MFMA runs (an f32 step is one 64-cycle MFMA
-    // on two floats a lane, so it reads furthest ahead).  The loop runs the
+    // in flight while step s's MFMAs run.  The loop runs the
     // groups of NS steps whose look-ahead reads stay within K, with no branch
     // in its body (the compiler waits for every LDS read at a block
     // boundary); the last steps follow unrolled, reading ahead only while
     // steps remain.  Scheduling fences keep each step's look-ahead reads
     // ahead of its MFMA (left alone, the compiler sinks them next to their
     // use).  NS is even, so set j always holds steps of parity j % 2.
-    int NS = std::max(1, std::min(steps, mode == kMmF32 ? 8 : 4));
+    int NS = std::max(1, std::min(steps, 4));
     if (NS > 1 && NS % 2) --NS;
     for (int q = 0; q < NS; ++q) {
       if (narrow) b << "      xs8 fa" << q << ", fb" << q << ";\n";
