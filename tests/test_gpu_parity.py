@@ -262,14 +262,17 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
         (3, 9, 9, 1024, 48, 1, 1, 3, 9, (0, 0, 0, 0), (1, 1), (1, 1), "f16"),      # 1 x 1, Cout 48
         (1, 11, 13, 24, 200, 5, 5, 11, 13, (2, 2, 2, 2), (1, 1), (1, 1), "bf16"),  # Cin 24, Cout 200 (4 tiles, last 8 wide)
         (24, 14, 14, 512, 512, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # 148 tiles, 144 stages: K in halves
+        (2, 10, 10, 192, 256, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # deep: 64 x 128 tiles, 3 128-byte stages a tap
+        (8, 14, 14, 256, 256, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),  # C9's layer at batch 8: 50 deep tiles, K split
     ],
 )
 def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
     """Filters too large for the band kernel's LDS (Cin * Cout * taps * 2
     bytes above ~150 KB) with Cout a multiple of 64 take the implicit-GEMM
     kernel (conv_igemm.hip; 128 x 128 tiles for Cout a multiple of 128, else
-    256 x 64): operands by DMA, the input gathered per tap, padding and rows
-    past M read as zeros."""
+    256 x 64, and 64 x 128 tiles with 128-byte K stages for deep layers whose
+    128 x 128 tiles would fill at most half the CUs): operands by DMA, the
+    input gathered per tap, padding and rows past M read as zeros."""
     rng = np.random.default_rng(9)
     mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
                    pad=pad, stride=stride, dilation=dil)
@@ -335,6 +338,7 @@ def test_conv2d_igemm_k_split_in_a_graph(cuda):
         (1, 32, 64, 128, 64, 3, 3, 32, 64, (1, 1, 1, 1), (1, 1), "1"),  # kernels/conv2d.py, implicit GEMM first
         (2, 10, 10, 48, 80, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), "0"),    # Cin 48 padded to 64, Cout 80 (two tiles)
         (2, 12, 12, 272, 16, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), "0"),   # Cin 272 = 4 stages + 16, Cout 16
+        (2, 9, 9, 384, 128, 3, 3, 9, 9, (1, 1, 1, 1), (1, 1), "0"),     # deep: 64 x 128 tiles, three 128-channel stages a tap
     ],
 )
 def test_conv2d_igemm_i8_bit_exact(cuda, monkeypatch, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, first):

@@ -22,17 +22,21 @@
 //     v_mfma_f32_32x32x16_{f16,bf16}, f32 sums, or v_mfma_i32_32x32x32_i8,
 //     exact i32 sums rounded to f32 once); 64 or 80 KB of LDS, so two
 //     workgroups share a CU and one's barrier waits are the other's MFMA time.
-//   * A K stage is 64 bytes of one tap's channels in every pixel row (32
-//     f16 / bf16 or 64 i8 channels; a tap's last stage is padded with zeros
-//     when Cin is not a multiple of that, and a channel tile past Cout reads
-//     zeros and is not stored):
-//     A [BM rows][64 B] is an im2col gather done by the DMA itself: lane L of
-//     A instruction i fetches 16 bytes of pixel row 16 i + L/4 at the tap's
-//     source position, or, outside the image (padding) or past M, an offset
-//     past the buffer's end, which the DMA writes as zeros.  B [64 / esize
-//     k][BN esize B] holds the stage's filter rows for BN output channels.
+//     Deep layers, whose 128 x 128 tiles would fill at most half the CUs,
+//     take 64 x 128 tiles of four 32 x 64 waves with 128-byte stages (96 KB).
+//   * A K stage is KB = 64 (or 128) bytes of one tap's channels in every
+//     pixel row (32 f16 / bf16 or 64 i8 channels a 64-byte stage; a tap's
+//     last stage is padded with zeros when Cin is not a multiple of that, and
+//     a channel tile past Cout reads zeros and is not stored):
+//     A [BM rows][KB] is an im2col gather done by the DMA itself: lane L of
+//     A instruction i fetches 16 bytes of pixel row (1024 / KB) i + L / (KB /
+//     16) at the tap's source position, or, outside the image (padding) or
+//     past M, an offset past the buffer's end, which the DMA writes as zeros.
+//     B [KB / esize k][BN esize B] holds the stage's filter rows for BN
+//     output channels.
 //   * LDS layouts as in the DMA GEMM (gemm.hip): A row r keeps its 16-byte
-//     chunk c at c ^ ((r >> 2) & 3), B row k at c ^ ig_bsw(k); A fragments are
+//     chunk c at c ^ ((r / (256 / KB)) % (KB / 16)), B row k at c ^
+//     ig_bsw(k); A fragments are
 //     ds_read_b128, B fragments ds_read_b64_tr_b16 / _tr_b8 (K-contiguous
 //     lanes from the channel-contiguous filter rows).
 //   * Four stages in LDS, three in flight (the pipeline is described at the
@@ -71,8 +75,8 @@ struct IgArgs {
   int OH, OW;
   int pad_t, pad_l, sh, sw, dh, dw;
   int M;        // N * OH * OW
-  int stages;   // K * esize / 64: 64 bytes of one tap's channels each
-  int cs;       // stages per tap: C * esize / 64
+  int stages;   // stages of KB bytes of one tap's channels (64 or 128)
+  int cs;       // stages per tap: C * esize / KB, rounded up
   int ntiles;   // channel tiles: CO / BN
   int tiles;    // ceil(M / BM) * ntiles
   int ksplit;   // K ranges per tile (1: one workgroup per tile)
@@ -119,10 +123,12 @@ __device__ __forceinline__ int ig_bsw(int k) {
   else return BR == 128 ? (k >> 1) & 3 : (k >> 2) & 1;
 }
 
-// BM x BN workgroup tiles, four waves in a WGM x (4 / WGM) layout of 64 x 64
-// wave tiles: (BM, BN) = (128, 128) with 2 x 2 waves or (256, 64) with 4 x 1.
-template <int ELEM, int BM, int BN>
-__global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
+// BM x BN workgroup tiles, four waves in a WGM x (4 / WGM) layout of WTM x
+// WTN wave tiles: (BM, BN) = (128, 128) with 2 x 2 waves of 64 x 64, (256,
+// 64) with 4 x 1, or (64, 128) with 2 x 2 waves of 32 x 64.  A K stage is KBY
+// bytes of one tap's channels (64, or 128 for the 64 x 128 tiles).
+template <int ELEM, int BM, int BN, int WTM = 64, int WTN = 64, int KBY = 64>
+__global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
   // stages in LDS (64 or 80 KB, two workgroups a CU): five, or a pipeline
   // that also read each stage's fragments during the previous stage's MFMAs
   // and spread the DMA over them, measured slower on 3 x 3 convs with 128 to
@@ -131,16 +137,21 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   // left 32 x 14^2 x 256 -> 256 unchanged (29.0 / 30.4 us)
   constexpr int NS = 4;
   constexpr int ES = ELEM == kIgI8 ? 1 : 2;  // bytes per element
-  // a stage is 64 bytes of K: 32 f16 / bf16 or 64 i8 channels; a K step of
-  // the MFMAs is 32 bytes (KSR filter rows)
-  constexpr int KB = 64, AB = BM * KB, BR = BN * ES, KR = 64 / ES, KSR = 32 / ES;
-  constexpr int STAGE = AB + KR * BR;  // 16 KB or 20 KB
+  // a stage is KB bytes of K (KB / esize channels of one tap); a K step of
+  // the MFMAs is 32 bytes (KSR filter rows), KSTEPS of them a stage.  A DMA
+  // instruction fills RA pixel rows of CA 16-byte chunks; a row keeps its
+  // chunk c at c ^ ((r / SWD) % CA), so that the 16 rows one 16-lane group
+  // of a fragment read covers fall in distinct bank groups of the 256-byte
+  // bank window.
+  constexpr int KB = KBY, AB = BM * KB, BR = BN * ES, KR = KB / ES, KSR = 32 / ES, KSTEPS = KB / 32;
+  constexpr int RA = 1024 / KB, CA = KB / 16, SWD = 256 / KB;
+  constexpr int STAGE = AB + KR * BR;  // 16, 20 or 24 KB
   typedef typename IgAcc<ELEM>::type acc_t;
-  constexpr int WGM = BM / 64, WGN = 4 / WGM;
-  static_assert(WGM * WGN == 4 && BN == 64 * WGN, "wave layout");
-  constexpr int MI = 2, NI = 2;
-  constexpr int PA = BM / 64;        // A DMA instructions per wave and stage (16 rows each)
-  constexpr int PB = BN / 64;        // B DMA instructions per wave and stage
+  constexpr int WGM = BM / WTM, WGN = 4 / WGM;
+  static_assert(WGM * WGN == 4 && BN == WTN * WGN, "wave layout");
+  constexpr int MI = WTM / 32, NI = WTN / 32;
+  constexpr int PA = BM * KB / 4096;  // A DMA instructions per wave and stage (RA rows each)
+  constexpr int PB = BN * KB / 4096;  // B DMA instructions per wave and stage
   constexpr int PER = PA + PB;       // DMA instructions per wave and stage
   constexpr int CPR = BR / 16, RPI = 1024 / BR;  // B chunks per row, rows per DMA instruction
   typedef __attribute__((address_space(3))) unsigned char lds_t;
@@ -165,19 +176,21 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   const i32x4 ra = raw_rsrc(p.src, p.src_bytes), rb = raw_rsrc(p.filt, p.filt_bytes);
   const unsigned ldb = (unsigned)(p.CO * ES);
 
-  // A: this wave's instructions PA wave + q cover pixel rows 16 (PA wave + q)
-  // + lane / 4; the lane fetches global chunk (lane % 4) ^ ((lane / 16) % 4)
-  // of the stage's 64 bytes, which lands at LDS chunk lane % 4 of its row.
+  // A: this wave's instruction PA wave + q covers pixel rows RA (PA wave + q)
+  // + lane / CA; the lane fetches global chunk (lane % CA) ^ ((row / SWD) %
+  // CA) of the stage's KB bytes, which lands at LDS chunk lane % CA of its row.
   int ih0[PA], iw0[PA];
   unsigned abase[PA];
   // channel of the lane's 16 bytes within a stage (a stage past the last
   // channel reads zeros: channels are padded to whole stages per tap)
-  const int ach = ((lane & 3) ^ ((lane >> 4) & 3)) * (16 / ES);
+  int ach[PA];
   {
-    const unsigned gc = (unsigned)((lane & 3) ^ ((lane >> 4) & 3));
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
-      const int pix = m0 + 16 * (PA * wave + q) + (lane >> 2);
+      const int arow_q = RA * (PA * wave + q) + lane / CA;
+      const unsigned gc = (unsigned)((lane % CA) ^ ((arow_q / SWD) & (CA - 1)));
+      ach[q] = (int)gc * (16 / ES);
+      const int pix = m0 + arow_q;
       if (pix < p.M) {
         const int n = (int)p.d_ohw((unsigned)pix);
         const int rem = pix - n * p.OH * p.OW;
@@ -216,7 +229,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   auto tap_begin = [&]() {
     dih = lkh * p.dh;
     diw = lkw * p.dw;
-    soff = (unsigned)((dih * p.W + diw) * p.C * ES + lcc * 64);
+    soff = (unsigned)((dih * p.W + diw) * p.C * ES + lcc * KB);
   };
   // DMA instruction q of the stage being loaded (A for q < PA, then B)
   auto dma_one = [&](unsigned char* S, int q) {
@@ -224,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
     if (q < PA) {
       const int i = PA * wave + q;
       const bool in = (unsigned)(ih0[q] + dih) < (unsigned)p.H && (unsigned)(iw0[q] + diw) < (unsigned)p.W &&
-                      c0 + ach < p.C;
+                      c0 + ach[q] < p.C;
       dma16(ra, lds_addr(S + i * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
     } else {
       // filter rows tap * C + c0 + RPI i + brow (rows past the tap's
@@ -235,7 +248,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
             (unsigned)((lkh * p.KW + lkw) * p.C + c0 + RPI * i) * ldb);
     }
   };
-  // after a stage's DMA: the next 32 channels, then the next tap
+  // after a stage's DMA: the next KR channels, then the next tap
   auto tap_next = [&]() {
     ++lkt;
     if (++lcc == p.cs) {
@@ -253,16 +266,16 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
     tap_next();
   };
 
-  // fragment offsets (as in the DMA GEMM): A row r at r * 64, chunk c at
-  // c ^ ((r >> 2) & 3); B tile j, read h at boff[j][h] in the stage's first
-  // K step, KSR rows further for the second
+  // fragment offsets (as in the DMA GEMM): A row r at r * KB, chunk c at
+  // c ^ ((r / SWD) % CA); B tile j, read h at boff[j][h] in the stage's first
+  // K step, KSR rows further for each later one
   const int lrow = lane & 31, hi = lane >> 5;
   int arow[MI], asw[MI], boff[NI][2];
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-    const int r = wm * 64 + i * 32 + lrow;
+    const int r = wm * WTM + i * 32 + lrow;
     arow[i] = r * KB;
-    asw[i] = (r >> 2) & 3;
+    asw[i] = (r / SWD) & (CA - 1);
   }
   {
     const int g = lane >> 4, li = lane & 15;
@@ -273,10 +286,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
         int k, cb;
         if constexpr (ES == 2) {
           k = 8 * (g >> 1) + 4 * h + (li >> 2);
-          cb = (wn * 64 + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
+          cb = (wn * WTN + j * 32 + 16 * (g & 1) + 4 * (li & 3)) * 2;
         } else {
           k = 16 * (g >> 1) + 8 * h + (li >> 1);
-          cb = wn * 64 + j * 32 + 16 * (g & 1) + 8 * (li & 1);
+          cb = wn * WTN + j * 32 + 16 * (g & 1) + 8 * (li & 1);
         }
         boff[j][h] = AB + k * BR + (((cb >> 4) ^ ig_bsw<ES, BR>(k)) << 4) + (cb & 15);
       }
@@ -290,9 +303,9 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
   auto compute = [&](const unsigned char* S) {
-    uint4v af[2][MI], bf[2][NI];
+    uint4v af[KSTEPS][MI], bf[KSTEPS][NI];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
       for (int i = 0; i < MI; ++i)
         af[ks][i] = *reinterpret_cast<const uint4v*>(S + arow[i] + (((ks * 2 + hi) ^ asw[i]) << 4));
@@ -315,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -348,10 +361,10 @@ __global__ __launch_bounds__(256, 2) void conv_igemm_kernel(IgArgs p) {
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + lrow;
+      const int col = n0 + wn * WTN + j * 32 + lrow;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+        const int row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
         // through a scalar (a bit-cast of an ext_vector element lvalue reads
         // element 0); an i8 sum is an exact i32, rounded to f32 once
         const float x = static_cast<float>(acc[i][j][v]);
@@ -430,23 +443,33 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.dh = (int)c.dil_h;
   a.dw = (int)c.dil_w;
   a.M = (int)M;
-  a.cs = (int)((c.C * es + 63) / 64);
-  a.stages = (int)(c.KH * c.KW) * a.cs;
-  // 128 x 128 tiles when Cout allows, else 256 x 64
-  const bool wide = c.CO % 128 == 0;
-  const int bm = wide ? 128 : 256, bn = wide ? 128 : 64;
-  a.ntiles = (int)((c.CO + bn - 1) / bn);
-  const long long tiles = (M + bm - 1) / bm * a.ntiles;
-  // K split when the tiles fill at most half the CUs (f16 / bf16: i8 sums stay
-  // exact and whole): up to one workgroup a CU, at least 16 stages each.
-  // Measured (batch 32, 3 x 3): 7 x 7 x 512 -> 512 (52 tiles) 56.9 us whole,
-  // 27.7 split in 4; 14 x 14 x 256 -> 256 (98 tiles) 31.3 / 27.9 in 2; 28 x 28
-  // x 128 -> 128 (196 tiles) 19.8 whole, 33.0 in 2 (the zero fill and the
-  // atomic adds of the output cost more than the idle CUs)
   int cus = 256, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
     cus = 256;
+  // 128 x 128 tiles when Cout allows, else 256 x 64.  When the 128 x 128
+  // tiles would fill at most half the CUs (deep layers) and a tap's channels
+  // are whole 128-byte stages: 64 x 128 tiles with 128-byte stages (twice
+  // the tiles, half the stages and barriers).  Measured on 32 x 14^2 x 256
+  // -> 256, 3 x 3 (one call, 500 launches each): 98 tiles of 128 x 128 split
+  // in two 29.7-31.2 us, 196 of 64 x 128 with 64-byte stages 27.9, with
+  // 128-byte stages 22.9-24.7 (six stages in LDS 25.2, two 23.2, 256-byte
+  // stages 23.0; 392 tiles of 64 x 64 23.7).
+  const bool wide = c.CO % 128 == 0;
+  const long long tiles128 = (M + 127) / 128 * ((c.CO + 127) / 128);
+  const bool deep = wide && tiles128 * 2 <= cus && (c.C * es) % 128 == 0;
+  const int bm = deep ? 64 : wide ? 128 : 256, bn = wide ? 128 : 64, kb = deep ? 128 : 64;
+  a.cs = (int)((c.C * es + kb - 1) / kb);
+  a.stages = (int)(c.KH * c.KW) * a.cs;
+  a.ntiles = (int)((c.CO + bn - 1) / bn);
+  const long long tiles = (M + bm - 1) / bm * a.ntiles;
+  // K split when the tiles fill at most half the CUs (f16 / bf16: i8 sums stay
+  // exact and whole): up to one workgroup a CU, at least 16 stages each.
+  // Measured (batch 32, 3 x 3, 128 x 128 tiles): 7 x 7 x 512 -> 512 (52
+  // tiles) 56.9 us whole, 27.7 split in 4; 14 x 14 x 256 -> 256 (98 tiles)
+  // 31.3 / 27.9 in 2; 28 x 28 x 128 -> 128 (196 tiles) 19.8 whole, 33.0 in 2
+  // (the zero fill and the atomic adds of the output cost more than the idle
+  // CUs)
   // (XTILE_AMD_KSPLIT=0 keeps every tile whole.)  Ranges are spread evenly:
   // their lengths differ by at most one stage.
   long long ksplit = 1;
@@ -471,8 +494,9 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   const int el = i8 ? kIgI8 : c.elem == xt::Elem::BF16 ? kIgBF16 : kIgF16;
 #define XT_IG(E)                                                                                       \
   do {                                                                                                 \
-    if (wide) hipLaunchKernelGGL((conv_igemm_kernel<E, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a); \
-    else hipLaunchKernelGGL((conv_igemm_kernel<E, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);       \
+    if (deep) hipLaunchKernelGGL((conv_igemm_kernel<E, 64, 128, 32, 64, 128>), dim3(a.nwg), dim3(256), 0, s, a); \
+    else if (wide) hipLaunchKernelGGL((conv_igemm_kernel<E, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a);      \
+    else hipLaunchKernelGGL((conv_igemm_kernel<E, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);                 \
   } while (0)
   if (el == kIgI8) XT_IG(kIgI8);
   else if (el == kIgBF16) XT_IG(kIgBF16);
