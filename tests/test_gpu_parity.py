@@ -245,6 +245,45 @@ def test_conv2d_general(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, d
 
 
 @pytest.mark.parametrize(
+    "n,h,w,cin,pad,stride,dil,dt",
+    [
+        (32, 56, 56, 64, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # C4: 256 bands of 7 rows, 32 per XCD
+        (2, 14, 14, 64, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),
+        (2, 16, 16, 64, (1, 1, 1, 1), (2, 2), (1, 1), "f16"),    # stride 2
+        (2, 11, 13, 32, (0, 1, 2, 1), (2, 2), (1, 1), "f16"),    # Cin 32 (two K steps a tap), asymmetric pad
+        (2, 12, 12, 32, (2, 2, 2, 2), (1, 1), (2, 2), "bf16"),   # dilation 2
+        (3, 30, 17, 64, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),   # odd width: M tiles cross rows unevenly
+        (1, 100, 9, 32, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),    # one-row bands, a single M tile
+        (4, 40, 120, 64, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # 122-pixel halo rows
+        (1, 5, 300, 64, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),    # 10 M tiles in a one-row band
+    ],
+)
+def test_conv2d_band_kernel_shapes(cuda, n, h, w, cin, pad, stride, dil, dt):
+    """3 x 3 convolutions to 64 channels (f16 / bf16, Cin 32 or 64, Blocks
+    covering the output) on the band kernel: bands dealt to the XCDs in
+    contiguous runs, M tiles that cross output rows unevenly, one-row bands,
+    wide halo rows, strides, dilation and asymmetric padding, against the
+    oracle."""
+    rng = np.random.default_rng(12)
+    kh = kw = 3
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * (kw - 1) - 1) // stride[1] + 1
+    th = next(t for t in (4, 3, 2, 1) if oh % t == 0)
+    mod = K.conv2d(n, h, w, cin, 64, kh, kw, th, ow, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
+                   pad=pad, stride=stride, dilation=dil)
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (kh, kw, cin, 64)).astype(np.float32)
+    if dt == "bf16":
+        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    else:
+        x, f = x.astype(np.float16), f.astype(np.float16)
+    o = np.zeros((n, oh, ow, 64), np.float32)
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda, case=f"conv band {n}x{h}x{w}x{cin}->64 s{stride} d{dil} {dt}")[2]
+    want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+
+
+@pytest.mark.parametrize(
     "n,h,w,cin,cout,kh,kw,th,tw,pad,stride,dil,dt",
     [
         (2, 12, 12, 128, 128, 3, 3, 4, 12, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # 295 KB filter: M 288, 3 tiles
