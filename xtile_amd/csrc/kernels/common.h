@@ -36,17 +36,11 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 // account for these loads themselves (explicit vmcnt waits before their
 // barriers), where the compiler, which cannot tell LDS buffers apart
 // reliably, would wait for every DMA in flight before the next LDS read.
-// M0 carries the LDS address and is restored afterwards.
+// M0 carries the LDS address: an input bound to M0, so the compiler sets it
+// once per DMA (and not at all when it already holds the address) instead of
+// a save / set / restore around every instruction.
 __device__ __forceinline__ void dma16(i32x4 rsrc, unsigned lds, unsigned voff, unsigned soff) {
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-      : "memory");
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds) : "memory");
 }
 
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: expcnt and lgkmcnt fields at

@@ -213,57 +213,66 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
   // (lane % CPR) ^ ig_bsw(k), and ig_bsw(k) depends on lane / CPR only.
   const unsigned vb = (unsigned)(lane / CPR) * ldb + (unsigned)(n0 * ES) +
                       (unsigned)(((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4);
-  // the lane's filter row within a DMA instruction, and whether its 16 bytes
-  // lie within Cout (a tile past Cout reads zeros)
-  const int brow = lane / CPR;
-  const bool bcol = n0 * ES + (((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4) < p.CO * ES;
+  // Channel limits: A instruction q's lane reads channels c0 + ach[q] .. of
+  // a stage whose first channel is c0, B instruction q's lane filter row c0
+  // + RPI (PB wave + q) + lane / CPR; each is in range while c0 is below its
+  // limit (a stage past the last channel, or a column past Cout, reads zeros)
+  int alim[PA], blim[PB];
+#pragma unroll
+  for (int q = 0; q < PA; ++q) alim[q] = p.C - ach[q];
+  {
+    const bool bcol = n0 * ES + (((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4) < p.CO * ES;
+#pragma unroll
+    for (int q = 0; q < PB; ++q) blim[q] = bcol ? p.C - RPI * (PB * wave + q) - lane / CPR : -(1 << 30);
+  }
 
-  // tap state of the next stage to load
+  // DMA state of the next stage to load: its tap (kh, kw), its channel
+  // stage lcc within the tap (first channel c0 = lcc KR), the tap's source
+  // offset soff, filter row krow = tap C + c0, and whether each A
+  // instruction's pixel is inside the image at this tap (recomputed only
+  // when the tap changes; the stages of one tap differ by KB bytes of
+  // source and KR filter rows).
   // this workgroup's stages [s_begin, s_begin + ns)
   const int s_begin = (int)((long long)kr * p.stages / p.ksplit);
-  int lkt = s_begin, lcc = s_begin % p.cs, lkh = 0, lkw = s_begin / p.cs;
+  int lcc = s_begin % p.cs, lkw = s_begin / p.cs, lkh;
   lkh = lkw / p.KW;
   lkw -= lkh * p.KW;
-  int dih = 0, diw = 0;
   unsigned soff = 0;
+  int krow = 0;
+  bool ain[PA];
   auto tap_begin = [&]() {
-    dih = lkh * p.dh;
-    diw = lkw * p.dw;
+    const int dih = lkh * p.dh, diw = lkw * p.dw;
     soff = (unsigned)((dih * p.W + diw) * p.C * ES + lcc * KB);
+    krow = (lkh * p.KW + lkw) * p.C + lcc * KR;
+#pragma unroll
+    for (int q = 0; q < PA; ++q)
+      ain[q] = ((unsigned)(ih0[q] + dih) < (unsigned)p.H) & ((unsigned)(iw0[q] + diw) < (unsigned)p.W);
   };
-  // DMA instruction q of the stage being loaded (A for q < PA, then B)
-  auto dma_one = [&](unsigned char* S, int q) {
+  tap_begin();
+  const unsigned bstep = (unsigned)RPI * ldb;  // filter bytes between B instructions
+  auto dma_stage = [&](unsigned char* S) {
     const int c0 = lcc * KR;  // the stage's first channel
-    if (q < PA) {
-      const int i = PA * wave + q;
-      const bool in = (unsigned)(ih0[q] + dih) < (unsigned)p.H && (unsigned)(iw0[q] + diw) < (unsigned)p.W &&
-                      c0 + ach[q] < p.C;
-      dma16(ra, lds_addr(S + i * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
-    } else {
-      // filter rows tap * C + c0 + RPI i + brow (rows past the tap's
-      // channels, or columns past Cout, read zeros)
-      const int i = PB * wave + (q - PA);
-      const bool in = bcol && c0 + RPI * i + brow < p.C;
-      dma16(rb, lds_addr(S + AB + i * 1024), in ? vb : kIgOutOfRange,
-            (unsigned)((lkh * p.KW + lkw) * p.C + c0 + RPI * i) * ldb);
+#pragma unroll
+    for (int q = 0; q < PA; ++q) {
+      const bool in = ain[q] & (c0 < alim[q]);
+      dma16(ra, lds_addr(S + (PA * wave + q) * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
     }
-  };
-  // after a stage's DMA: the next KR channels, then the next tap
-  auto tap_next = [&]() {
-    ++lkt;
+    const unsigned sb = (unsigned)(krow + RPI * PB * wave) * ldb;
+#pragma unroll
+    for (int q = 0; q < PB; ++q)
+      dma16(rb, lds_addr(S + AB + (PB * wave + q) * 1024), c0 < blim[q] ? vb : kIgOutOfRange, sb + q * bstep);
+    // the next stage: the next KR channels of this tap, or the next tap
     if (++lcc == p.cs) {
       lcc = 0;
       if (++lkw == p.KW) {
         lkw = 0;
         ++lkh;
       }
+      tap_begin();
+    } else {
+      soff += KB;
+      krow += KR;
     }
-  };
-  auto dma_stage = [&](unsigned char* S) {
-    tap_begin();
-#pragma unroll
-    for (int q = 0; q < PER; ++q) dma_one(S, q);
-    tap_next();
   };
 
   // fragment offsets (as in the DMA GEMM): A row r at r * KB, chunk c at
@@ -345,13 +354,20 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
 #pragma unroll
   for (int q = 0; q < NS - 1; ++q)
     if (q < ns) dma_stage(buf(q));
-  for (int s = 0; s < ns; ++s) {
-    const int fly = min(ns - 1, s + NS - 2) - s;  // this wave's later stages in flight
-    if (fly >= 2) XTK_WAIT_VM(2 * PER);
-    else if (fly >= 1) XTK_WAIT_VM(PER);
-    else XTK_WAIT_VM(0);
+  static_assert(NS == 4, "the loop below keeps two later stages in flight");
+  int s = 0;
+  // steady state: stages s + 1 and s + 2 of this wave stay in flight
+  for (; s + 2 < ns; ++s) {
+    XTK_WAIT_VM(2 * PER);
     asm volatile("s_barrier" ::: "memory");
     if (s + NS - 1 < ns) dma_stage(buf(s + NS - 1));
+    compute(buf(s));
+  }
+  // the last two stages (no DMA left to issue)
+  for (; s < ns; ++s) {
+    if (s + 1 < ns) XTK_WAIT_VM(PER);
+    else XTK_WAIT_VM(0);
+    asm volatile("s_barrier" ::: "memory");
     compute(buf(s));
   }
 
