@@ -49,6 +49,7 @@
 //     are ordered in groups of GROUP tile columns so that concurrently resident
 //     workgroups share A and B panels in their XCD's L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "launch.h"
@@ -705,8 +706,12 @@ __global__ __launch_bounds__(64 * NW, BMT * BNT <= 128 * 128 ? 2 : 1) void gemm_
   // one DMA instruction per slot, two in the first slots of a tile smaller
   // than 256 x 256 (6 for 4 slots, 4 for 2)
   static_assert(PER >= SLOTS && PER <= 2 * SLOTS, "DMA instructions per slot");
-  auto stage = [&](int s, unsigned char* S, const unsigned char* Snext, unsigned char* Sfree) {
-    const bool more = s + NS - 1 < nk;
+  // `more` (a stage NS - 1 ahead exists) is std::true_type in the steady
+  // state, so the DMA of each slot is issued with no test in front of it
+  // (a test per instruction cost C3 ~70 scalar instructions a stage), and
+  // a bool in the last stages.
+  auto stage = [&](auto more_c, int s, unsigned char* S, const unsigned char* Snext, unsigned char* Sfree) {
+    const bool more = more_c;
 #pragma unroll
     for (int g = 0; g < SLOTS; ++g) {
       const int set = g < HALF ? 0 : 1, n0 = 4 * (g % HALF);
@@ -737,10 +742,18 @@ __global__ __launch_bounds__(64 * NW, BMT * BNT <= 128 * 128 ? 2 : 1) void gemm_
     else XT_WAIT_VM(0);
     asm volatile("s_barrier" ::: "memory");
   };
-  for (int s0 = 0; s0 < nk; s0 += NS) {
+  int s0 = 0;
+  // steady state: every stage of the group has a stage NS - 1 ahead
+  for (; s0 + 2 * NS - 2 < nk; s0 += NS) {
 #pragma unroll
     for (int q = 0; q < NS; ++q)
-      if (s0 + q < nk) stage(s0 + q, buf[q], buf[(q + 1) % NS], buf[(q + NS - 1) % NS]);
+      stage(std::true_type{}, s0 + q, buf[q], buf[(q + 1) % NS], buf[(q + NS - 1) % NS]);
+  }
+  for (; s0 < nk; s0 += NS) {
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+      if (s0 + q < nk)
+        stage(s0 + q + NS - 1 < nk, s0 + q, buf[q], buf[(q + 1) % NS], buf[(q + NS - 1) % NS]);
   }
 #undef XT_WAIT_VM
 
