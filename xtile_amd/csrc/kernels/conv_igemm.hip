@@ -23,7 +23,8 @@
 //     exact i32 sums rounded to f32 once); 64 or 80 KB of LDS, so two
 //     workgroups share a CU and one's barrier waits are the other's MFMA time.
 //     Deep layers, whose 128 x 128 tiles would fill at most half the CUs,
-//     take 64 x 128 tiles of four 32 x 64 waves with 128-byte stages (96 KB).
+//     take 64 x 128 tiles of four 32 x 64 waves with 128-byte stages (96 KB)
+//     and eight more waves that only issue the DMA (below).
 //   * A K stage is KB = 64 (or 128) bytes of one tap's channels in every
 //     pixel row (32 f16 / bf16 or 64 i8 channels a 64-byte stage; a tap's
 //     last stage is padded with zeros when Cin is not a multiple of that, and
@@ -127,8 +128,19 @@ __device__ __forceinline__ int ig_bsw(int k) {
 // WTN wave tiles: (BM, BN) = (128, 128) with 2 x 2 waves of 64 x 64, (256,
 // 64) with 4 x 1, or (64, 128) with 2 x 2 waves of 32 x 64.  A K stage is KBY
 // bytes of one tap's channels (64, or 128 for the 64 x 128 tiles).
-template <int ELEM, int BM, int BN, int WTM = 64, int WTN = 64, int KBY = 64>
-__global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
+//
+// LW > 0: LW more waves, 4 .. 3 + LW, that only issue the DMA, while waves
+// 0-3 only read fragments and run the MFMAs.  A wave waits in issue until
+// the CU's address unit takes each DMA instruction (~50 B/clk a CU for these
+// gathers), so with one wave per SIMD doing both, a deep layer's stage spent
+// ~470 cycles issuing its DMA and then ~455 on its fragments and MFMAs, one
+// after the other (s_memtime stamps, 32 x 14^2 x 256 -> 256); split, the two
+// run side by side and a stage takes ~740 (18.8 -> 17.5 us; four loader
+// waves 17.9).  Reading each stage's fragments during the previous stage's
+// MFMAs, or two K groups of 64 x 64 waves that halve the filter-fragment
+// reads, measured slower on top of it.
+template <int ELEM, int BM, int BN, int WTM = 64, int WTN = 64, int KBY = 64, int LW = 0>
+__global__ __launch_bounds__(64 * (4 + LW), 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
   // stages in LDS (64 or 80 KB, two workgroups a CU): five, or a pipeline
   // that also read each stage's fragments during the previous stage's MFMAs
   // and spread the DMA over them, measured slower on 3 x 3 convs with 128 to
@@ -150,9 +162,11 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
   constexpr int WGM = BM / WTM, WGN = 4 / WGM;
   static_assert(WGM * WGN == 4 && BN == WTN * WGN, "wave layout");
   constexpr int MI = WTM / 32, NI = WTN / 32;
-  constexpr int PA = BM * KB / 4096;  // A DMA instructions per wave and stage (RA rows each)
-  constexpr int PB = BN * KB / 4096;  // B DMA instructions per wave and stage
-  constexpr int PER = PA + PB;       // DMA instructions per wave and stage
+  constexpr int DW = LW ? LW : 4;            // waves sharing the DMA
+  constexpr int PA = BM * KB / (1024 * DW);  // A DMA instructions per DMA wave and stage (RA rows each)
+  constexpr int PB = BN * KB / (1024 * DW);  // B DMA instructions per DMA wave and stage
+  constexpr int PER = PA + PB;               // DMA instructions per DMA wave and stage
+  static_assert(PA * 1024 * DW == BM * KB && PB * 1024 * DW == BN * KB, "DMA share");
   constexpr int CPR = BR / 16, RPI = 1024 / BR;  // B chunks per row, rows per DMA instruction
   typedef __attribute__((address_space(3))) unsigned char lds_t;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
@@ -171,6 +185,8 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
   const int m0 = mt * BM, n0 = (L - mt * p.ntiles) * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the wave's share of the DMA (every wave's, or a loader wave's)
+  const int dw = LW ? wave - 4 : wave;
   const int wm = wave / WGN, wn = wave % WGN;
 
   const i32x4 ra = raw_rsrc(p.src, p.src_bytes), rb = raw_rsrc(p.filt, p.filt_bytes);
@@ -187,7 +203,7 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
   {
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
-      const int arow_q = RA * (PA * wave + q) + lane / CA;
+      const int arow_q = RA * (PA * dw + q) + lane / CA;
       const unsigned gc = (unsigned)((lane % CA) ^ ((arow_q / SWD) & (CA - 1)));
       ach[q] = (int)gc * (16 / ES);
       const int pix = m0 + arow_q;
@@ -223,7 +239,7 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
   {
     const bool bcol = n0 * ES + (((lane % CPR) ^ ig_bsw<ES, BR>(lane / CPR)) << 4) < p.CO * ES;
 #pragma unroll
-    for (int q = 0; q < PB; ++q) blim[q] = bcol ? p.C - RPI * (PB * wave + q) - lane / CPR : -(1 << 30);
+    for (int q = 0; q < PB; ++q) blim[q] = bcol ? p.C - RPI * (PB * dw + q) - lane / CPR : -(1 << 30);
   }
 
   // DMA state of the next stage to load: its tap (kh, kw), its channel
@@ -255,12 +271,12 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
 #pragma unroll
     for (int q = 0; q < PA; ++q) {
       const bool in = ain[q] & (c0 < alim[q]);
-      dma16(ra, lds_addr(S + (PA * wave + q) * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
+      dma16(ra, lds_addr(S + (PA * dw + q) * 1024), in ? abase[q] + soff : kIgOutOfRange, 0);
     }
-    const unsigned sb = (unsigned)(krow + RPI * PB * wave) * ldb;
+    const unsigned sb = (unsigned)(krow + RPI * PB * dw) * ldb;
 #pragma unroll
     for (int q = 0; q < PB; ++q)
-      dma16(rb, lds_addr(S + AB + (PB * wave + q) * 1024), c0 < blim[q] ? vb : kIgOutOfRange, sb + q * bstep);
+      dma16(rb, lds_addr(S + AB + (PB * dw + q) * 1024), c0 < blim[q] ? vb : kIgOutOfRange, sb + q * bstep);
     // the next stage: the next KR channels of this tap, or the next tap
     if (++lcc == p.cs) {
       lcc = 0;
@@ -351,24 +367,52 @@ __global__ __launch_bounds__(256, 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void
   // The barriers are bare s_barriers: __syncthreads' release fence would wait
   // for every DMA in flight.
   const int ns = (int)((long long)(kr + 1) * p.stages / p.ksplit) - s_begin;
+  static_assert(NS == 4, "the loops below keep two later stages in flight");
+  if (LW && wave >= 4) {
+    // loader wave: barrier s follows its own DMA of stage s (stages s + 1
+    // and s + 2 may stay in flight) and frees stage s - 1's buffer for
+    // stage s + 3.  As many barriers as the MFMA waves, then done.
 #pragma unroll
-  for (int q = 0; q < NS - 1; ++q)
-    if (q < ns) dma_stage(buf(q));
-  static_assert(NS == 4, "the loop below keeps two later stages in flight");
-  int s = 0;
-  // steady state: stages s + 1 and s + 2 of this wave stay in flight
-  for (; s + 2 < ns; ++s) {
-    XTK_WAIT_VM(2 * PER);
-    asm volatile("s_barrier" ::: "memory");
-    if (s + NS - 1 < ns) dma_stage(buf(s + NS - 1));
-    compute(buf(s));
+    for (int q = 0; q < NS - 1; ++q)
+      if (q < ns) dma_stage(buf(q));
+    int s = 0;
+    for (; s + 2 < ns; ++s) {
+      XTK_WAIT_VM(2 * PER);
+      asm volatile("s_barrier" ::: "memory");
+      if (s + NS - 1 < ns) dma_stage(buf(s + NS - 1));
+    }
+    for (; s < ns; ++s) {
+      if (s + 1 < ns) XTK_WAIT_VM(PER);
+      else XTK_WAIT_VM(0);
+      asm volatile("s_barrier" ::: "memory");
+    }
+    return;
   }
-  // the last two stages (no DMA left to issue)
-  for (; s < ns; ++s) {
-    if (s + 1 < ns) XTK_WAIT_VM(PER);
-    else XTK_WAIT_VM(0);
-    asm volatile("s_barrier" ::: "memory");
-    compute(buf(s));
+  if constexpr (LW > 0) {
+    // MFMA wave: after barrier s, stage s has landed
+    for (int s = 0; s < ns; ++s) {
+      asm volatile("s_barrier" ::: "memory");
+      compute(buf(s));
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < NS - 1; ++q)
+      if (q < ns) dma_stage(buf(q));
+    int s = 0;
+    // steady state: stages s + 1 and s + 2 of this wave stay in flight
+    for (; s + 2 < ns; ++s) {
+      XTK_WAIT_VM(2 * PER);
+      asm volatile("s_barrier" ::: "memory");
+      if (s + NS - 1 < ns) dma_stage(buf(s + NS - 1));
+      compute(buf(s));
+    }
+    // the last two stages (no DMA left to issue)
+    for (; s < ns; ++s) {
+      if (s + 1 < ns) XTK_WAIT_VM(PER);
+      else XTK_WAIT_VM(0);
+      asm volatile("s_barrier" ::: "memory");
+      compute(buf(s));
+    }
   }
 
   // D = A x B per 32 x 32 tile: lane l holds channel l % 32 of tile j and
@@ -510,7 +554,7 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   const int el = i8 ? kIgI8 : c.elem == xt::Elem::BF16 ? kIgBF16 : kIgF16;
 #define XT_IG(E)                                                                                       \
   do {                                                                                                 \
-    if (deep) hipLaunchKernelGGL((conv_igemm_kernel<E, 64, 128, 32, 64, 128>), dim3(a.nwg), dim3(256), 0, s, a); \
+    if (deep) hipLaunchKernelGGL((conv_igemm_kernel<E, 64, 128, 32, 64, 128, 8>), dim3(a.nwg), dim3(768), 0, s, a); \
     else if (wide) hipLaunchKernelGGL((conv_igemm_kernel<E, 128, 128>), dim3(a.nwg), dim3(256), 0, s, a);      \
     else hipLaunchKernelGGL((conv_igemm_kernel<E, 256, 64>), dim3(a.nwg), dim3(256), 0, s, a);                 \
   } while (0)
