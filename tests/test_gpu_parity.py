@@ -303,6 +303,7 @@ def test_conv2d_band_kernel_shapes(cuda, n, h, w, cin, pad, stride, dil, dt):
         (24, 14, 14, 512, 512, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # 148 tiles, 144 stages: K in halves
         (2, 10, 10, 192, 256, 3, 3, 5, 10, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),   # deep: 64 x 128 tiles, 3 128-byte stages a tap
         (8, 14, 14, 256, 256, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),  # C9's layer at batch 8: 50 deep tiles, K split
+        (32, 14, 14, 256, 256, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # C9's layer: 196 deep tiles, rotated K walks
     ],
 )
 def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
@@ -310,8 +311,10 @@ def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil
     bytes above ~150 KB) with Cout a multiple of 64 take the implicit-GEMM
     kernel (conv_igemm.hip; 128 x 128 tiles for Cout a multiple of 128, else
     256 x 64, and 64 x 128 tiles with 128-byte K stages for deep layers whose
-    128 x 128 tiles would fill at most half the CUs): operands by DMA, the
-    input gathered per tap, padding and rows past M read as zeros."""
+    128 x 128 tiles would fill at most half the CUs, their DMA issued by
+    eight loader waves and, for whole-K tiles, walked from a stage rotated
+    per pixel tile): operands by DMA, the input gathered per tap, padding and
+    rows past M read as zeros."""
     rng = np.random.default_rng(9)
     mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
                    pad=pad, stride=stride, dilation=dil)

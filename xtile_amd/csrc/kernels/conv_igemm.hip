@@ -83,6 +83,7 @@ struct IgArgs {
   int ksplit;   // K ranges per tile (1: one workgroup per tile)
   int kstages;  // the shortest K range: range r covers stages [r S / ksplit, (r + 1) S / ksplit)
   int nwg;      // tiles * ksplit
+  int rot;      // 1: a whole-K tile walks its stages from (pixel tile % stages), wrapping
   Div31 d_ohw, d_ow;
 };
 
@@ -139,15 +140,16 @@ __device__ __forceinline__ int ig_bsw(int k) {
 // waves 17.9).  Reading each stage's fragments during the previous stage's
 // MFMAs, or two K groups of 64 x 64 waves that halve the filter-fragment
 // reads, measured slower on top of it.
-template <int ELEM, int BM, int BN, int WTM = 64, int WTN = 64, int KBY = 64, int LW = 0>
-__global__ __launch_bounds__(64 * (4 + LW), 4 * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
+template <int ELEM, int BM, int BN, int WTM = 64, int WTN = 64, int KBY = 64, int LW = 0, int NSTAGES = 4>
+__global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
   // stages in LDS (64 or 80 KB, two workgroups a CU): five, or a pipeline
   // that also read each stage's fragments during the previous stage's MFMAs
   // and spread the DMA over them, measured slower on 3 x 3 convs with 128 to
   // 512 channels (e.g. 28 x 28 x 128: 18.3 us with this loop at four stages,
   // 19.2 at five, 21.1 / 23.2 pipelined); eight stages (one workgroup a CU)
   // left 32 x 14^2 x 256 -> 256 unchanged (29.0 / 30.4 us)
-  constexpr int NS = 4;
+  constexpr int NS = NSTAGES;
+  static_assert(NS == 4 || (LW > 0 && NS >= 3 && NS <= 5), "stages in LDS");
   constexpr int ES = ELEM == kIgI8 ? 1 : 2;  // bytes per element
   // a stage is KB bytes of K (KB / esize channels of one tap); a K step of
   // the MFMAs is 32 bytes (KSR filter rows), KSTEPS of them a stage.  A DMA
@@ -250,7 +252,15 @@ __global__ __launch_bounds__(64 * (4 + LW), 4 * KBY * (BM + BN) <= 80 * 1024 ? 2
   // source and KR filter rows).
   // this workgroup's stages [s_begin, s_begin + ns)
   const int s_begin = (int)((long long)kr * p.stages / p.ksplit);
-  int lcc = s_begin % p.cs, lkw = s_begin / p.cs, lkh;
+  // With rot (whole-K tiles only), pixel tile mt starts its walk at stage mt
+  // % stages and wraps: the workgroups of one XCD, which run in step, then
+  // ask for different filter rows at any one time instead of all sending
+  // the same lines' requests to the same L2 channels (c9: 17.5 -> 16.4 us;
+  // a start per workgroup rather than per pixel tile 16.6, since the two
+  // channel tiles of a pixel tile share its input rows).  The sum over the
+  // stages is the same; the order of the f32 additions is not.
+  int lst = s_begin + (p.rot ? mt % p.stages : 0);
+  int lcc = lst % p.cs, lkw = lst / p.cs, lkh;
   lkh = lkw / p.KW;
   lkw -= lkh * p.KW;
   unsigned soff = 0;
@@ -278,7 +288,15 @@ __global__ __launch_bounds__(64 * (4 + LW), 4 * KBY * (BM + BN) <= 80 * 1024 ? 2
     for (int q = 0; q < PB; ++q)
       dma16(rb, lds_addr(S + AB + (PB * dw + q) * 1024), c0 < blim[q] ? vb : kIgOutOfRange, sb + q * bstep);
     // the next stage: the next KR channels of this tap, or the next tap
-    if (++lcc == p.cs) {
+    if (++lst == p.stages) {
+      // past the last stage: wrap to the first (only a rotated walk has
+      // stages left to load then)
+      lst = 0;
+      lcc = 0;
+      lkw = 0;
+      lkh = 0;
+      tap_begin();
+    } else if (++lcc == p.cs) {
       lcc = 0;
       if (++lkw == p.KW) {
         lkw = 0;
@@ -367,22 +385,23 @@ __global__ __launch_bounds__(64 * (4 + LW), 4 * KBY * (BM + BN) <= 80 * 1024 ? 2
   // The barriers are bare s_barriers: __syncthreads' release fence would wait
   // for every DMA in flight.
   const int ns = (int)((long long)(kr + 1) * p.stages / p.ksplit) - s_begin;
-  static_assert(NS == 4, "the loops below keep two later stages in flight");
   if (LW && wave >= 4) {
     // loader wave: barrier s follows its own DMA of stage s (stages s + 1
-    // and s + 2 may stay in flight) and frees stage s - 1's buffer for
-    // stage s + 3.  As many barriers as the MFMA waves, then done.
+    // .. s + NS - 2 may stay in flight) and frees stage s - 1's buffer for
+    // stage s + NS - 1.  As many barriers as the MFMA waves, then done.
 #pragma unroll
     for (int q = 0; q < NS - 1; ++q)
       if (q < ns) dma_stage(buf(q));
     int s = 0;
-    for (; s + 2 < ns; ++s) {
-      XTK_WAIT_VM(2 * PER);
+    for (; s + NS - 2 < ns; ++s) {
+      XTK_WAIT_VM((NS - 2) * PER);
       asm volatile("s_barrier" ::: "memory");
       if (s + NS - 1 < ns) dma_stage(buf(s + NS - 1));
     }
+    // the last NS - 2 stages: fewer later stages in flight
     for (; s < ns; ++s) {
-      if (s + 1 < ns) XTK_WAIT_VM(PER);
+      if (NS > 3 && s + 2 < ns) XTK_WAIT_VM(2 * PER);
+      else if (s + 1 < ns) XTK_WAIT_VM(PER);
       else XTK_WAIT_VM(0);
       asm volatile("s_barrier" ::: "memory");
     }
@@ -395,6 +414,7 @@ __global__ __launch_bounds__(64 * (4 + LW), 4 * KBY * (BM + BN) <= 80 * 1024 ? 2
       compute(buf(s));
     }
   } else {
+    static_assert(NS == 4, "the loops below keep two later stages in flight");
 #pragma unroll
     for (int q = 0; q < NS - 1; ++q)
       if (q < ns) dma_stage(buf(q));
@@ -543,6 +563,10 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   if (!grid_fits(nwg, 256) || M * c.CO % 4) return false;
   a.tiles = (int)tiles;
   a.ksplit = (int)ksplit;
+  // the rotated walk keeps a whole filter and the XCD's input rows in its
+  // 4 MB L2 at once (the walk in step reads one stage of them at a time):
+  // deep whole-K tiles with a filter up to 2 MB
+  a.rot = deep && ksplit == 1 && filt_bytes <= (2LL << 20) ? 1 : 0;
   a.nwg = (int)nwg;
   if (ksplit > 1) {
     const long long n4 = M * c.CO / 4;
