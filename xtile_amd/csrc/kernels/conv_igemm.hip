@@ -388,7 +388,8 @@ __global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 10
   if (LW && wave >= 4) {
     // loader wave: barrier s follows its own DMA of stage s (stages s + 1
     // .. s + NS - 2 may stay in flight) and frees stage s - 1's buffer for
-    // stage s + NS - 1.  As many barriers as the MFMA waves, then done.
+    // stage s + NS - 1.  As many barriers as the MFMA waves; then, for a
+    // whole-K tile, its share of the stores below.
 #pragma unroll
     for (int q = 0; q < NS - 1; ++q)
       if (q < ns) dma_stage(buf(q));
@@ -405,9 +406,8 @@ __global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 10
       else XTK_WAIT_VM(0);
       asm volatile("s_barrier" ::: "memory");
     }
-    return;
-  }
-  if constexpr (LW > 0) {
+    if (p.ksplit > 1) return;
+  } else if constexpr (LW > 0) {
     // MFMA wave: after barrier s, stage s has landed
     for (int s = 0; s < ns; ++s) {
       asm volatile("s_barrier" ::: "memory");
@@ -437,6 +437,42 @@ __global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 10
 
   // D = A x B per 32 x 32 tile: lane l holds channel l % 32 of tile j and
   // register v pixel row 8 (v / 4) + 4 (l / 32) + v % 4 of tile i
+  if constexpr (LW > 0) {
+    if (p.ksplit == 1) {
+      // A whole-K tile's results go through LDS ([BM rows][BN f32], rows OP
+      // bytes apart: the two half-waves' rows r and r + 4 fall 32 banks
+      // apart) and leave as 16-byte non-temporal lanes from all 4 + LW
+      // waves: a quarter of the store instructions of 4-byte lanes from
+      // the four MFMA waves (c9: 1.8 us of stores after the K loop).
+      constexpr int OP = BN * 4 + 32;
+      static_assert(BM * OP <= NS * STAGE && (4 * (OP / 4)) % 64 == 32, "staging rows");
+      float* const st = reinterpret_cast<float*>(smem);
+      __syncthreads();  // every wave is done with the stage buffers
+      if (wave < 4) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int row = wm * WTM + i * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+              const float x = static_cast<float>(acc[i][j][v]);
+              st[row * (OP / 4) + wn * WTN + j * 32 + lrow] = x;
+            }
+      }
+      __syncthreads();
+      constexpr int PR = BN / 4;  // 16-byte pieces a row
+      for (int k = tid; k < BM * PR; k += 64 * (4 + LW)) {
+        const int row = k / PR, c4 = k - row * PR;
+        // Cout is a multiple of 8 (16-byte filter rows), so a piece that
+        // starts below Cout ends below it
+        if (m0 + row < p.M && n0 + 4 * c4 < p.CO)
+          __builtin_nontemporal_store(*reinterpret_cast<const float4v*>(st + row * (OP / 4) + 4 * c4),
+                                      reinterpret_cast<float4v*>(p.out + (long long)(m0 + row) * p.CO + n0 + 4 * c4));
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
