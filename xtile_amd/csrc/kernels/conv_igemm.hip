@@ -141,7 +141,7 @@ __device__ __forceinline__ int ig_bsw(int k) {
 // MFMAs, or two K groups of 64 x 64 waves that halve the filter-fragment
 // reads, measured slower on top of it.
 template <int ELEM, int BM, int BN, int WTM = 64, int WTN = 64, int KBY = 64, int LW = 0, int NSTAGES = 4>
-__global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
+__global__ __launch_bounds__(64 * (4 + LW), LW == 0 && NSTAGES * KBY * (BM + BN) <= 80 * 1024 ? 2 : 1) void conv_igemm_kernel(IgArgs p) {
   // stages in LDS (64 or 80 KB, two workgroups a CU): five, or a pipeline
   // that also read each stage's fragments during the previous stage's MFMAs
   // and spread the DMA over them, measured slower on 3 x 3 convs with 128 to
@@ -160,6 +160,9 @@ __global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 10
   constexpr int KB = KBY, AB = BM * KB, BR = BN * ES, KR = KB / ES, KSR = 32 / ES, KSTEPS = KB / 32;
   constexpr int RA = 1024 / KB, CA = KB / 16, SWD = 256 / KB;
   constexpr int STAGE = AB + KR * BR;  // 16, 20 or 24 KB
+  // whole-K results staged through LDS for 16-byte stores (below): with
+  // loader waves, when the tile's results fit the stage buffers
+  constexpr bool STAGED = LW > 0 && BM * (BN * 4 + 32) <= NS * STAGE;
   typedef typename IgAcc<ELEM>::type acc_t;
   constexpr int WGM = BM / WTM, WGN = 4 / WGM;
   static_assert(WGM * WGN == 4 && BN == WTN * WGN, "wave layout");
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 10
       else XTK_WAIT_VM(0);
       asm volatile("s_barrier" ::: "memory");
     }
-    if (p.ksplit > 1) return;
+    if (!STAGED || p.ksplit > 1) return;
   } else if constexpr (LW > 0) {
     // MFMA wave: after barrier s, stage s has landed
     for (int s = 0; s < ns; ++s) {
@@ -437,7 +440,7 @@ __global__ __launch_bounds__(64 * (4 + LW), NSTAGES * KBY * (BM + BN) <= 80 * 10
 
   // D = A x B per 32 x 32 tile: lane l holds channel l % 32 of tile j and
   // register v pixel row 8 (v / 4) + 4 (l / 32) + v % 4 of tile i
-  if constexpr (LW > 0) {
+  if constexpr (STAGED) {
     if (p.ksplit == 1) {
       // A whole-K tile's results go through LDS ([BM rows][BN f32], rows OP
       // bytes apart: the two half-waves' rows r and r + 4 fall 32 banks
