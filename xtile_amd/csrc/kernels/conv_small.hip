@@ -25,6 +25,13 @@
 //     64 columns (KH * KP rows, zero past each kh's KW * Cin) in LDS once, then
 //     runs every K step from LDS: source fragments as element reads at the
 //     pixel's patch position, filter fragments by ds_read_b64_tr_b16 / _b8.
+//   * With one channel tile, the patch in one round and enough output rows
+//     (the 7 x 7 stem), three workgroups a CU walk the tasks instead
+//     (TASKS): filter tile and K table staged once, the next task's patch
+//     loads in flight behind the current task, every patch piece's row and
+//     position known at compile time.  The one-workgroup-a-task form spent
+//     most of its time issuing the staging's index arithmetic (~545
+//     instructions a round, three rounds a wave): C8 38.1 -> 31.8 us.
 //   * i8: exact i32 sums, rounded to f32 once at the store.
 //   * Results: a half-wave stores one 128-byte run of 32 channels per
 //     accumulator register (non-temporal); pixels past the row and channels
@@ -58,10 +65,18 @@ struct ScArgs {
   int chunks;   // 128-pixel chunks per output row
   int ntiles;   // 64-channel tiles
   int nwg;      // workgroups
+  int ntask;    // TASKS: images * OH * chunks (one channel tile)
 };
 
-template <int ELEM, bool BIG>
-__global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p) {
+// TASKS: the workgroup walks output-row tasks (one 64-channel tile, the
+// patch in one round of loads, NPR 256-element pieces a patch row) instead
+// of taking one: the filter tile and the K table are staged once, the next
+// task's patch loads are issued as soon as the current patch is in LDS (they
+// land behind the current task's K loop and stores), and each piece's patch
+// row and position are compile-time constants (the counters of the one-task
+// staging cost ~25 scalar instructions a piece).
+template <int ELEM, bool BIG, bool TASKS = false, int NPR = 0>
+__global__ __launch_bounds__(256, TASKS ? 3 : BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p) {
   constexpr bool I8 = ELEM == kScI8;
   constexpr int ES = I8 ? 1 : 2;       // element bytes
   constexpr int KS = I8 ? 32 : 16;     // MFMA depth
@@ -71,19 +86,6 @@ __global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p
   extern __shared__ __attribute__((aligned(16))) unsigned char sm[];
   typedef __attribute__((address_space(3))) unsigned char lds_t;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // workgroup -> (image, output row, pixel chunk, channel tile); with a
-  // multiple of 8 workgroups the 8 XCDs (dispatched round-robin) receive
-  // contiguous runs of output rows, which share their input rows in one L2
-  int L = blockIdx.x;
-  if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
-  const int nt = L % p.ntiles;
-  L /= p.ntiles;
-  const int ch = L % p.chunks;
-  L /= p.chunks;
-  const int oh = L % p.OH;
-  const int n = L / p.OH;
-  const int ow0 = ch * 128, n0 = nt * 64;
-
   // LDS: the patch [KH rows][pw * C elements], the filter tile [kp rows][64
   // channels] (K = (kh, kw, c) in HWIO row order, zero rows past K; FR-byte
   // rows, 16-byte chunk c of row k at c ^ fsw(k) so that a transposing read's
@@ -100,9 +102,6 @@ __global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p
     const int kh = k / p.run;
     T[k] = k < p.K ? (unsigned short)((kh * prow_pad + k - kh * p.run) * ES) : 0;
   }
-  const int iw_lo = ow0 * p.sw - p.pad_l;
-  // a patch row's elements inside the image: columns [0, W), a range of j
-  const int jlo = max(0, -iw_lo) * p.C, jhi = min(prow, (p.W - iw_lo) * p.C);
   const int nrow = p.KH * p.npr;       // 256-element patch pieces
   // buffer loads: an offset at or past the buffer's size (kOor) reads zero,
   // so no load sits behind a branch and a round's loads are in flight together
@@ -118,61 +117,11 @@ __global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p
   // image row and offset are the same for every thread.
   constexpr int U = BIG ? 28 : 12, UF = BIG ? 5 : 2;
   const int fq = tid % PPR, fk0 = tid / PPR;  // this thread's filter piece column, first row
-  int kh_t = 0, i_t = 0;                      // piece t's row and position, t = r U + u
-  for (int r = 0; r * U < nrow || r * UF * RPR < p.kp; ++r) {
-    unsigned short v[U];
-    int dst[U];
-    uint4v w[UF];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int ih = oh * p.sh - p.pad_t + kh_t * p.dh;
-      const int j = tid + 256 * i_t;
-      const int rowoff = ((n * p.H + ih) * p.W + iw_lo) * p.C;
-      const bool in = r * U + u < nrow && (unsigned)ih < (unsigned)p.H && j >= jlo && j < jhi;
-      const unsigned off = in ? (unsigned)(rowoff + j) * ES : kOor;
-      if constexpr (I8)
-        v[u] = __builtin_amdgcn_raw_buffer_load_b8(rs, off, 0, 0);
-      else
-        v[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
-      dst[u] = r * U + u < nrow && j < prow_pad ? kh_t * prow_pad + j : -1;
-      if (++i_t == p.npr) {
-        i_t = 0;
-        ++kh_t;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UF; ++u) {
-      const int k = fk0 + RPR * (r * UF + u);
-      const bool in = k < p.K && n0 + fq * (16 / ES) < p.CO;
-      w[u] = __builtin_amdgcn_raw_buffer_load_b128(rf, in ? (unsigned)(k * p.CO + n0 + fq * (16 / ES)) * ES : kOor,
-                                                   0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (dst[u] >= 0) {
-        if constexpr (I8)
-          patch[dst[u]] = (unsigned char)v[u];
-        else
-          reinterpret_cast<unsigned short*>(patch)[dst[u]] = v[u];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UF; ++u) {
-      const int k = fk0 + RPR * (r * UF + u);
-      if (k < p.kp) *reinterpret_cast<uint4v*>(ftile + k * FR + ((fq ^ fsw(k)) << 4)) = w[u];
-    }
-  }
-  __syncthreads();
-
   // this wave's 32 pixels: lane l % 32; K positions (KS / 2) (l / 32) .. + KS / 2 - 1 of a step
   const int lr = lane & 31, hi = lane >> 5;
   const int g = lane >> 4, li = lane & 15;
   typedef typename std::conditional<I8, sc_i16v, sc_f16v>::type acc_t;
   acc_t acc[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[t][v] = 0;
   const int px = wave * 32 + lr;                                // pixel within the chunk
   const unsigned char* const pwin = patch + px * p.sw * p.C * ES;  // its patch window
   // filter fragment offsets (N tile t, read h) in a step's first row block
@@ -253,27 +202,178 @@ __global__ __launch_bounds__(256, BIG ? 4 : 1) void conv2d_small_kernel(ScArgs p
                                                         acc[t], 0, 0, 0);
     }
   };
-  for (int s = 0; s + 1 < nsteps; ++s) step(s, std::false_type{});
-  step(nsteps - 1, std::true_type{});
+  // one task's K loop and stores, after its patch and the filter tile are in LDS
+  auto compute_store = [&](int n, int oh, int ow0, int n0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[t][v] = 0;
+    for (int s = 0; s + 1 < nsteps; ++s) step(s, std::false_type{});
+    step(nsteps - 1, std::true_type{});
 
-  // D = A x B: lane l holds channel 32 t + l % 32 of N tile t, register v
-  // pixel 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's 32
-  float* const orow = p.out + (((long long)n * p.OH + oh) * p.OW) * p.CO;
+    // D = A x B: lane l holds channel 32 t + l % 32 of N tile t, register v
+    // pixel 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's 32
+    float* const orow = p.out + (((long long)n * p.OH + oh) * p.OW) * p.CO;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int co = n0 + t * 32 + lr;
-    if (co >= p.CO) continue;
+    for (int t = 0; t < 2; ++t) {
+      const int co = n0 + t * 32 + lr;
+      if (co >= p.CO) continue;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int ow = ow0 + wave * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
-      if (ow < p.OW) __builtin_nontemporal_store(static_cast<float>(acc[t][v]), orow + (long long)ow * p.CO + co);
+      for (int v = 0; v < 16; ++v) {
+        const int ow = ow0 + wave * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
+        if (ow < p.OW) __builtin_nontemporal_store(static_cast<float>(acc[t][v]), orow + (long long)ow * p.CO + co);
+      }
+    }
+  };
+
+  if constexpr (!TASKS) {
+    // workgroup -> (image, output row, pixel chunk, channel tile); with a
+    // multiple of 8 workgroups the 8 XCDs (dispatched round-robin) receive
+    // contiguous runs of output rows, which share their input rows in one L2
+    int L = blockIdx.x;
+    if ((p.nwg & 7) == 0) L = (L & 7) * (p.nwg >> 3) + (L >> 3);
+    const int nt = L % p.ntiles;
+    L /= p.ntiles;
+    const int ch = L % p.chunks;
+    L /= p.chunks;
+    const int oh = L % p.OH;
+    const int n = L / p.OH;
+    const int ow0 = ch * 128, n0 = nt * 64;
+
+    const int iw_lo = ow0 * p.sw - p.pad_l;
+    // a patch row's elements inside the image: columns [0, W), a range of j
+    const int jlo = max(0, -iw_lo) * p.C, jhi = min(prow, (p.W - iw_lo) * p.C);
+    int kh_t = 0, i_t = 0;                      // piece t's row and position, t = r U + u
+    for (int r = 0; r * U < nrow || r * UF * RPR < p.kp; ++r) {
+      unsigned short v[U];
+      int dst[U];
+      uint4v w[UF];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int ih = oh * p.sh - p.pad_t + kh_t * p.dh;
+        const int j = tid + 256 * i_t;
+        const int rowoff = ((n * p.H + ih) * p.W + iw_lo) * p.C;
+        const bool in = r * U + u < nrow && (unsigned)ih < (unsigned)p.H && j >= jlo && j < jhi;
+        const unsigned off = in ? (unsigned)(rowoff + j) * ES : kOor;
+        if constexpr (I8)
+          v[u] = __builtin_amdgcn_raw_buffer_load_b8(rs, off, 0, 0);
+        else
+          v[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+        dst[u] = r * U + u < nrow && j < prow_pad ? kh_t * prow_pad + j : -1;
+        if (++i_t == p.npr) {
+          i_t = 0;
+          ++kh_t;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UF; ++u) {
+        const int k = fk0 + RPR * (r * UF + u);
+        const bool in = k < p.K && n0 + fq * (16 / ES) < p.CO;
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(rf, in ? (unsigned)(k * p.CO + n0 + fq * (16 / ES)) * ES : kOor,
+                                                     0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (dst[u] >= 0) {
+          if constexpr (I8)
+            patch[dst[u]] = (unsigned char)v[u];
+          else
+            reinterpret_cast<unsigned short*>(patch)[dst[u]] = v[u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UF; ++u) {
+        const int k = fk0 + RPR * (r * UF + u);
+        if (k < p.kp) *reinterpret_cast<uint4v*>(ftile + k * FR + ((fq ^ fsw(k)) << 4)) = w[u];
+      }
+    }
+    __syncthreads();
+    compute_store(n, oh, ow0, n0);
+  } else {
+    // the filter tile (channels 0 .. 63), rounds of UF pieces a thread
+    for (int r = 0; r * UF * RPR < p.kp; ++r) {
+      uint4v w[UF];
+#pragma unroll
+      for (int u = 0; u < UF; ++u) {
+        const int k = fk0 + RPR * (r * UF + u);
+        const bool in = k < p.K && fq * (16 / ES) < p.CO;
+        w[u] = __builtin_amdgcn_raw_buffer_load_b128(rf, in ? (unsigned)(k * p.CO + fq * (16 / ES)) * ES : kOor, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < UF; ++u) {
+        const int k = fk0 + RPR * (r * UF + u);
+        if (k < p.kp) *reinterpret_cast<uint4v*>(ftile + k * FR + ((fq ^ fsw(k)) << 4)) = w[u];
+      }
+    }
+    // tasks (image, output row, pixel chunk): each XCD (workgroups reach the
+    // 8 XCDs round-robin; the grid is a multiple of 8) takes a contiguous
+    // range of them, its G / 8 workgroups the range's tasks j, j + G / 8, ...
+    // (neighbouring rows, which share input rows, in one L2 at once)
+    const int ntask = p.ntask, gx = (int)(gridDim.x >> 3), xcd = blockIdx.x & 7;
+    const int tend = (int)((long long)(xcd + 1) * ntask / 8);
+    int task = (int)((long long)xcd * ntask / 8) + (int)(blockIdx.x >> 3);
+    // the patch of one task: piece u (patch row u / NPR, elements 256 (u %
+    // NPR) + tid) in register v[u]; rows past KH load nothing
+    static_assert(NPR >= 1 && NPR <= U, "pieces a patch row");
+    constexpr int KHM = U / NPR;  // patch rows one round holds
+    unsigned short v[U];
+    auto load_patch = [&](int t) {
+      const int ch = t % p.chunks, r = t / p.chunks, oh = r % p.OH, n = r / p.OH;
+      const int iw_lo = ch * 128 * p.sw - p.pad_l;
+      const int jlo = max(0, -iw_lo) * p.C, jhi = min(prow, (p.W - iw_lo) * p.C);
+      const int ih0 = oh * p.sh - p.pad_t;
+#pragma unroll
+      for (int kh = 0; kh < KHM; ++kh) {
+        const int ih = ih0 + kh * p.dh;
+        const bool row_in = kh < p.KH && (unsigned)ih < (unsigned)p.H;
+        const int rowoff = ((n * p.H + ih) * p.W + iw_lo) * p.C;
+#pragma unroll
+        for (int i = 0; i < NPR; ++i) {
+          const int j = tid + 256 * i;
+          const bool in = row_in && j >= jlo && j < jhi;
+          const unsigned off = in ? (unsigned)(rowoff + j) * ES : kOor;
+          if constexpr (I8)
+            v[kh * NPR + i] = __builtin_amdgcn_raw_buffer_load_b8(rs, off, 0, 0);
+          else
+            v[kh * NPR + i] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+        }
+      }
+    };
+    if (task < tend) load_patch(task);
+    while (task < tend) {
+#pragma unroll
+      for (int kh = 0; kh < KHM; ++kh)
+#pragma unroll
+        for (int i = 0; i < NPR; ++i) {
+          const int j = tid + 256 * i;
+          if (kh < p.KH && j < prow_pad) {
+            if constexpr (I8)
+              patch[kh * prow_pad + j] = (unsigned char)v[kh * NPR + i];
+            else
+              reinterpret_cast<unsigned short*>(patch)[kh * prow_pad + j] = v[kh * NPR + i];
+          }
+        }
+      __syncthreads();  // the patch (and, the first time, the filter tile and T) in LDS
+      const int next = task + gx;
+      if (next < tend) load_patch(next);
+      const int ch = task % p.chunks, r = task / p.chunks;
+      compute_store(r / p.OH, r % p.OH, ch * 128, 0);
+      task = next;
+      if (task < tend) __syncthreads();  // every wave is done with the patch
     }
   }
 }
 
 template <int E>
-hipError_t launch_sc(bool big, long long wgs, size_t lds, hipStream_t s, const ScArgs& a) {
-  auto kern = big ? conv2d_small_kernel<E, true> : conv2d_small_kernel<E, false>;
+hipError_t launch_sc(bool big, int tasks_npr, long long wgs, size_t lds, hipStream_t s, const ScArgs& a) {
+  // the task walk stages with the one-round constants (28 patch pieces a
+  // thread), NPR of them a patch row
+  auto kern = tasks_npr == 1   ? conv2d_small_kernel<E, true, true, 1>
+              : tasks_npr == 2 ? conv2d_small_kernel<E, true, true, 2>
+              : tasks_npr == 3 ? conv2d_small_kernel<E, true, true, 3>
+              : tasks_npr == 4 ? conv2d_small_kernel<E, true, true, 4>
+              : big            ? conv2d_small_kernel<E, true>
+                               : conv2d_small_kernel<E, false>;
   const hipError_t e = allow_full_lds(reinterpret_cast<const void*>(kern));
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(256), lds, s, a);
@@ -348,12 +448,29 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   a.nwg = (int)wgs;
   // four workgroups a CU or fewer by LDS: the register-heavy one-round staging
   const bool big = lds * 5 > size_t(kMaxLds);
+  // One channel tile, the patch in one round of loads and enough tasks
+  // (output-row chunks): three workgroups a CU (a multiple of 8; the next
+  // patch's registers leave room for three) walk them,
+  // the filter staged once per workgroup and the next task's patch in flight
+  // behind the current task.
+  const long long ntask = images * c.out_H * chunks;
+  const bool tasks = ntiles == 1 && a.npr <= 4 && c.KH * a.npr <= 28 && ntask >= 2048;
+  if (tasks) {
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 2)
+      cus = 256;
+    a.ntask = (int)ntask;
+    a.nwg = (int)(std::min<long long>(ntask, 3LL * cus) & ~7LL);
+  }
+  const long long grid = tasks ? a.nwg : wgs;
+  const int tasks_npr = tasks ? a.npr : 0;
   if (i8)
-    e = launch_sc<kScI8>(big, wgs, lds, s, a);
+    e = launch_sc<kScI8>(big, tasks_npr, grid, lds, s, a);
   else if (c.elem == xt::Elem::BF16)
-    e = launch_sc<kScBF16>(big, wgs, lds, s, a);
+    e = launch_sc<kScBF16>(big, tasks_npr, grid, lds, s, a);
   else
-    e = launch_sc<kScF16>(big, wgs, lds, s, a);
+    e = launch_sc<kScF16>(big, tasks_npr, grid, lds, s, a);
   return true;
 }
 
