@@ -29,13 +29,18 @@
 //     (the 7 x 7 stem), three workgroups a CU walk the tasks instead
 //     (TASKS): filter tile and K table staged once, the next task's patch
 //     loads in flight behind the current task, every patch piece's row and
-//     position known at compile time.  The one-workgroup-a-task form spent
+//     position known at compile time, patch rows one slot per piece apart
+//     (no range check before a write).  The one-workgroup-a-task form spent
 //     most of its time issuing the staging's index arithmetic (~545
-//     instructions a round, three rounds a wave): C8 38.1 -> 31.8 us.
+//     instructions a round, three rounds a wave): C8 38.1 -> 31.8 us; the
+//     stores as buffer stores against the output row (a pixel past the row
+//     is past the buffer: no compare and branch a store) and the unchecked
+//     patch writes, 1019 -> 592 instructions a task: 25.9 us.
 //   * i8: exact i32 sums, rounded to f32 once at the store.
 //   * Results: a half-wave stores one 128-byte run of 32 channels per
-//     accumulator register (non-temporal); pixels past the row and channels
-//     past Cout are not stored.
+//     accumulator register (non-temporal buffer stores against the output
+//     row); pixels past the row and channels past Cout fall outside the
+//     buffer and are not stored.
 #include <type_traits>
 
 #include "common.h"
@@ -94,7 +99,9 @@ __global__ __launch_bounds__(256, TASKS ? 3 : BIG ? 4 : 1) void conv2d_small_ker
   // patch window (kh * row pitch + (k - kh * run)) * esize.
   auto fsw = [](int k) { return I8 ? (k >> 2) & 1 : 2 * ((k >> 1) & 1); };
   const int prow = p.pw * p.C;                                 // elements per patch row
-  const int prow_pad = (prow + 16 / ES - 1) & ~(16 / ES - 1);  // 16-byte multiple
+  // patch row pitch: a 16-byte multiple; with TASKS every piece's slot (no
+  // piece needs a range check before its write)
+  const int prow_pad = TASKS ? 256 * NPR : (prow + 16 / ES - 1) & ~(16 / ES - 1);
   unsigned char* const patch = sm;
   unsigned char* const ftile = sm + p.KH * prow_pad * ES;
   unsigned short* const T = reinterpret_cast<unsigned short*>(ftile + p.kp * FR);
@@ -212,17 +219,19 @@ __global__ __launch_bounds__(256, TASKS ? 3 : BIG ? 4 : 1) void conv2d_small_ker
     step(nsteps - 1, std::true_type{});
 
     // D = A x B: lane l holds channel 32 t + l % 32 of N tile t, register v
-    // pixel 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's 32
-    float* const orow = p.out + (((long long)n * p.OH + oh) * p.OW) * p.CO;
+    // pixel 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's 32.  Buffer stores
+    // against the output row: a pixel past OW is past the buffer's records
+    // and is dropped, a channel past Cout gets an offset past them.
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        p.out + (((long long)n * p.OH + oh) * p.OW) * p.CO, (short)0, p.OW * p.CO * 4, 0x00020000);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int co = n0 + t * 32 + lr;
-      if (co >= p.CO) continue;
+      const unsigned lbase = co < p.CO ? (unsigned)(((ow0 + wave * 32 + 4 * hi) * p.CO + co) * 4) : kOor;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int ow = ow0 + wave * 32 + 8 * (v >> 2) + 4 * hi + (v & 3);
-        if (ow < p.OW) __builtin_nontemporal_store(static_cast<float>(acc[t][v]), orow + (long long)ow * p.CO + co);
-      }
+      for (int v = 0; v < 16; ++v)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(static_cast<float>(acc[t][v])), ro,
+                                              lbase + (unsigned)((8 * (v >> 2) + (v & 3)) * p.CO * 4), 0, 2);
     }
   };
 
@@ -343,14 +352,13 @@ __global__ __launch_bounds__(256, TASKS ? 3 : BIG ? 4 : 1) void conv2d_small_ker
     while (task < tend) {
 #pragma unroll
       for (int kh = 0; kh < KHM; ++kh)
+        if (kh < p.KH) {
 #pragma unroll
-        for (int i = 0; i < NPR; ++i) {
-          const int j = tid + 256 * i;
-          if (kh < p.KH && j < prow_pad) {
+          for (int i = 0; i < NPR; ++i) {
             if constexpr (I8)
-              patch[kh * prow_pad + j] = (unsigned char)v[kh * NPR + i];
+              patch[kh * prow_pad + tid + 256 * i] = (unsigned char)v[kh * NPR + i];
             else
-              reinterpret_cast<unsigned short*>(patch)[kh * prow_pad + j] = v[kh * NPR + i];
+              reinterpret_cast<unsigned short*>(patch)[kh * prow_pad + tid + 256 * i] = v[kh * NPR + i];
           }
         }
       __syncthreads();  // the patch (and, the first time, the filter tile and T) in LDS
@@ -454,7 +462,11 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   // the filter staged once per workgroup and the next task's patch in flight
   // behind the current task.
   const long long ntask = images * c.out_H * chunks;
-  const bool tasks = ntiles == 1 && a.npr <= 4 && c.KH * a.npr <= 28 && ntask >= 2048;
+  // (patch rows 256 * npr elements apart: three workgroups' LDS a CU, byte
+  // offsets into the patch below 2^16 for the K table)
+  const size_t lds_tasks = (size_t)(c.KH * 256 * a.npr * es + kp * fr + kp * 2);
+  const bool tasks = ntiles == 1 && a.npr <= 4 && c.KH * a.npr <= 28 && ntask >= 2048 &&
+                     c.KH * 256 * a.npr * es < 65536 && 3 * lds_tasks <= size_t(kMaxLds);
   if (tasks) {
     int cus = 256, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -465,12 +477,13 @@ bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   }
   const long long grid = tasks ? a.nwg : wgs;
   const int tasks_npr = tasks ? a.npr : 0;
+  const size_t lds_launch = tasks ? lds_tasks : lds;
   if (i8)
-    e = launch_sc<kScI8>(big, tasks_npr, grid, lds, s, a);
+    e = launch_sc<kScI8>(big, tasks_npr, grid, lds_launch, s, a);
   else if (c.elem == xt::Elem::BF16)
-    e = launch_sc<kScBF16>(big, tasks_npr, grid, lds, s, a);
+    e = launch_sc<kScBF16>(big, tasks_npr, grid, lds_launch, s, a);
   else
-    e = launch_sc<kScF16>(big, tasks_npr, grid, lds, s, a);
+    e = launch_sc<kScF16>(big, tasks_npr, grid, lds_launch, s, a);
   return true;
 }
 
