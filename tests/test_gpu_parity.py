@@ -834,6 +834,12 @@ def test_reference_traced_matmul_program(cuda):
         (1, 29, 35, 20, 32, 3, 3, 5, 18, (1, 1, 1, 1), (2, 2), (1, 1), "f16"),
         (1, 29, 35, 20, 32, 3, 3, 5, 18, (1, 1, 1, 1), (2, 2), (1, 1), "bf16"),
         (1, 24, 30, 13, 48, 5, 5, 6, 15, (2, 2, 2, 2), (1, 1), (1, 1), "f16"),   # odd Cin, 5 x 5
+        # >= 2048 output-row chunks with one channel tile: workgroups walk the chunks
+        (32, 224, 224, 3, 64, 7, 7, 4, 112, (3, 3, 3, 3), (2, 2), (1, 1), "f16"),  # C8's stem, 3584 chunks
+        (32, 128, 128, 3, 64, 7, 7, 4, 64, (3, 3, 3, 3), (2, 2), (1, 1), "bf16"),  # 2048 chunks
+        (32, 128, 128, 3, 32, 7, 7, 4, 64, (3, 3, 3, 3), (2, 2), (1, 1), "i8"),    # Cout 32: half a channel tile
+        (67, 62, 62, 3, 64, 7, 7, 1, 31, (3, 3, 3, 3), (2, 2), (1, 1), "f16"),     # 2077 chunks: uneven XCD ranges
+        (40, 64, 64, 3, 16, 3, 3, 8, 64, (1, 1, 1, 1), (1, 1), (1, 1), "bf16"),    # two pieces a patch row
     ],
 )
 def test_conv2d_few_input_channels(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
@@ -842,7 +848,9 @@ def test_conv2d_few_input_channels(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad
     LDS-patch kernel (conv_small.hip): the
     KH input rows of 128 output pixels staged in LDS, K in runs of KW * Cin
     rounded up to 16 with zero filter rows, pixels past the row and channels
-    past Cout not stored."""
+    past Cout not stored; with one channel tile and at least 2048 row chunks
+    the workgroups walk the chunks (filter staged once, the next chunk's
+    patch loads in flight)."""
     rng = np.random.default_rng(21)
     xdt = {"bf16": xt.bfloat16, "f16": xt.float16, "i8": xt.int8}[dt]
     mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xdt, pad=pad, stride=stride, dilation=dil)
