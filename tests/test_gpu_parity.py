@@ -306,7 +306,7 @@ def test_conv2d_band_kernel_shapes(cuda, n, h, w, cin, pad, stride, dil, dt):
         (32, 14, 14, 256, 256, 3, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16"),  # C9's layer: 196 deep tiles, rotated K walks
     ],
 )
-def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
+def test_conv2d_igemm(cuda, monkeypatch, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil, dt):
     """Filters too large for the band kernel's LDS (Cin * Cout * taps * 2
     bytes above ~150 KB) with Cout a multiple of 64 take the implicit-GEMM
     kernel (conv_igemm.hip; 128 x 128 tiles for Cout a multiple of 128, else
@@ -314,7 +314,9 @@ def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil
     128 x 128 tiles would fill at most half the CUs, their DMA issued by
     eight loader waves and, for whole-K tiles, walked from a stage rotated
     per pixel tile): operands by DMA, the input gathered per tap, padding and
-    rows past M read as zeros."""
+    rows past M read as zeros.  XTILE_AMD_CONV_IMAGE=0 keeps the shapes the
+    resident-image kernel would take (C9's layer) on this one."""
+    monkeypatch.setenv("XTILE_AMD_CONV_IMAGE", "0")
     rng = np.random.default_rng(9)
     mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
                    pad=pad, stride=stride, dilation=dil)
@@ -330,6 +332,48 @@ def test_conv2d_igemm(cuda, n, h, w, cin, cout, kh, kw, th, tw, pad, stride, dil
     got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
                   case=f"conv igemm {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s{stride} d{dil} {dt}")[2]
     want = run_oracle(mod, [x, f, o], oracle_threads())[2]
+    assert frob_rel(got, want) <= MM_FROB
+
+
+@pytest.mark.parametrize(
+    "n,h,w,cin,cout,kh,th,tw,pad,stride,dil,dt,force",
+    [
+        (32, 14, 14, 256, 256, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16", ""),    # C9's layer: 256 workgroups, 7 M tiles
+        (2, 14, 14, 256, 256, 3, 7, 14, (1, 1, 1, 1), (1, 1), (1, 1), "bf16", "1"),   # the same image, bf16, 16 workgroups
+        (3, 16, 16, 64, 96, 3, 8, 16, (1, 1, 1, 1), (1, 1), (1, 1), "f16", "1"),      # 256 pixels (8 M tiles), one sub-chunk, Cout 96
+        (2, 15, 15, 128, 64, 3, 8, 8, (1, 1, 1, 1), (2, 2), (1, 1), "f16", "1"),      # stride 2: 64 outputs of a 225-pixel image
+        (2, 9, 9, 192, 32, 3, 5, 5, (0, 0, 0, 0), (1, 1), (2, 2), "bf16", "1"),       # dilation 2, no padding: 25 outputs, one tile
+        (1, 10, 12, 64, 64, 5, 10, 12, (2, 1, 2, 1), (1, 1), (1, 1), "f16", "1"),     # 5 x 3 filter, asymmetric padding
+        (2, 14, 14, 128, 64, 3, 12, 12, (0, 0, 0, 0), (1, 1), (1, 1), "f16", "1"),    # no padding: 144 of 196 pixels
+        (2, 9, 9, 512, 64, 3, 9, 9, (1, 1, 1, 1), (1, 1), (1, 1), "bf16", "1"),       # 8 sub-chunks (133 KB of LDS)
+    ],
+)
+def test_conv2d_resident_image(cuda, monkeypatch, n, h, w, cin, cout, kh, th, tw, pad, stride, dil, dt, force):
+    """Deep layers whose image fits in LDS (Cin a multiple of 64, Cout of 32,
+    a 3-wide filter, at most 256 outputs an image) take the resident-image
+    kernel (conv_image.hip) when its workgroups, one per image and 32 output
+    channels, fill the CUs (C9's layer), or always with
+    XTILE_AMD_CONV_IMAGE=1: the image reaches LDS once in 64-channel
+    sub-chunks, the filter streams through three stage buffers, four MFMA
+    waves split K and add their partial sums through LDS; taps outside the
+    image read a zero block."""
+    if force:
+        monkeypatch.setenv("XTILE_AMD_CONV_IMAGE", force)
+    rng = np.random.default_rng(13)
+    mod = K.conv2d(n, h, w, cin, cout, kh, 3, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
+                   pad=pad, stride=stride, dilation=dil)
+    oh = (h + pad[0] + pad[2] - dil[0] * (kh - 1) - 1) // stride[0] + 1
+    ow = (w + pad[1] + pad[3] - dil[1] * 2 - 1) // stride[1] + 1
+    x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+    f = rng.normal(0, 0.1, (kh, 3, cin, cout)).astype(np.float32)
+    if dt == "bf16":
+        x, f = f32_to_bf16_bits(x), f32_to_bf16_bits(f)
+    else:
+        x, f = x.astype(np.float16), f.astype(np.float16)
+    o = np.full((n, oh, ow, cout), 7.0, np.float32)  # every output is written
+    got = run_gpu(mod, [x, f, o], [dt, dt, "f32"], cuda,
+                  case=f"conv image {n}x{h}x{w}x{cin}->{cout} k{kh}x3 s{stride} d{dil} {dt} force={force}")[2]
+    want = run_oracle(mod, [x, f, np.zeros_like(o)], oracle_threads())[2]
     assert frob_rel(got, want) <= MM_FROB
 
 

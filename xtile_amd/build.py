@@ -38,7 +38,7 @@ CXX = shutil.which("g++") or "g++"
 ARCH = "gfx950"
 
 HOST_SOURCES = ["ir.cpp", "verify.cpp", "passes.cpp", "plan.cpp", "fused.cpp", "staged.cpp", "to_nova.cpp"]
-KERNEL_SOURCES = ["kernels/elementwise.hip", "kernels/gemm.hip", "kernels/conv.hip", "kernels/conv_general.hip", "kernels/conv_igemm.hip", "kernels/conv_small.hip",
+KERNEL_SOURCES = ["kernels/elementwise.hip", "kernels/gemm.hip", "kernels/conv.hip", "kernels/conv_general.hip", "kernels/conv_igemm.hip", "kernels/conv_image.hip", "kernels/conv_small.hip",
                   "kernels/tilevm.hip", "kernels/fused_jit.cpp"]
 HOST_FLAGS = ["-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 # Packed-FP32 instruction forms are disabled for every HIP compile.

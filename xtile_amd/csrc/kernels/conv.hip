@@ -986,7 +986,9 @@ hipError_t launch_conv2d(const xt::Plan& p, void* const* bufs, hipStream_t s, st
   const bool igemm_first = igemm_env && igemm_env[0] == '1';
   if (igemm_first && launch_conv2d_igemm(p, bufs, s, e)) return e;
   if (try_band(p, bufs, s, max_lds, cus, e)) return e;
-  // filters beyond the band kernel's LDS: the implicit GEMM with DMA operands
+  // filters beyond the band kernel's LDS: each image resident in LDS when
+  // its channels fit there, else the implicit GEMM with DMA operands
+  if (launch_conv2d_image(p, bufs, s, e)) return e;
   if (launch_conv2d_igemm(p, bufs, s, e)) return e;
   // Cin below 8 (the RGB stem): input rows staged in LDS, K in runs of KW * Cin
   if (launch_conv2d_small(p, bufs, s, e)) return e;

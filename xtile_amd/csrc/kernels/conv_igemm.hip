@@ -506,15 +506,8 @@ __global__ __launch_bounds__(256) void ig_zero_kernel(float4v* __restrict__ o, l
 
 }  // namespace
 
-bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
+bool conv_blocks_cover_output(const xt::Plan& p, long long es) {
   const xt::ConvPlan& c = p.conv;
-  const bool i8 = c.elem == xt::Elem::I8;
-  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16 && !i8) return false;
-  const long long es = i8 ? 1 : 2;
-  // a K stage is 64 bytes of one tap's channels (the last stage of a tap
-  // padded with zeros), read in 16-byte pieces: Cin * esize and Cout * esize
-  // multiples of 16
-  if (c.out_elem != xt::Elem::F32 || c.TC != c.CO || (c.C * es) % 16 || (c.CO * es) % 16) return false;
   if (c.cb.axis < 0 || c.ch.axis < 0 || c.cw.axis < 0 || c.cb.axis == c.ch.axis || c.cb.axis == c.cw.axis ||
       c.ch.axis == c.cw.axis)
     return false;
@@ -529,7 +522,20 @@ bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
       (gH > 1 && step(c.out_addr, c.ch.axis) != c.TH * c.out_W * c.out_C) ||
       (gW > 1 && step(c.out_addr, c.cw.axis) != c.TW * c.out_C))
     return false;
-  if (c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || (c.filt_addr.c0 * es) % 16) return false;
+  return !(c.filt_addr.sx || c.filt_addr.sy || c.filt_addr.sz || (c.filt_addr.c0 * es) % 16);
+}
+
+bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
+  const xt::ConvPlan& c = p.conv;
+  const bool i8 = c.elem == xt::Elem::I8;
+  if (c.elem != xt::Elem::F16 && c.elem != xt::Elem::BF16 && !i8) return false;
+  const long long es = i8 ? 1 : 2;
+  // a K stage is 64 bytes of one tap's channels (the last stage of a tap
+  // padded with zeros), read in 16-byte pieces: Cin * esize and Cout * esize
+  // multiples of 16
+  if (c.out_elem != xt::Elem::F32 || c.TC != c.CO || (c.C * es) % 16 || (c.CO * es) % 16) return false;
+  if (!conv_blocks_cover_output(p, es)) return false;
+  const long long gB = p.grid[c.cb.axis];
   // the source batch entries the Blocks read: images [0, gB) of an NHWC tensor
   const long long src_bytes = gB * c.TB * c.H * c.W * c.C * es;
   const long long K = c.KH * c.KW * c.C;

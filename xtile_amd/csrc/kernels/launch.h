@@ -67,6 +67,13 @@ hipError_t launch_conv2d_general(const xt::Plan& p, void* const* bufs, hipStream
 // The implicit-GEMM conv kernel (conv_igemm.hip): false, with nothing
 // launched, when the plan is outside what it takes; else `e` is the launch's status.
 bool launch_conv2d_igemm(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e);
+// The resident-image conv kernel (conv_image.hip), same contract.
+bool launch_conv2d_image(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e);
+// Whether a conv plan's Blocks tile images [0, grid[batch axis] * TB) x every
+// output row, column and channel once in the output's natural NHWC
+// addressing, with one filter whose origin is 16-byte aligned (`es` bytes an
+// element); shared by the implicit-GEMM and resident-image kernels.
+bool conv_blocks_cover_output(const xt::Plan& p, long long es);
 // The few-input-channel conv kernel (conv_small.hip), same contract.
 bool launch_conv2d_small(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e);
 hipError_t launch_tilevm(const xt::Plan& p, void* const* bufs, hipStream_t s, std::string& why);
