@@ -339,6 +339,7 @@ def test_conv2d_igemm(cuda, monkeypatch, n, h, w, cin, cout, kh, kw, th, tw, pad
     "n,h,w,cin,cout,kh,th,tw,pad,stride,dil,dt,force",
     [
         (32, 14, 14, 256, 256, 3, 2, 14, (1, 1, 1, 1), (1, 1), (1, 1), "f16", ""),    # C9's layer: 256 workgroups, 7 M tiles
+        (8, 12, 12, 256, 256, 3, 4, 12, (1, 1, 1, 1), (1, 1), (1, 1), "bf16", ""),    # 64 workgroups, 144 outputs: taken unforced
         (2, 14, 14, 256, 256, 3, 7, 14, (1, 1, 1, 1), (1, 1), (1, 1), "bf16", "1"),   # the same image, bf16, 16 workgroups
         (3, 16, 16, 64, 96, 3, 8, 16, (1, 1, 1, 1), (1, 1), (1, 1), "f16", "1"),      # 256 pixels (8 M tiles), one sub-chunk, Cout 96
         (2, 15, 15, 128, 64, 3, 8, 8, (1, 1, 1, 1), (2, 2), (1, 1), "f16", "1"),      # stride 2: 64 outputs of a 225-pixel image
@@ -350,10 +351,10 @@ def test_conv2d_igemm(cuda, monkeypatch, n, h, w, cin, cout, kh, kw, th, tw, pad
 )
 def test_conv2d_resident_image(cuda, monkeypatch, n, h, w, cin, cout, kh, th, tw, pad, stride, dil, dt, force):
     """Deep layers whose image fits in LDS (Cin a multiple of 64, Cout of 32,
-    a 3-wide filter, at most 256 outputs an image) take the resident-image
+    a 3-wide filter, 128 to 256 outputs an image) take the resident-image
     kernel (conv_image.hip) when its workgroups, one per image and 32 output
-    channels, fill the CUs (C9's layer), or always with
-    XTILE_AMD_CONV_IMAGE=1: the image reaches LDS once in 64-channel
+    channels, fill at least a quarter of the CUs (C9's layer), and any such
+    layer with XTILE_AMD_CONV_IMAGE=1: the image reaches LDS once in 64-channel
     sub-chunks, the filter streams through three stage buffers, four MFMA
     waves split K and add their partial sums through LDS; taps outside the
     image read a zero block."""

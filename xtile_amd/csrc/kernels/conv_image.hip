@@ -9,8 +9,9 @@
 // with source elements outside the image read as zero.  Taken when the
 // Blocks tile the whole output (every output channel, one filter), f16 /
 // bf16 sources with Cin a multiple of 64 and Cout a multiple of 32, a 3-wide
-// filter, at most 256 output pixels an image, and the image's channels fit
-// in LDS beside the filter stages.
+// filter, 128 to 256 output pixels an image, the image's channels fit in
+// LDS beside the filter stages, and at least a quarter of the CUs' worth of
+// workgroups (measurements at the launcher).
 //
 //   * One workgroup per (image, 32 output channels): N * Cout / 32
 //     workgroups (32 x 14^2 x 256 -> 256: 256, one a CU).  The image reaches
@@ -291,7 +292,7 @@ hipError_t launch_im(const ImArgs& a, int mt, size_t lds, hipStream_t s) {
 
 bool launch_conv2d_image(const xt::Plan& p, void* const* bufs, hipStream_t s, hipError_t& e) {
   // XTILE_AMD_CONV_IMAGE=0 keeps these shapes on the implicit GEMM; =1 takes
-  // this kernel also when its workgroups do not fill the CUs (tests)
+  // this kernel also for small images and few workgroups (tests)
   const char* env = std::getenv("XTILE_AMD_CONV_IMAGE");
   if (env && env[0] == '0') return false;
   const bool force = env && env[0] == '1';
@@ -312,14 +313,20 @@ bool launch_conv2d_image(const xt::Plan& p, void* const* bufs, hipStream_t s, hi
   const long long mt = (P + 31) / 32;
   const long long lds = std::max(nsub * region + 256 + kImNS * 3 * 4096, 16 * mt * 1024);
   if (lds > kMaxLds) return false;
-  // one workgroup a CU at most (the image and the stages take most of the
-  // LDS): worth it while the workgroups fill the CUs
+  // Taken for images of at least four M tiles (128 outputs) and at least a
+  // quarter of the CUs' worth of workgroups.  Measured (HIP graphs of 100
+  // launches, inputs L2-resident), implicit GEMM / this kernel: 32 x 14^2 x
+  // 256 -> 256 16.2 / 13.0 us, 64 x 14^2 x 256 32.3 / 23.4, 8 x 14^2 x 256
+  // (64 workgroups) 12.6 / 10.7, 32 x 14^2 x 128 -> 128 9.6 / 7.7, 32 x
+  // 12^2 x 256 14.4 / 10.9; but 7 x 7 images (49 outputs: each workgroup
+  // streams its filter columns for few pixels) 32 x 7^2 x 512 -> 512 21.2 /
+  // 22.1, 64 x 7^2 x 512 27.9 / 37.7, 32 x 7^2 x 1024 60.8 / 89.7.
   int cus = 256, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
     cus = 256;
   const long long nwg = images * (c.CO / 32);
-  if ((nwg < cus && !force) || !grid_fits(nwg, 512)) return false;
+  if ((!force && (mt < 4 || nwg * 4 < cus)) || !grid_fits(nwg, 512)) return false;
   const unsigned char* src = static_cast<const unsigned char*>(bufs[c.src_arg]);
   const unsigned char* filt = static_cast<const unsigned char*>(bufs[c.filt_arg]) + c.filt_addr.c0 * 2;
   float* out = static_cast<float*>(bufs[c.out_arg]);
