@@ -455,3 +455,51 @@ def _plans(mod) -> bool:
         return True
     except NotImplementedError:
         return False
+
+
+def image_conv_case(seed: int):
+    """Random `load_conv2d` programs in the resident-image kernel's range
+    (conv_image.hip): f16 / bf16, Blocks tiling the whole output, Cin a
+    multiple of 64 up to 256, Cout a multiple of 32 up to 256, a 3-wide filter
+    of height 1, 3 or 5, strides and dilations of 1 or 2, asymmetric pads, at
+    most 256 outputs an image, and the image's channels (144-byte pixels, 7 a
+    DMA instruction) plus four 12 KB filter stages within 160 KB of LDS.
+    Returns (module, host inputs, dtypes, description)."""
+    import xtile_amd as xt
+    from xtile_amd import kernels as K
+
+    rng = np.random.default_rng(27_000 + seed)
+    for _ in range(500):
+        dt = str(rng.choice(["f16", "bf16"]))
+        n = int(rng.integers(1, 3))
+        kh, kw = int(rng.choice([1, 3, 5])), 3
+        sh, sw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        dh, dw = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        pad = tuple(int(rng.integers(0, k // 2 + 1)) for k in (kh, kw, kh, kw))
+        h, w = int(rng.integers(5, 17)), int(rng.integers(5, 17))
+        cin, cout = 64 * int(rng.integers(1, 5)), 32 * int(rng.integers(1, 9))
+        oh = (h + pad[0] + pad[2] - dh * (kh - 1) - 1) // sh + 1
+        ow = (w + pad[1] + pad[3] - dw * (kw - 1) - 1) // sw + 1
+        if oh < 1 or ow < 1 or oh * ow > 256:
+            continue
+        mt = (oh * ow + 31) // 32
+        region = (h * w + 6) // 7 * 1008 + 16
+        if max(cin // 64 * region + 256 + 4 * 12288, 16 * mt * 1024) > 160 * 1024:
+            continue
+        th = int(rng.choice([d for d in range(1, oh + 1) if oh % d == 0]))
+        tw = int(rng.choice([d for d in range(1, ow + 1) if ow % d == 0]))
+        try:
+            mod = K.conv2d(n, h, w, cin, cout, kh, kw, th, tw, dtype=xt.bfloat16 if dt == "bf16" else xt.float16,
+                           pad=pad, stride=(sh, sw), dilation=(dh, dw))
+            xt.plan(mod)
+        except (ValueError, NotImplementedError):
+            continue
+        x = rng.normal(0, 0.1, (n, h, w, cin)).astype(np.float32)
+        f = rng.normal(0, 0.1, (kh, kw, cin, cout)).astype(np.float32)
+        x, f = (f32_to_bf16_bits(x), f32_to_bf16_bits(f)) if dt == "bf16" else (x.astype(np.float16),
+                                                                                 f.astype(np.float16))
+        o = np.full((n, oh, ow, cout), 7.0, np.float32)
+        desc = (f"{dt} {n}x{h}x{w}x{cin}->{cout} k{kh}x{kw} s({sh},{sw}) d({dh},{dw}) pad{pad} "
+                f"tile {th}x{tw}")
+        return mod, [x, f, o], [dt, dt, "f32"], desc
+    raise RuntimeError(f"no resident-image conv case for seed {seed}")

@@ -14,7 +14,7 @@ import pytest
 
 import xtile_amd as xt
 from tests.gpu_util import frob_rel, run_gpu, run_oracle
-from tests.random_programs import conv_case, wide_conv_case
+from tests.random_programs import conv_case, image_conv_case, wide_conv_case
 
 pytestmark = pytest.mark.gpu
 
@@ -42,3 +42,17 @@ def test_random_wide_conv_matches_the_oracle(cuda, seed):
         assert np.array_equal(got, want)
     else:
         assert frob_rel(got, want) <= 1e-3
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_resident_image_conv_matches_the_oracle(cuda, monkeypatch, seed):
+    """Shapes in the resident-image kernel's range (tests/random_programs.py:
+    image_conv_case), forced onto it with XTILE_AMD_CONV_IMAGE=1 whatever
+    the image size and workgroup count: 1 x 3 to 5 x 3 filters, strides,
+    dilations, asymmetric pads, 64 to 256 input and 32 to 256 output
+    channels; every output is overwritten (the buffer starts at 7)."""
+    monkeypatch.setenv("XTILE_AMD_CONV_IMAGE", "1")
+    mod, host, dtypes, desc = image_conv_case(seed)
+    got = run_gpu(mod, host, dtypes, cuda, case=f"random image conv {seed}: {desc}")[2]
+    want = run_oracle(mod, [host[0], host[1], np.zeros_like(host[2])], 8)[2]
+    assert frob_rel(got, want) <= 1e-3
